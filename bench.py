@@ -1,0 +1,244 @@
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+Workload: one 27B-class dense decoder layer's linears -- hidden 5120, q
+[6144, 5120], k and v [1024, 5120], o [5120, 6144], gate and up
+[17408, 5120], down [5120, 17408]; 340,787,200 weights per layer.  Weights
+are N(0, 0.02), quantized on the GPU by the library's own quantizers;
+activations are bf16 N(0, 1).
+
+A step is one decode pass (M = 1) over the layer's seven linears in W8A16
+(int8 per row + bf16 scale).  Layer copies rotate so the weight working set
+(COPIES x 341 MB) exceeds the 256 MB Infinity Cache and the figure measures
+HBM.  `value` = algorithmic weight bytes streamed / wall time of the timed
+steps, in GB/s.  Extra keys report the same decode for Q4_K / FP8-128 /
+MXFP4, the prefill GEMM TFLOP/s (W8A16 and Q4_K at M = 2048, FP8-128 and
+MXFP4 native at M = 1024), the roofline of the dominant kernel and the CPU
+baseline.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dial-27b_amd"))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "fp4": 10100.0}
+LAYER_27B = [("q", 6144, 5120), ("k", 1024, 5120), ("v", 1024, 5120), ("o", 5120, 6144),
+             ("gate", 17408, 5120), ("up", 17408, 5120), ("down", 5120, 17408)]
+METRIC = "quant GEMV weight GB/s (% HBM peak) + prefill GEMM TFLOP/s, 27B shapes, 1 GPU"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--copies", type=int, default=3, help="layer copies rotated per step")
+    ap.add_argument("--prefill-iters", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--sweep", default="w8a16,q4_k,fp8_block,mxfp4",
+                    help="formats for the extra decode / prefill numbers ('' = none)")
+    return ap.parse_args()
+
+
+def build_layers(dq, torch, fmt, copies, dev, seed=0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    layers = []
+    for _ in range(copies):
+        lins = []
+        for name, n, k in LAYER_27B:
+            w = torch.randn(n, k, device=dev, generator=g, dtype=torch.float32) * 0.02
+            lins.append(dq.Linear.quantize(fmt, w, scale_dtype=dq.BF16))
+            del w
+        layers.append(lins)
+    torch.cuda.synchronize()
+    return layers
+
+
+def layer_bytes(dq, fmt):
+    return sum(dq.raw_weight_bytes(fmt, n, k) for _, n, k in LAYER_27B)
+
+
+def decode_pass(dq, lins, xs, ys, stream):
+    for lin, x, y in zip(lins, xs, ys):
+        lin.forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+
+
+def time_decode(dq, torch, layers, steps, warmup, dev):
+    """Wall time of `steps` decode passes (rotating layer copies)."""
+    stream = torch.cuda.current_stream()
+    xs = [torch.randn(1, k, device=dev).to(torch.bfloat16) for _, n, k in LAYER_27B]
+    ys = [torch.empty(1, n, device=dev, dtype=torch.bfloat16) for _, n, k in LAYER_27B]
+    for i in range(warmup):
+        decode_pass(dq, layers[i % len(layers)], xs, ys, stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        decode_pass(dq, layers[i % len(layers)], xs, ys, stream)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def time_per_linear(dq, torch, layers, dev, reps=60):
+    """Average device time of each linear's GEMV launch (HIP events on the
+    stream the kernels are launched on)."""
+    stream = torch.cuda.current_stream()
+    out = {}
+    for li, (name, n, k) in enumerate(LAYER_27B):
+        x = torch.randn(1, k, device=dev).to(torch.bfloat16)
+        y = torch.empty(1, n, device=dev, dtype=torch.bfloat16)
+        for i in range(5):
+            layers[i % len(layers)][li].forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            layers[i % len(layers)][li].forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+        e1.record(stream)
+        e1.synchronize()
+        out[name] = e0.elapsed_time(e1) / reps * 1e-3  # seconds per launch
+    return out
+
+
+def time_prefill(dq, torch, lins, m, iters, dev, path):
+    stream = torch.cuda.current_stream()
+    xs = [torch.randn(m, k, device=dev).to(torch.bfloat16) for _, n, k in LAYER_27B]
+    ys = [torch.empty(m, n, device=dev, dtype=torch.bfloat16) for _, n, k in LAYER_27B]
+    for lin, x, y in zip(lins, xs, ys):
+        lin.forward(x, y, path=path, stream=stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(iters):
+        for lin, x, y in zip(lins, xs, ys):
+            lin.forward(x, y, path=path, stream=stream)
+    e1.record(stream)
+    e1.synchronize()
+    secs = e0.elapsed_time(e1) * 1e-3 / iters
+    flops = 2.0 * m * sum(n * k for _, n, k in LAYER_27B)
+    return flops / secs / 1e12, secs
+
+
+def cpu_baseline(seconds):
+    """The oracle's multi-threaded CPU GEMV (oracle/cpu_baseline.c) on this
+    host, W8A16 at the gate shape [17408, 5120], M = 1, repeated for a
+    bounded time."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # the checker library; timed here as the CPU baseline
+    threads = max(1, min(16, os.cpu_count() or 1))
+    n, k = 17408, 5120
+    rng = np.random.default_rng(0)
+    q = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    s = np.full(n, 0x3c00, np.uint16)
+    x = (rng.normal(size=(1, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    O.cpu_w8a16_gemv(x, q, s, threads)
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        O.cpu_w8a16_gemv(x, q, s, threads)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    gbs = (n * k + 2 * n) / dt / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"W8A16 decode GEMV [17408x5120] M=1 (the layer's gate linear), {reps} reps, "
+                      f"{threads} OpenMP threads, dequantize-on-the-fly f32 dot per row"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported (this build "
+              "has no multi-GPU path)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import dialq as dq
+
+    dev = torch.device("cuda:0")
+    fmt_of = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}
+
+    # ---- headline: W8A16 decode over the 27B layer -----------------------
+    layers = build_layers(dq, torch, dq.W8A16, a.copies, dev)
+    secs = time_decode(dq, torch, layers, a.steps, a.warmup, dev)
+    lbytes = layer_bytes(dq, dq.W8A16)
+    value = lbytes * a.steps / secs / 1e9
+    per = time_per_linear(dq, torch, layers, dev)
+    # dominant kernel: the GEMV launch with the largest device time per layer
+    dom = max(per, key=per.get)
+    dn, dk = [(n, k) for name, n, k in LAYER_27B if name == dom][0]
+    dbytes = dq.raw_weight_bytes(dq.W8A16, dn, dk)
+    achieved = dbytes / per[dom] / 1e9
+    print(f"# w8a16 decode: {value:.1f} GB/s over the layer; per-launch us: "
+          + ", ".join(f"{k}={v * 1e6:.1f}" for k, v in per.items()), file=sys.stderr, flush=True)
+
+    extra = {"decode_gbs": {"w8a16": round(value, 1)}, "decode_us_per_launch_w8a16":
+             {k: round(v * 1e6, 2) for k, v in per.items()}, "prefill_tflops": {}}
+    sweep = [s for s in a.sweep.split(",") if s]
+    if "w8a16" in sweep:
+        tf, s2 = time_prefill(dq, torch, layers[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
+        extra["prefill_tflops"]["w8a16_m2048"] = round(tf, 1)
+        print(f"# w8a16 prefill M=2048: {tf:.1f} TFLOP/s ({s2 * 1e3:.2f} ms/layer)", file=sys.stderr, flush=True)
+    del layers
+    torch.cuda.empty_cache()
+    for name in sweep:
+        if name == "w8a16":
+            continue
+        fmt = fmt_of[name]
+        ls = build_layers(dq, torch, fmt, a.copies if fmt != dq.MXFP4 and fmt != dq.Q4_K else a.copies + 2, dev)
+        sd = time_decode(dq, torch, ls, max(a.steps // 3, 10), 10, dev)
+        gbs = layer_bytes(dq, fmt) * max(a.steps // 3, 10) / sd / 1e9
+        extra["decode_gbs"][name] = round(gbs, 1)
+        if fmt in (dq.FP8_BLOCK, dq.MXFP4):
+            tf, s2 = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE)
+            extra["prefill_tflops"][name + "_native_m1024"] = round(tf, 1)
+        else:
+            tf, s2 = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
+            extra["prefill_tflops"][name + "_m2048"] = round(tf, 1)
+        print(f"# {name}: decode {gbs:.1f} GB/s, prefill {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)
+        del ls
+        torch.cuda.empty_cache()
+
+    cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(secs / a.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "27B-class dense layer linears (hidden 5120; q 6144x5120, k/v 1024x5120, "
+                        "o 5120x6144, gate/up 17408x5120, down 5120x17408), W8A16 decode GEMV, M=1",
+            "weights_per_layer": sum(n * k for _, n, k in LAYER_27B),
+            "weight_bytes_per_step": lbytes,
+            "layer_copies_rotated": a.copies,
+            "rows": 1,
+            "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"k_gemv<W8A16> ({dom} {dn}x{dk}, M=1)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        **extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,588 @@
+// C ABI of the dialq library (include/dialq.h): handle lifetime, argument
+// validation with the reference's error messages, buffer staging for host
+// pointers, and kernel dispatch.  Nothing here throws across the ABI; every
+// failure returns -1 / NULL with a NUL-terminated message.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/dialq.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace {
+
+using namespace dialq;
+
+struct Error : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+[[noreturn]] void fail(const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  throw Error(buf);
+}
+
+void hip_check(hipError_t e, const char *what) {
+  if (e != hipSuccess) fail("%s failed: %s", what, hipGetErrorString(e));
+}
+
+void write_error(char *error, size_t error_size, const char *msg) {
+  if (error && error_size > 0) {
+    snprintf(error, error_size, "%s", msg);
+  }
+}
+
+// Device memory owned by a handle or a call.
+struct DevBuf {
+  void *p = nullptr;
+  size_t n = 0;
+  DevBuf() = default;
+  explicit DevBuf(size_t bytes) { alloc(bytes); }
+  void alloc(size_t bytes) {
+    release();
+    if (bytes) hip_check(hipMalloc(&p, bytes), "hipMalloc");
+    n = bytes;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+  ~DevBuf() { release(); }
+  DevBuf(const DevBuf &) = delete;
+  DevBuf &operator=(const DevBuf &) = delete;
+};
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    hip_check(hipGetDevice(&prev), "hipGetDevice");
+    if (prev != dev) hip_check(hipSetDevice(dev), "hipSetDevice");
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && prev >= 0 && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+struct Linear {
+  dialq_linear_desc desc{};
+  int device = 0;
+  int64_t n_strips = 0, k_chunks = 0, nbk = 0;
+  DevBuf tiles, aux, row_scale, block_scale;
+  DevBuf scratch;  // activation codes for native prefill / local q8
+  std::mutex scratch_mu;
+  float global = 1.0f;
+
+  WeightView view() const {
+    WeightView w;
+    w.fmt = desc.format;
+    w.N = desc.out_dim;
+    w.K = desc.in_dim;
+    w.n_strips = n_strips;
+    w.k_chunks = k_chunks;
+    w.nbk = nbk;
+    w.tiles = (const uint8_t *)tiles.p;
+    w.aux = (const uint8_t *)aux.p;
+    w.row_scale = (const float *)row_scale.p;
+    w.block_scale = (const float *)block_scale.p;
+    w.global = global;
+    return w;
+  }
+};
+
+const char *format_name(int fmt) {
+  switch (fmt) {
+    case DIALQ_FORMAT_W8A16: return "W8A16";
+    case DIALQ_FORMAT_Q8_0: return "Q8_0";
+    case DIALQ_FORMAT_Q4_K: return "Q4_K";
+    case DIALQ_FORMAT_FP8_ROW: return "FP8";
+    case DIALQ_FORMAT_FP8_BLOCK: return "FP8 block";
+    case DIALQ_FORMAT_NVFP4: return "NVFP4";
+    case DIALQ_FORMAT_MXFP4: return "MXFP4";
+  }
+  return "unknown";
+}
+
+size_t dtype_size(int dt) {
+  switch (dt) {
+    case DIALQ_F32: return 4;
+    case DIALQ_F16:
+    case DIALQ_BF16: return 2;
+  }
+  fail("unsupported dtype %d (expected 0=f32, 1=f16, 2=bf16)", dt);
+}
+
+// Raw byte sizes of a format's weight and scale buffers.
+void raw_sizes(const dialq_linear_desc &d, size_t &wbytes, size_t &sbytes, size_t &scount) {
+  const int64_t N = d.out_dim, K = d.in_dim;
+  switch (d.format) {
+    case DIALQ_FORMAT_W8A16:
+      wbytes = (size_t)(N * K);
+      scount = (size_t)N;
+      sbytes = scount * (d.scale_dtype == DIALQ_BF16 ? 2 : 4);
+      return;
+    case DIALQ_FORMAT_Q8_0:
+      wbytes = (size_t)(N * (K / 32) * 34);
+      sbytes = scount = 0;
+      return;
+    case DIALQ_FORMAT_Q4_K:
+      wbytes = (size_t)(N * (K / 256) * 144);
+      sbytes = scount = 0;
+      return;
+    case DIALQ_FORMAT_FP8_ROW:
+      wbytes = (size_t)(N * K);
+      scount = (size_t)N;
+      sbytes = scount * 4;
+      return;
+    case DIALQ_FORMAT_FP8_BLOCK:
+      wbytes = (size_t)(N * K);
+      scount = (size_t)(((N + 127) / 128) * ((K + 127) / 128));
+      sbytes = scount * 4;
+      return;
+    case DIALQ_FORMAT_NVFP4:
+      wbytes = (size_t)(N * K / 2);
+      scount = (size_t)(N * K / 16);
+      sbytes = scount;
+      return;
+    case DIALQ_FORMAT_MXFP4:
+      wbytes = (size_t)(N * K / 2);
+      scount = (size_t)(N * K / 32);
+      sbytes = scount;
+      return;
+  }
+  fail("unknown weight format %d", d.format);
+}
+
+void validate_desc(const dialq_linear_desc *d) {
+  if (!d) fail("desc is NULL");
+  if (d->out_dim <= 0 || d->in_dim <= 0)
+    fail("invalid %s shape [%lld, %lld]", format_name(d->format), (long long)d->out_dim,
+         (long long)d->in_dim);
+  FormatGeom fg = format_geom(d->format);
+  if (fg.chunk == 0) fail("unknown weight format %d", d->format);
+  // Messages follow CudaQuantLinear::nvfp4 (cuda_quant.rs:301-303) and
+  // decode_nvfp4_values (quant.rs:167-171).
+  if (d->format == DIALQ_FORMAT_NVFP4 && d->in_dim % 16 != 0)
+    fail("NVFP4 QuantLinear input dimension %lld is not divisible by 16", (long long)d->in_dim);
+  if (d->in_dim % fg.k_align != 0)
+    fail("%s input dimension %lld is not divisible by %d", format_name(d->format),
+         (long long)d->in_dim, fg.k_align);
+  if (d->format == DIALQ_FORMAT_W8A16 && d->scale_dtype != DIALQ_F32 && d->scale_dtype != DIALQ_BF16)
+    fail("W8A16 scale dtype must be f32 or bf16, got %d", d->scale_dtype);
+  if (d->format == DIALQ_FORMAT_NVFP4) {
+    float gs = d->global_scale;
+    if (!(gs == gs) || gs == 0.0f)
+      fail("NVFP4 global scale must contain one non-zero value, got %g", (double)gs);
+  }
+}
+
+Linear *alloc_linear(const dialq_linear_desc &d, int device) {
+  Linear *L = new Linear();
+  L->desc = d;
+  L->device = device;
+  FormatGeom fg = format_geom(d.format);
+  L->n_strips = (d.out_dim + 15) / 16;
+  L->k_chunks = (d.in_dim + fg.chunk - 1) / fg.chunk;
+  L->nbk = (d.in_dim + 127) / 128;
+  L->tiles.alloc((size_t)(L->n_strips * L->k_chunks * fg.tile_bytes));
+  if (fg.aux_bytes) L->aux.alloc((size_t)(L->n_strips * L->k_chunks * fg.aux_bytes));
+  if (d.format == DIALQ_FORMAT_W8A16 || d.format == DIALQ_FORMAT_FP8_ROW)
+    L->row_scale.alloc((size_t)(L->n_strips * 16) * sizeof(float));
+  if (d.format == DIALQ_FORMAT_FP8_BLOCK)
+    L->block_scale.alloc((size_t)(((d.out_dim + 127) / 128) * L->nbk) * sizeof(float));
+  if (d.format == DIALQ_FORMAT_NVFP4) {
+    L->global = (d.flags & DIALQ_FLAG_GLOBAL_IS_DIVISOR) ? 1.0f / d.global_scale : d.global_scale;
+  }
+  return L;
+}
+
+// Copy `bytes` from a host or device source into a fresh device buffer.
+void stage_in(DevBuf &dst, const void *src, size_t bytes, bool host, hipStream_t st) {
+  dst.alloc(bytes);
+  if (bytes)
+    hip_check(hipMemcpyAsync(dst.p, src, bytes, host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice, st),
+              "hipMemcpyAsync");
+}
+
+template <typename F>
+int guarded(char *error, size_t error_size, F &&f) {
+  try {
+    f();
+    if (error && error_size) error[0] = '\0';
+    return 0;
+  } catch (const std::exception &e) {
+    write_error(error, error_size, e.what());
+  } catch (...) {
+    write_error(error, error_size, "unknown error");
+  }
+  return -1;
+}
+
+void ensure_scratch(Linear *L, size_t bytes) {
+  if (L->scratch.n < bytes) L->scratch.alloc(bytes);
+}
+
+void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, int y_dtype, int path,
+                 hipStream_t st) {
+  WeightView w = L->view();
+  const int fmt = L->desc.format;
+  if (path == DIALQ_PATH_AUTO) {
+    if (rows <= 64) path = DIALQ_PATH_GEMV;
+    else if ((fmt == DIALQ_FORMAT_FP8_BLOCK || fmt == DIALQ_FORMAT_MXFP4) &&
+             !(L->desc.flags & DIALQ_FLAG_WEIGHT_ONLY_PREFILL))
+      path = DIALQ_PATH_GEMM_NATIVE;
+    else path = DIALQ_PATH_GEMM;
+  }
+  if (path == DIALQ_PATH_GEMV) {
+    hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, st), "GEMV launch");
+  } else if (path == DIALQ_PATH_GEMM) {
+    hip_check(launch_gemm(w, x, x_dtype, rows, y, y_dtype, st), "GEMM launch");
+  } else if (path == DIALQ_PATH_GEMM_NATIVE) {
+    if (fmt != DIALQ_FORMAT_FP8_BLOCK && fmt != DIALQ_FORMAT_MXFP4)
+      fail("native fp8/fp4 prefill needs an FP8 block or MXFP4 weight, got %s", format_name(fmt));
+    const int64_t k_pad = w.k_chunks * 128;
+    std::lock_guard<std::mutex> lock(L->scratch_mu);
+    if (fmt == DIALQ_FORMAT_FP8_BLOCK) {
+      size_t codes = (size_t)(rows * k_pad), off = (codes + 255) / 256 * 256;
+      ensure_scratch(L, off + (size_t)rows * sizeof(float));
+      uint8_t *xq = (uint8_t *)L->scratch.p;
+      float *xs = (float *)((uint8_t *)L->scratch.p + off);
+      hip_check(launch_act_fp8(x, x_dtype, rows, w.K, k_pad, xq, xs, st), "activation quantizer");
+      hip_check(launch_gemm_native(w, xq, xs, rows, k_pad, y, y_dtype, st), "native GEMM launch");
+    } else {
+      size_t codes = (size_t)(rows * k_pad / 2), off = (codes + 255) / 256 * 256;
+      ensure_scratch(L, off + (size_t)(rows * k_pad / 32));
+      uint8_t *xq = (uint8_t *)L->scratch.p;
+      uint8_t *xs = (uint8_t *)L->scratch.p + off;
+      hip_check(launch_act_mxfp4(x, x_dtype, rows, w.K, k_pad, xq, xs, st), "activation quantizer");
+      hip_check(launch_gemm_native(w, xq, xs, rows, k_pad, y, y_dtype, st), "native GEMM launch");
+    }
+  } else {
+    fail("unknown path %d", path);
+  }
+}
+
+void check_ptr_align(const void *p, const char *what) {
+  if (((uintptr_t)p) & 15u) fail("%s must be 16-byte aligned", what);
+}
+
+void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void *y, int32_t y_dtype,
+                  int32_t path, void *stream, int device_io, bool local_q8) {
+  if (!L) fail("linear handle is NULL");
+  if (rows < 0) fail("rows must be >= 0, got %lld", (long long)rows);
+  size_t xs = dtype_size(x_dtype), ys = dtype_size(y_dtype);
+  if (rows == 0) return;
+  if (!x || !y) fail("x and y must not be NULL");
+  DeviceGuard dg(L->device);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t N = L->desc.out_dim, K = L->desc.in_dim;
+  size_t xbytes = (size_t)(rows * K) * xs, ybytes = (size_t)(rows * N) * ys;
+  DevBuf dx, dy;
+  const void *xp = x;
+  void *yp = y;
+  if (!device_io) {
+    stage_in(dx, x, xbytes, true, st);
+    dy.alloc(ybytes);
+    xp = dx.p;
+    yp = dy.p;
+  } else {
+    check_ptr_align(x, "x");
+  }
+  if (local_q8) {
+    if (L->desc.format != DIALQ_FORMAT_W8A16 || L->desc.scale_dtype != DIALQ_F32)
+      fail("local q8 linear needs a W8A16 weight with f32 scales");
+    if (rows != 1) fail("local q8 linear expects decode [1, 1, %lld], got %lld rows", (long long)K, (long long)rows);
+    std::lock_guard<std::mutex> lock(L->scratch_mu);
+    int64_t k_pad = L->k_chunks * 64;
+    ensure_scratch(L, (size_t)((k_pad + 255) / 256 * 256 + 256));
+    hip_check(launch_local_q8(L->view(), xp, x_dtype, yp, y_dtype, L->scratch.p, st), "local q8 launch");
+  } else {
+    run_forward(L, xp, x_dtype, rows, yp, y_dtype, path, st);
+  }
+  if (!device_io) {
+    hip_check(hipMemcpyAsync(y, yp, ybytes, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+    hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t dialq_abi_version(void) { return DIALQ_ABI_VERSION; }
+
+void *dialq_linear_create(const dialq_linear_desc *desc, const void *weight, size_t weight_bytes,
+                          const void *scales, size_t scale_bytes, int device, int host_io,
+                          void *stream, char *error, size_t error_size) {
+  Linear *out = nullptr;
+  guarded(error, error_size, [&] {
+    validate_desc(desc);
+    const dialq_linear_desc &d = *desc;
+    size_t wexp, sexp, scount;
+    raw_sizes(d, wexp, sexp, scount);
+    // Length checks and messages of CudaQuantLinear::nvfp4 / ::fp8
+    // (cuda_quant.rs:304-309, 339-344).
+    if (d.format == DIALQ_FORMAT_NVFP4) {
+      if (weight_bytes != wexp) fail("invalid NVFP4 packed weight length %zu", weight_bytes);
+      if (scale_bytes != sexp) fail("invalid NVFP4 scale length %zu", scale_bytes);
+    } else if (d.format == DIALQ_FORMAT_FP8_ROW) {
+      if (weight_bytes != wexp) fail("invalid FP8 weight length %zu", weight_bytes);
+      if (scale_bytes != sexp && scale_bytes != 4) fail("invalid FP8 scale length %zu", scale_bytes / 4);
+      scount = scale_bytes / 4;
+    } else {
+      if (weight_bytes != wexp)
+        fail("invalid %s weight length %zu, expected %zu", format_name(d.format), weight_bytes, wexp);
+      if (scale_bytes != sexp)
+        fail("invalid %s scale length %zu, expected %zu", format_name(d.format), scale_bytes, sexp);
+    }
+    if (!weight || (sexp && !scales)) fail("weight/scales must not be NULL");
+    DeviceGuard dg(device);
+    hipStream_t st = (hipStream_t)stream;
+    Linear *L = alloc_linear(d, device);
+    try {
+      DevBuf rw, rs;
+      stage_in(rw, weight, weight_bytes, host_io != 0, st);
+      if (scale_bytes) stage_in(rs, scales, scale_bytes, host_io != 0, st);
+      hip_check(launch_repack(d.format, d.out_dim, d.in_dim, rw.p, rs.p, d.scale_dtype == DIALQ_BF16,
+                              (int64_t)scount, (uint8_t *)L->tiles.p, (uint8_t *)L->aux.p,
+                              (float *)L->row_scale.p, (float *)L->block_scale.p, st),
+                "repack");
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+    } catch (...) {
+      delete L;
+      throw;
+    }
+    out = L;
+  });
+  return out;
+}
+
+void *dialq_linear_quantize(const dialq_linear_desc *desc, const void *dense, int32_t dense_dtype,
+                            int device, int host_io, void *stream, char *error, size_t error_size) {
+  Linear *out = nullptr;
+  guarded(error, error_size, [&] {
+    validate_desc(desc);
+    const dialq_linear_desc &d = *desc;
+    if (d.format == DIALQ_FORMAT_FP8_ROW || d.format == DIALQ_FORMAT_NVFP4)
+      fail("%s weights come pre-quantized from the checkpoint; use dialq_linear_create", format_name(d.format));
+    if (!dense) fail("dense weight must not be NULL");
+    size_t es = dtype_size(dense_dtype);
+    size_t wexp, sexp, scount;
+    raw_sizes(d, wexp, sexp, scount);
+    DeviceGuard dg(device);
+    hipStream_t st = (hipStream_t)stream;
+    Linear *L = alloc_linear(d, device);
+    try {
+      DevBuf dd, rw, rs;
+      const void *src = dense;
+      if (host_io) {
+        stage_in(dd, dense, (size_t)(d.out_dim * d.in_dim) * es, true, st);
+        src = dd.p;
+      }
+      rw.alloc(wexp);
+      // the quantizer always writes f32 row scales; bf16 storage rounds them
+      DevBuf rs32;
+      if (d.format == DIALQ_FORMAT_W8A16) rs32.alloc((size_t)d.out_dim * 4);
+      else if (sexp) rs.alloc(sexp);
+      hip_check(launch_quantize(d.format, src, dense_dtype, d.out_dim, d.in_dim, rw.p,
+                                d.format == DIALQ_FORMAT_W8A16 ? rs32.p : rs.p, st),
+                "quantize");
+      const void *scale_src = d.format == DIALQ_FORMAT_W8A16 ? rs32.p : rs.p;
+      if (d.format == DIALQ_FORMAT_W8A16 && d.scale_dtype == DIALQ_BF16) {
+        // round the f32 row scales to bf16 storage (RNE); q stays as computed
+        // against the f32 scale
+        std::vector<float> hs((size_t)d.out_dim);
+        hip_check(hipMemcpyAsync(hs.data(), rs32.p, hs.size() * 4, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+        hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+        std::vector<uint16_t> hb(hs.size());
+        for (size_t i = 0; i < hs.size(); ++i) {
+          uint32_t u;
+          memcpy(&u, &hs[i], 4);
+          if ((u & 0x7fffffffu) > 0x7f800000u) hb[i] = (uint16_t)((u >> 16) | 0x40u);
+          else hb[i] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+        }
+        rs.alloc(hb.size() * 2);
+        hip_check(hipMemcpyAsync(rs.p, hb.data(), hb.size() * 2, hipMemcpyHostToDevice, st), "hipMemcpyAsync");
+        scale_src = rs.p;
+        hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+      }
+      hip_check(launch_repack(d.format, d.out_dim, d.in_dim, rw.p, scale_src, d.scale_dtype == DIALQ_BF16,
+                              (int64_t)scount, (uint8_t *)L->tiles.p, (uint8_t *)L->aux.p,
+                              (float *)L->row_scale.p, (float *)L->block_scale.p, st),
+                "repack");
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+    } catch (...) {
+      delete L;
+      throw;
+    }
+    out = L;
+  });
+  return out;
+}
+
+void dialq_linear_destroy(void *linear) {
+  Linear *L = (Linear *)linear;
+  if (!L) return;
+  int prev = -1;
+  (void)hipGetDevice(&prev);
+  (void)hipSetDevice(L->device);
+  delete L;
+  if (prev >= 0) (void)hipSetDevice(prev);
+}
+
+uint64_t dialq_linear_resident_bytes(const void *linear) {
+  const Linear *L = (const Linear *)linear;
+  if (!L) return 0;
+  const dialq_linear_desc &d = L->desc;
+  const uint64_t N = (uint64_t)d.out_dim, K = (uint64_t)d.in_dim;
+  switch (d.format) {
+    case DIALQ_FORMAT_NVFP4: return N * K / 2 + N * K / 16 + 4;
+    case DIALQ_FORMAT_FP8_ROW: return N * K + N * 4;
+    case DIALQ_FORMAT_W8A16: return N * K + N * (d.scale_dtype == DIALQ_BF16 ? 2 : 4);
+    case DIALQ_FORMAT_Q8_0: return N * (K / 32) * 34;
+    case DIALQ_FORMAT_Q4_K: return N * (K / 256) * 144;
+    case DIALQ_FORMAT_FP8_BLOCK: return N * K + 4 * ((N + 127) / 128) * ((K + 127) / 128);
+    case DIALQ_FORMAT_MXFP4: return N * K / 2 + N * K / 32;
+  }
+  return 0;
+}
+
+uint64_t dialq_linear_device_bytes(const void *linear) {
+  const Linear *L = (const Linear *)linear;
+  if (!L) return 0;
+  return L->tiles.n + L->aux.n + L->row_scale.n + L->block_scale.n + L->scratch.n;
+}
+
+int dialq_linear_describe(const void *linear, dialq_linear_desc *desc) {
+  const Linear *L = (const Linear *)linear;
+  if (!L || !desc) return -1;
+  *desc = L->desc;
+  return 0;
+}
+
+int dialq_linear_forward(void *linear, const void *x, int32_t x_dtype, int64_t rows, void *y,
+                         int32_t y_dtype, void *stream, int device_io, char *error, size_t error_size) {
+  return guarded(error, error_size, [&] {
+    forward_impl((Linear *)linear, x, x_dtype, rows, y, y_dtype, DIALQ_PATH_AUTO, stream, device_io, false);
+  });
+}
+
+int dialq_linear_forward_ex(void *linear, const void *x, int32_t x_dtype, int64_t rows, void *y,
+                            int32_t y_dtype, int32_t path, void *stream, int device_io, char *error,
+                            size_t error_size) {
+  return guarded(error, error_size, [&] {
+    forward_impl((Linear *)linear, x, x_dtype, rows, y, y_dtype, path, stream, device_io, false);
+  });
+}
+
+int dialq_local_q8_forward(void *linear, const void *x, int32_t x_dtype, int64_t rows, void *y,
+                           int32_t y_dtype, void *stream, int device_io, char *error,
+                           size_t error_size) {
+  return guarded(error, error_size, [&] {
+    forward_impl((Linear *)linear, x, x_dtype, rows, y, y_dtype, DIALQ_PATH_AUTO, stream, device_io, true);
+  });
+}
+
+int dialq_linear_dequantize(const void *linear, void *out, int32_t out_dtype, void *stream,
+                            int device_io, char *error, size_t error_size) {
+  return guarded(error, error_size, [&] {
+    const Linear *L = (const Linear *)linear;
+    if (!L) fail("linear handle is NULL");
+    if (!out) fail("out must not be NULL");
+    size_t es = dtype_size(out_dtype);
+    DeviceGuard dg(L->device);
+    hipStream_t st = (hipStream_t)stream;
+    const dialq_linear_desc &d = L->desc;
+    size_t bytes = (size_t)(d.out_dim * d.in_dim) * es;
+    DevBuf tmp;
+    void *dst = out;
+    if (!device_io) {
+      tmp.alloc(bytes);
+      dst = tmp.p;
+    }
+    FormatGeom fg = format_geom(d.format);
+    DequantArgs a;
+    a.fmt = d.format;
+    a.N = d.out_dim;
+    a.K = d.in_dim;
+    a.k_chunks = L->k_chunks;
+    a.nbk = L->nbk;
+    a.chunk = fg.chunk;
+    a.tile_bytes = fg.tile_bytes;
+    a.tiles = (const uint8_t *)L->tiles.p;
+    a.aux = (const uint8_t *)L->aux.p;
+    a.row_scale = (const float *)L->row_scale.p;
+    a.block_scale = (const float *)L->block_scale.p;
+    a.global = L->global;
+    a.out = dst;
+    a.out_dtype = out_dtype;
+    hip_check(launch_dequant(a, st), "dequantize launch");
+    if (!device_io) {
+      hip_check(hipMemcpyAsync(out, dst, bytes, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+    }
+  });
+}
+
+int dialq_linear_export(const void *linear, void *weight, size_t weight_bytes, void *scales,
+                        size_t scale_bytes, char *error, size_t error_size) {
+  return guarded(error, error_size, [&] {
+    const Linear *L = (const Linear *)linear;
+    if (!L) fail("linear handle is NULL");
+    const dialq_linear_desc &d = L->desc;
+    size_t wexp, sexp, scount;
+    raw_sizes(d, wexp, sexp, scount);
+    if (weight_bytes != wexp) fail("export weight buffer has %zu bytes, expected %zu", weight_bytes, wexp);
+    if (d.format == DIALQ_FORMAT_W8A16 || d.format == DIALQ_FORMAT_FP8_ROW) {
+      // per-row scales are kept as f32; export them in the requested width
+      size_t n = (size_t)d.out_dim;
+      bool bf16 = d.format == DIALQ_FORMAT_W8A16 && d.scale_dtype == DIALQ_BF16;
+      if (scale_bytes != n * (bf16 ? 2 : 4)) fail("export scale buffer has %zu bytes, expected %zu", scale_bytes, n * (bf16 ? 2 : 4));
+    } else if (scale_bytes != sexp) {
+      fail("export scale buffer has %zu bytes, expected %zu", scale_bytes, sexp);
+    }
+    DeviceGuard dg(L->device);
+    hipStream_t st = nullptr;
+    DevBuf rw(wexp), rs(sexp);
+    hip_check(launch_unpack(d.format, d.out_dim, d.in_dim, (const uint8_t *)L->tiles.p,
+                            (const uint8_t *)L->aux.p, rw.p, rs.p, st),
+              "unpack");
+    hip_check(hipMemcpyAsync(weight, rw.p, wexp, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+    if (d.format == DIALQ_FORMAT_W8A16 || d.format == DIALQ_FORMAT_FP8_ROW) {
+      std::vector<float> hs((size_t)d.out_dim);
+      hip_check(hipMemcpyAsync(hs.data(), L->row_scale.p, hs.size() * 4, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+      if (d.format == DIALQ_FORMAT_W8A16 && d.scale_dtype == DIALQ_BF16) {
+        uint16_t *o = (uint16_t *)scales;
+        for (size_t i = 0; i < hs.size(); ++i) {
+          uint32_t u;
+          memcpy(&u, &hs[i], 4);
+          o[i] = (uint16_t)(u >> 16);  // exact: the value came from bf16
+        }
+      } else {
+        memcpy(scales, hs.data(), hs.size() * 4);
+      }
+    } else if (d.format == DIALQ_FORMAT_FP8_BLOCK) {
+      hip_check(hipMemcpyAsync(scales, L->block_scale.p, sexp, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+    } else if (sexp) {
+      hip_check(hipMemcpyAsync(scales, rs.p, sexp, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+    }
+    hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+  });
+}
+
+}  // extern "C"

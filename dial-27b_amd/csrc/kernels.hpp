@@ -1,0 +1,63 @@
+// Internal launcher interface between the C ABI (dialq.cpp) and the HIP
+// kernels.  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dialq {
+
+struct DequantArgs {
+  int fmt;
+  int64_t N, K, k_chunks, nbk;
+  int chunk, tile_bytes;
+  const uint8_t *tiles;
+  const uint8_t *aux;
+  const float *row_scale;
+  const float *block_scale;
+  float global;
+  void *out;
+  int out_dtype;
+};
+
+// Everything a product kernel needs to read one resident weight.
+struct WeightView {
+  int fmt;
+  int64_t N, K;
+  int64_t n_strips, k_chunks, nbk;
+  const uint8_t *tiles;
+  const uint8_t *aux;
+  const float *row_scale;    // W8A16, FP8_ROW: [n_strips*16]
+  const float *block_scale;  // FP8_BLOCK: [ceil(N/128), nbk]
+  float global;              // NVFP4 multiplier (1 otherwise)
+};
+
+hipError_t launch_quantize(int fmt, const void *dense, int dtype, int64_t N, int64_t K, void *raw_w,
+                           void *raw_s, hipStream_t st);
+hipError_t launch_repack(int fmt, int64_t N, int64_t K, const void *raw_w, const void *raw_s,
+                         int scale_is_bf16, int64_t scale_count, uint8_t *tiles, uint8_t *aux,
+                         float *row_scale, float *block_scale, hipStream_t st);
+hipError_t launch_unpack(int fmt, int64_t N, int64_t K, const uint8_t *tiles, const uint8_t *aux,
+                         void *raw_w, void *raw_s, hipStream_t st);
+hipError_t launch_dequant(const DequantArgs &a, hipStream_t st);
+hipError_t launch_act_fp8(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad, uint8_t *q,
+                          float *scale, hipStream_t st);
+hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad,
+                            uint8_t *packed, uint8_t *scales, hipStream_t st);
+
+// Decode GEMV: y[M,N] = x[M,K] W^T for any M (row groups of 16 per pass).
+hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
+                       int y_dtype, hipStream_t st);
+// Prefill GEMM with weight-only dequantization (bf16 / f16 MFMA operands).
+hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
+                       int y_dtype, hipStream_t st);
+// Native low-precision prefill: FP8_BLOCK with per-token fp8 activations,
+// MXFP4 with per-32 MXFP4 activations.  `xq` / `xs` are the quantized
+// activations (codes and scales) produced by launch_act_*.
+hipError_t launch_gemm_native(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M,
+                              int64_t k_pad, void *y, int y_dtype, hipStream_t st);
+// Local q8 W8A8 decode (one row).
+hipError_t launch_local_q8(const WeightView &w, const void *x, int x_dtype, void *y, int y_dtype,
+                           void *scratch, hipStream_t st);
+
+}  // namespace dialq

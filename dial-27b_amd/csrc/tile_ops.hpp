@@ -1,0 +1,323 @@
+// Per-format tile operations shared by the decode GEMV and the prefill GEMM.
+//
+// A resident tile (see common.hpp) is loaded by one wavefront, one 16- or
+// 32-byte piece per lane, and unpacked in registers into exact bf16 B
+// operands of v_mfma_f32_16x16x32_bf16 (BOps), together with the per-lane
+// scale factors of the lane's weight row n = lane % 16.  bops_mac then
+// multiply-accumulates those operands against NX activation operands
+// (XOp, lane l = row m = l % 16 of x) into the f32x4 accumulator
+// C[m = 4(l/16)+i][n = l%16].
+//
+// Exactness: every weight code is converted to an exact bf16 value (int8,
+// E4M3, E2M1 times an E4M3 or E8M0 scale, Q4_K nibbles offset by 128), so
+// the products are exact and only the fp32 accumulation order differs from
+// the oracle.  Scales that cannot be folded exactly into a bf16 operand
+// (Q8_0's f16 d, Q4_K's d*sc and dmin*m, FP8_BLOCK's f32 block scale) are
+// applied to the f32 partial product of their own k block.
+#pragma once
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace dialq {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// ---- activation operands ----------------------------------------------------
+// ACT = DIALQ_BF16: one bf16 part.  DIALQ_F16 / DIALQ_F32: bf16 hi + lo parts
+// (exact for f16, 2^-17 relative for f32), two MFMAs per product.
+template <int ACT>
+struct XOp {
+  u32x4 hi;
+  u32x4 lo;
+};
+
+template <int ACT>
+struct ActTraits {
+  static constexpr int PARTS = (ACT == DIALQ_BF16) ? 1 : 2;
+  static constexpr int BYTES = (ACT == DIALQ_F32) ? 4 : 2;
+};
+
+__device__ __forceinline__ void split_f32(float v, uint32_t &h, uint32_t &l) {
+  uint32_t b = __float_as_uint(v);
+  h = b >> 16;  // truncation is the exact high part
+  l = f32_to_bf16_bits(v - __uint_as_float(b & 0xffff0000u));
+}
+
+// 8 consecutive activations starting at element `idx` -> operand parts.
+template <int ACT>
+__device__ __forceinline__ XOp<ACT> x8_from_global(const void *x, int64_t idx) {
+  XOp<ACT> r;
+  if constexpr (ACT == DIALQ_BF16) {
+    r.hi = *(const u32x4 *)((const uint16_t *)x + idx);
+    r.lo = (u32x4){0, 0, 0, 0};
+  } else if constexpr (ACT == DIALQ_F16) {
+    u32x4 raw = *(const u32x4 *)((const uint16_t *)x + idx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t h0, l0, h1, l1;
+      split_f32(f16_bits_to_f32(raw[i] & 0xffffu), h0, l0);
+      split_f32(f16_bits_to_f32(raw[i] >> 16), h1, l1);
+      r.hi[i] = h0 | (h1 << 16);
+      r.lo[i] = l0 | (l1 << 16);
+    }
+  } else {
+    u32x8 raw = *(const u32x8 *)((const float *)x + idx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t h0, l0, h1, l1;
+      split_f32(__uint_as_float(raw[2 * i]), h0, l0);
+      split_f32(__uint_as_float(raw[2 * i + 1]), h1, l1);
+      r.hi[i] = h0 | (h1 << 16);
+      r.lo[i] = l0 | (l1 << 16);
+    }
+  }
+  return r;
+}
+
+template <int ACT>
+__device__ __forceinline__ XOp<ACT> load_x8(const void *x, int64_t m, int64_t k, int64_t M,
+                                            int64_t K) {
+  if (m < M && k < K) return x8_from_global<ACT>(x, m * K + k);
+  XOp<ACT> r;
+  r.hi = (u32x4){0, 0, 0, 0};
+  r.lo = (u32x4){0, 0, 0, 0};
+  return r;
+}
+
+template <int ACT>
+__device__ __forceinline__ f32x4 mfma_x(const XOp<ACT> &a, u32x4 b, f32x4 c) {
+  c = mfma_bf16(a.hi, b, c);
+  if constexpr (ACT != DIALQ_BF16) c = mfma_bf16(a.lo, b, c);
+  return c;
+}
+
+// ---- weight code -> exact bf16 --------------------------------------------
+__device__ __forceinline__ u32x4 i8x8_to_bf16(uint32_t d0, uint32_t d1) {
+  u32x4 r;
+  uint32_t d[2] = {d0, d1};
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    float f0 = (float)((int32_t)(d[w] << 24) >> 24);
+    float f1 = (float)((int32_t)(d[w] << 16) >> 24);
+    float f2 = (float)((int32_t)(d[w] << 8) >> 24);
+    float f3 = (float)((int32_t)d[w] >> 24);
+    r[2 * w] = pack_bf16_trunc(f0, f1);
+    r[2 * w + 1] = pack_bf16_trunc(f2, f3);
+  }
+  return r;
+}
+
+__device__ __forceinline__ u32x4 e4m3x8_to_bf16(uint32_t d0, uint32_t d1) {
+  u32x4 r;
+  r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, false));
+  r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, true));
+  r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, false));
+  r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, true));
+  return r;
+}
+
+// 8 E2M1 codes (low nibble first) times an f32 scale whose product with
+// any E2M1 value is exact in bf16 (an E4M3 or E8M0 value): decode to f32,
+// multiply (exact), keep the high half.
+__device__ __forceinline__ u32x4 e2m1x8_to_bf16(uint32_t d, float scale) {
+  u32x4 r;
+  f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 0);
+  f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 1);
+  f32x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 2);
+  f32x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 3);
+  r[0] = pack_bf16_trunc(v0[0] * scale, v0[1] * scale);
+  r[1] = pack_bf16_trunc(v1[0] * scale, v1[1] * scale);
+  r[2] = pack_bf16_trunc(v2[0] * scale, v2[1] * scale);
+  r[3] = pack_bf16_trunc(v3[0] * scale, v3[1] * scale);
+  return r;
+}
+
+// 8 nibbles (shift 0 = low, 4 = high) of two dwords -> bf16 (128 + q).
+__device__ __forceinline__ u32x4 nib8_to_bf16_off128(uint32_t d0, uint32_t d1, int shift) {
+  uint32_t a = (d0 >> shift) & 0x0f0f0f0fu, b = (d1 >> shift) & 0x0f0f0f0fu;
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(0x43434343u, a, 0x04010400u);
+  r[1] = __builtin_amdgcn_perm(0x43434343u, a, 0x04030402u);
+  r[2] = __builtin_amdgcn_perm(0x43434343u, b, 0x04010400u);
+  r[3] = __builtin_amdgcn_perm(0x43434343u, b, 0x04030402u);
+  return r;
+}
+
+// ---- format traits -----------------------------------------------------------
+// CHUNK: k per tile; LANE: bytes per lane; NX: MFMA k-slices per tile;
+// xk(t, g): k offset (within the chunk) of slice t for lane group g.
+template <int FMT>
+struct FmtTraits;
+template <>
+struct FmtTraits<DIALQ_FORMAT_W8A16> {
+  static constexpr int CHUNK = 64, LANE = 16, NX = 2;
+  __device__ static int xk(int t, int g) { return 16 * g + 8 * t; }
+};
+template <>
+struct FmtTraits<DIALQ_FORMAT_FP8_ROW> {
+  static constexpr int CHUNK = 64, LANE = 16, NX = 2;
+  __device__ static int xk(int t, int g) { return 16 * g + 8 * t; }
+};
+template <>
+struct FmtTraits<DIALQ_FORMAT_Q8_0> {
+  static constexpr int CHUNK = 64, LANE = 16, NX = 2;
+  __device__ static int xk(int t, int g) { return 32 * t + 8 * g; }
+};
+template <>
+struct FmtTraits<DIALQ_FORMAT_FP8_BLOCK> {
+  static constexpr int CHUNK = 128, LANE = 32, NX = 4;
+  __device__ static int xk(int t, int g) { return 32 * g + 8 * t; }
+};
+template <>
+struct FmtTraits<DIALQ_FORMAT_NVFP4> {
+  static constexpr int CHUNK = 128, LANE = 16, NX = 4;
+  __device__ static int xk(int t, int g) { return 32 * g + 8 * t; }
+};
+template <>
+struct FmtTraits<DIALQ_FORMAT_MXFP4> {
+  static constexpr int CHUNK = 128, LANE = 16, NX = 4;
+  __device__ static int xk(int t, int g) { return 32 * g + 8 * t; }
+};
+template <>
+struct FmtTraits<DIALQ_FORMAT_Q4_K> {
+  static constexpr int CHUNK = 256, LANE = 32, NX = 8;
+  __device__ static int xk(int t, int g) { return 32 * t + 8 * g; }
+};
+
+struct RawTile {
+  u32x4 a;
+  u32x4 b;  // second 16 bytes (LANE == 32 formats)
+};
+
+template <int FMT>
+__device__ __forceinline__ RawTile load_tile(const uint8_t *tiles, int64_t tile_idx, int lane) {
+  constexpr int LANE = FmtTraits<FMT>::LANE;
+  const uint8_t *p = tiles + tile_idx * (64 * LANE) + lane * LANE;
+  RawTile r;
+  r.a = __builtin_nontemporal_load((const u32x4 *)p);
+  if constexpr (LANE == 32)
+    r.b = __builtin_nontemporal_load((const u32x4 *)(p + 16));
+  else
+    r.b = (u32x4){0, 0, 0, 0};
+  return r;
+}
+
+// B operands of one tile plus the lane row's scale factors.
+template <int FMT>
+struct BOps {
+  u32x4 b[FmtTraits<FMT>::NX];
+  float s1[FmtTraits<FMT>::NX];  // Q8_0: d per block; Q4_K: d*sc; FP8_BLOCK: s
+  float s2[FmtTraits<FMT>::NX];  // Q4_K: 128*d*sc + dmin*m
+};
+
+template <int FMT>
+__device__ __forceinline__ BOps<FMT> make_bops(const RawTile &t, const WeightView &w, int64_t s,
+                                               int64_t c, int lane) {
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t tidx = s * w.k_chunks + c;
+  BOps<FMT> o;
+  if constexpr (FMT == DIALQ_FORMAT_W8A16) {
+    o.b[0] = i8x8_to_bf16(t.a[0], t.a[1]);
+    o.b[1] = i8x8_to_bf16(t.a[2], t.a[3]);
+  } else if constexpr (FMT == DIALQ_FORMAT_FP8_ROW) {
+    o.b[0] = e4m3x8_to_bf16(t.a[0], t.a[1]);
+    o.b[1] = e4m3x8_to_bf16(t.a[2], t.a[3]);
+  } else if constexpr (FMT == DIALQ_FORMAT_Q8_0) {
+    uint32_t dd = *(const uint32_t *)(w.aux + tidx * 64 + r * 4);
+    o.s1[0] = f16_bits_to_f32(dd & 0xffffu);
+    o.s1[1] = f16_bits_to_f32(dd >> 16);
+    o.b[0] = i8x8_to_bf16(t.a[0], t.a[1]);
+    o.b[1] = i8x8_to_bf16(t.a[2], t.a[3]);
+  } else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK) {
+    o.s1[0] = w.block_scale[((s * 16) / 128) * w.nbk + c];
+    o.b[0] = e4m3x8_to_bf16(t.a[0], t.a[1]);
+    o.b[1] = e4m3x8_to_bf16(t.a[2], t.a[3]);
+    o.b[2] = e4m3x8_to_bf16(t.b[0], t.b[1]);
+    o.b[3] = e4m3x8_to_bf16(t.b[2], t.b[3]);
+  } else if constexpr (FMT == DIALQ_FORMAT_NVFP4) {
+    uint32_t sb = *(const uint16_t *)(w.aux + tidx * 128 + r * 8 + 2 * g);
+    float g0 = e4m3_to_f32(sb & 0xffu), g1 = e4m3_to_f32(sb >> 8);
+    o.b[0] = e2m1x8_to_bf16(t.a[0], g0);
+    o.b[1] = e2m1x8_to_bf16(t.a[1], g0);
+    o.b[2] = e2m1x8_to_bf16(t.a[2], g1);
+    o.b[3] = e2m1x8_to_bf16(t.a[3], g1);
+  } else if constexpr (FMT == DIALQ_FORMAT_MXFP4) {
+    float sc = e8m0_to_f32(w.aux[tidx * 64 + r * 4 + g]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o.b[i] = e2m1x8_to_bf16(t.a[i], sc);
+  } else if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
+    u32x4 h = *(const u32x4 *)(w.aux + tidx * 256 + r * 16);
+    float d = f16_bits_to_f32(h[0] & 0xffffu), dmin = f16_bits_to_f32(h[0] >> 16);
+    uint32_t sc8[12];
+#pragma unroll
+    for (int i = 0; i < 12; ++i) sc8[i] = (h[1 + i / 4] >> (8 * (i % 4))) & 0xffu;
+    const uint32_t qd[8] = {t.a[0], t.a[1], t.a[2], t.a[3], t.b[0], t.b[1], t.b[2], t.b[3]};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t scj, mj;
+      if (j < 4) {
+        scj = sc8[j] & 63u;
+        mj = sc8[j + 4] & 63u;
+      } else {
+        scj = (sc8[j + 4] & 0xfu) | ((sc8[j - 4] >> 6) << 4);
+        mj = (sc8[j + 4] >> 4) | ((sc8[j] >> 6) << 4);
+      }
+      float s1 = d * (float)scj;
+      o.s1[j] = s1;
+      o.s2[j] = __builtin_fmaf(128.0f, s1, dmin * (float)mj);
+      const int i4 = j >> 1;
+      o.b[j] = nib8_to_bf16_off128(qd[2 * i4], qd[2 * i4 + 1], (j & 1) ? 4 : 0);
+    }
+  }
+  return o;
+}
+
+// acc += (x slices) . (weight tile) for one 16-row group of x.
+template <int FMT, int ACT>
+__device__ __forceinline__ void bops_mac(const BOps<FMT> &o, const XOp<ACT> *xo, f32x4 &acc) {
+  const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW ||
+                FMT == DIALQ_FORMAT_NVFP4 || FMT == DIALQ_FORMAT_MXFP4) {
+#pragma unroll
+    for (int t = 0; t < FmtTraits<FMT>::NX; ++t) acc = mfma_x<ACT>(xo[t], o.b[t], acc);
+  } else if constexpr (FMT == DIALQ_FORMAT_Q8_0) {
+    f32x4 p0 = mfma_x<ACT>(xo[0], o.b[0], zero);
+    f32x4 p1 = mfma_x<ACT>(xo[1], o.b[1], zero);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc[i] = __builtin_fmaf(o.s1[1], p1[i], __builtin_fmaf(o.s1[0], p0[i], acc[i]));
+  } else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK) {
+    f32x4 p = zero;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) p = mfma_x<ACT>(xo[t], o.b[t], p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(o.s1[0], p[i], acc[i]);
+  } else if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
+    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      f32x4 pq = mfma_x<ACT>(xo[j], o.b[j], zero);
+      f32x4 px = mfma_x<ACT>(xo[j], ones, zero);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[i] = __builtin_fmaf(o.s1[j], pq[i], __builtin_fmaf(-o.s2[j], px[i], acc[i]));
+    }
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ float epilogue_scale(const WeightView &w, int64_t n) {
+  if constexpr (FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW) return w.row_scale[n];
+  if constexpr (FMT == DIALQ_FORMAT_NVFP4) return w.global;
+  return 1.0f;
+}
+
+}  // namespace dialq

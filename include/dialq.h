@@ -1,0 +1,181 @@
+/*
+ * dialq -- C ABI of the MI355X (gfx950) quantized-linear library.
+ *
+ * This is the drop-in boundary for DIAL's quantized linear layer: the entry
+ * points below are what a thin Rust FFI crate behind dial-core's
+ * TextLinear / QuantLinear (candle CustomOp1) call sites binds.  The
+ * conventions follow the reference's only C ABI, the GGML adapter
+ * (backends/qwen38_ggml/adapter.h:8-46): an ABI-version export, opaque owned
+ * handles, `char *error, size_t error_size` out-parameters, int 0 / -1
+ * status, and a `device_io` flag that says whether buffers are device
+ * (HIP) pointers or host pointers.  Nothing here throws across the ABI.
+ *
+ * Threading: calls on different handles may run concurrently.  Calls on one
+ * handle are stream-ordered; callers serialize forward calls that share a
+ * handle across streams (each handle owns one scratch area), and never
+ * destroy a handle while a forward on it is in flight.
+ *
+ * Weight layout: W is [out_dim (N), in_dim (K)] row-major (out x in), as in
+ * the reference (worker_w8a16.rs:294-297, cuda_quant.rs:289-358).  x is
+ * [rows (M), K] row-major contiguous; y is [M, N].
+ */
+#ifndef DIALQ_H
+#define DIALQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DIALQ_ABI_VERSION 1u
+
+/* Weight formats.  The raw byte layouts are the reference's (or GGUF's /
+ * OCP MX's) storage layouts; dialq_linear_create repacks them into the
+ * device-resident tiled layout. */
+enum dialq_format {
+  /* int8 [N,K] + one scale per row, f32 (worker_w8a16.rs:294-297) or bf16 */
+  DIALQ_FORMAT_W8A16 = 1,
+  /* GGUF Q8_0: [N, K/32] blocks of {f16 d; i8 qs[32]} (34 B) */
+  DIALQ_FORMAT_Q8_0 = 2,
+  /* GGUF Q4_K: [N, K/256] super-blocks {f16 d, dmin; u8 scales[12]; u8 qs[128]} */
+  DIALQ_FORMAT_Q4_K = 3,
+  /* E4M3 [N,K] + f32 scale per row, or one per tensor (cuda_quant.rs:58-65) */
+  DIALQ_FORMAT_FP8_ROW = 4,
+  /* E4M3 [N,K] + f32 scale per 128x128 block, [ceil(N/128), ceil(K/128)] */
+  DIALQ_FORMAT_FP8_BLOCK = 5,
+  /* NVFP4: E2M1 [N, K/2] (low nibble = even k) + E4M3 scale per 16 + f32
+   * global (cuda_quant.rs:43-56, quant.rs:160-208) */
+  DIALQ_FORMAT_NVFP4 = 6,
+  /* MXFP4 (OCP MX v1.0): E2M1 [N, K/2] + E8M0 scale per 32 along K */
+  DIALQ_FORMAT_MXFP4 = 7
+};
+
+enum dialq_dtype { DIALQ_F32 = 0, DIALQ_F16 = 1, DIALQ_BF16 = 2 };
+
+/* desc.flags */
+#define DIALQ_FLAG_GLOBAL_IS_DIVISOR 0x1 /* NVFP4 compressed-tensors: the
+  stored global scale is a divisor; the multiplier is 1/global
+  (quant.rs:322-329, quant.rs:407-412) */
+#define DIALQ_FLAG_WEIGHT_ONLY_PREFILL 0x2 /* FP8_BLOCK / MXFP4: keep the
+  weight-only bf16 product for prefill instead of quantizing activations
+  for the native fp8 / fp4 MFMA product */
+
+typedef struct dialq_linear_desc {
+  int32_t format;      /* enum dialq_format */
+  int32_t scale_dtype; /* W8A16: DIALQ_F32 or DIALQ_BF16; else ignored */
+  int64_t out_dim;     /* N */
+  int64_t in_dim;      /* K */
+  float global_scale;  /* NVFP4 global scale (see DIALQ_FLAG_GLOBAL_IS_DIVISOR) */
+  int32_t flags;
+} dialq_linear_desc;
+
+/* Kernel selection for dialq_linear_forward_ex. */
+enum dialq_path {
+  DIALQ_PATH_AUTO = 0,        /* GEMV for rows <= 64, GEMM above */
+  DIALQ_PATH_GEMV = 1,        /* decode kernel, any rows (loops over row groups) */
+  DIALQ_PATH_GEMM = 2,        /* weight-only MFMA GEMM (bf16/f16 operands) */
+  DIALQ_PATH_GEMM_NATIVE = 3  /* FP8_BLOCK / MXFP4: activations quantized per
+                                 token (fp8) or per 32 (MXFP4), fp8/fp4 MFMA */
+};
+
+/* Replaces the NVRTC kernel-availability checks of
+ * worker_w8a16.rs:236-289 / cuda_quant.rs:214-267 and the adapter's
+ * dial_ggml_abi_version (adapter.h:16). */
+uint32_t dialq_abi_version(void);
+
+/* Upload and repack pre-quantized weights.  Replaces the constructors
+ * CudaQuantLinear::nvfp4 / ::fp8 (cuda_quant.rs:289-358, including their
+ * length checks and messages) and the upload half of
+ * CudaW8A16Linear::from_linear (worker_w8a16.rs:343-350).
+ *   weight / weight_bytes: raw format bytes (layout per enum dialq_format)
+ *   scales / scale_bytes:  W8A16: N f32|bf16; FP8_ROW: N or 1 f32;
+ *                          FP8_BLOCK: ceil(N/128)*ceil(K/128) f32;
+ *                          NVFP4: N*K/16 E4M3 bytes; MXFP4: N*K/32 E8M0 bytes;
+ *                          Q8_0 / Q4_K: NULL, 0 (scales live in the blocks)
+ *   host_io: 1 = weight/scales are host pointers, 0 = device pointers
+ *   stream:  hipStream_t (NULL = default stream); the call synchronizes it
+ * Returns an owned handle, or NULL with a message in `error`. */
+void *dialq_linear_create(const dialq_linear_desc *desc, const void *weight,
+                          size_t weight_bytes, const void *scales,
+                          size_t scale_bytes, int device, int host_io,
+                          void *stream, char *error, size_t error_size);
+
+/* Quantize a dense [N,K] weight on the GPU and keep it resident.
+ * W8A16 replaces CudaW8A16Linear::from_linear (worker_w8a16.rs:302-366: the
+ * reference downloads the F16 weight, quantizes per row on the host and
+ * uploads; here the same per-row arithmetic runs on the device).  Q8_0 and
+ * Q4_K replace candle's QTensor::quantize (called at worker_gguf.rs:641,657
+ * and ggml_tests.rs:83-84).  FP8_BLOCK and MXFP4 quantize round-to-nearest-
+ * even with one f32 scale per 128x128 block / one E8M0 scale per 32.
+ *   dense: [N,K] of dense_dtype (F32, F16 or BF16); host pointer if
+ *   host_io = 1, else a device pointer. */
+void *dialq_linear_quantize(const dialq_linear_desc *desc, const void *dense,
+                            int32_t dense_dtype, int device, int host_io,
+                            void *stream, char *error, size_t error_size);
+
+/* Free a handle (Drop of CudaW8A16Linear / CudaQuantLinear). NULL is a no-op. */
+void dialq_linear_destroy(void *linear);
+
+/* Bytes the reference would count as resident for this weight: the formula
+ * of CudaQuantLinear::resident_bytes (cuda_quant.rs:360-371) for NVFP4
+ * (N*K/2 + N*K/16 + 4) and FP8_ROW (N*K + 4N), of from_linear's summary for
+ * W8A16 (N*K + N*sizeof(scale), worker_w8a16.rs:351), and the packed format
+ * size for the others. */
+uint64_t dialq_linear_resident_bytes(const void *linear);
+
+/* Bytes actually held on the device (tiles + scales + scratch). */
+uint64_t dialq_linear_device_bytes(const void *linear);
+
+/* Copy the handle's description out. */
+int dialq_linear_describe(const void *linear, dialq_linear_desc *desc);
+
+/* Forward y = x W^T.  Replaces CudaW8A16Linear::forward + cuda_fwd
+ * (worker_w8a16.rs:368-386,402-475), CudaQuantLinear::forward + cuda_fwd
+ * (cuda_quant.rs:373-391,406-499) and the GGUF QMatMul::forward call of
+ * forward_worker_gguf (worker_gguf.rs:574-611).
+ *   x: [rows, K] of x_dtype (F16, BF16 or F32), contiguous
+ *   y: [rows, N] of y_dtype (F16, BF16 or F32), written in full
+ *   device_io: 1 = x / y are device pointers (asynchronous on `stream`);
+ *              0 = host pointers (copied in and out; synchronous)
+ * rows == 0 is a successful no-op.  Returns 0, or -1 with a message. */
+int dialq_linear_forward(void *linear, const void *x, int32_t x_dtype,
+                         int64_t rows, void *y, int32_t y_dtype, void *stream,
+                         int device_io, char *error, size_t error_size);
+
+/* As dialq_linear_forward with an explicit kernel choice (enum dialq_path). */
+int dialq_linear_forward_ex(void *linear, const void *x, int32_t x_dtype,
+                            int64_t rows, void *y, int32_t y_dtype,
+                            int32_t path, void *stream, int device_io,
+                            char *error, size_t error_size);
+
+/* Dequantize the resident weight into a dense [N,K] matrix of out_dtype
+ * (F32, F16 or BF16, each rounded once to nearest-even from the exact f32
+ * value).  Replaces QMatMul::dequantize_f16 (worker_w8a16.rs:125, used by
+ * build_worker_gguf_fp16_prefill_linear, worker_gguf.rs:425-452) and the
+ * host decoders load_nvfp4 / load_fp8 / decode_nvfp4_values
+ * (quant.rs:160-208,252-363). */
+int dialq_linear_dequantize(const void *linear, void *out, int32_t out_dtype,
+                            void *stream, int device_io, char *error,
+                            size_t error_size);
+
+/* Export the raw (reference-layout) weight and scale bytes of a handle, e.g.
+ * after dialq_linear_quantize.  Sizes must equal the format's raw sizes.
+ * Host buffers; synchronous. */
+int dialq_linear_export(const void *linear, void *weight, size_t weight_bytes,
+                        void *scales, size_t scale_bytes, char *error,
+                        size_t error_size);
+
+/* Local q8 decode (qwen3_vl/text.rs:291-336): W8A8 with a per-tensor int8
+ * activation scale, exact int32 dot, y = f32(acc) * scale[n] * x_scale.
+ * Requires a W8A16 handle with f32 scales and rows == 1. */
+int dialq_local_q8_forward(void *linear, const void *x, int32_t x_dtype,
+                           int64_t rows, void *y, int32_t y_dtype,
+                           void *stream, int device_io, char *error,
+                           size_t error_size);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DIALQ_H */

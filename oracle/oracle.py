@@ -1,0 +1,332 @@
+"""numpy front end of the CPU oracle (oracle/lib/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke check and the
+benchmark's cpu_baseline leg, as the checker.  The product library never
+imports it.  Each wrapper names the C function (and through it the reference
+file:line) it calls; see oracle.h for the parity status of each.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "lib", "liboracle.so")
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile oracle.c / cpu_baseline.c with the Makefile beside them."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-C", _HERE] + (["-B"] if force else []), check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = C.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_P = C.c_void_p
+_I64 = C.c_int64
+
+
+def _declare(L):
+    sig = {
+        "or_version": (C.c_uint32, []),
+        "or_f16_to_f32": (C.c_float, [C.c_uint16]),
+        "or_f32_to_f16": (C.c_uint16, [C.c_float]),
+        "or_bf16_to_f32": (C.c_float, [C.c_uint16]),
+        "or_f32_to_bf16": (C.c_uint16, [C.c_float]),
+        "or_e4m3_to_f32": (C.c_float, [C.c_uint8]),
+        "or_e4m3_to_f32_ocp": (C.c_float, [C.c_uint8]),
+        "or_f32_to_e4m3": (C.c_uint8, [C.c_float]),
+        "or_e2m1_to_f32": (C.c_float, [C.c_uint8]),
+        "or_f32_to_e2m1": (C.c_uint8, [C.c_float]),
+        "or_e8m0_to_f32": (C.c_float, [C.c_uint8]),
+        "or_w8a16_quantize": (None, [_P, _I64, _I64, _P, _P, _P]),
+        "or_w8a16_dequant": (None, [_P, _P, C.c_int, _I64, _I64, _P]),
+        "or_q8_0_quantize": (None, [_P, _I64, _I64, _P]),
+        "or_q8_0_dequant": (None, [_P, _I64, _I64, _P]),
+        "or_q4_k_quantize": (None, [_P, _I64, _I64, _P]),
+        "or_q4_k_dequant": (None, [_P, _I64, _I64, _P]),
+        "or_fp8_row_dequant": (None, [_P, _P, _I64, _I64, _P]),
+        "or_fp8_block_quantize": (None, [_P, _I64, _I64, _P, _P]),
+        "or_fp8_block_dequant": (None, [_P, _P, _I64, _I64, _P]),
+        "or_nvfp4_dequant": (C.c_int, [_P, C.c_size_t, _P, C.c_size_t, C.c_int, C.c_float,
+                                       _I64, _I64, _P, C.c_char_p, C.c_size_t]),
+        "or_mxfp4_quantize": (None, [_P, _I64, _I64, _P, _P]),
+        "or_mxfp4_dequant": (None, [_P, _P, _I64, _I64, _P]),
+        "or_act_fp8_quantize": (None, [_P, _I64, _I64, _P, _P]),
+        "or_act_mxfp4_quantize": (None, [_P, _I64, _I64, _P, _P]),
+        "or_matmul_f64": (None, [_P, _P, _I64, _I64, _I64, _P]),
+        "or_w8a16_linear": (None, [_P, _P, _P, C.c_int, _I64, _I64, _I64, _P]),
+        "or_local_q8_forward": (None, [_P, _I64, _P, _P, _I64, _P]),
+        "cb_w8a16_gemv": (None, [_P, _I64, _I64, _P, _P, _I64, _P, C.c_int]),
+        "cb_q4_k_gemv": (None, [_P, _I64, _I64, _P, _I64, _P, C.c_int]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- scalar codecs (vectorised over numpy arrays) -------------------------
+def _vec(fn, dtype_out, arr):
+    L = lib()
+    f = getattr(L, fn)
+    flat = np.asarray(arr).ravel()
+    return np.array([f(v.item()) for v in flat], dtype=dtype_out).reshape(np.shape(arr))
+
+
+def f16_bits_to_f32(h):
+    return _vec("or_f16_to_f32", np.float32, np.asarray(h, np.uint16))
+
+
+def f32_to_f16_bits(f):
+    return _vec("or_f32_to_f16", np.uint16, np.asarray(f, np.float32))
+
+
+def bf16_bits_to_f32(h):
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(f):
+    return _vec("or_f32_to_bf16", np.uint16, np.asarray(f, np.float32))
+
+
+def e4m3_to_f32(codes, ocp: bool = False):
+    return _vec("or_e4m3_to_f32_ocp" if ocp else "or_e4m3_to_f32", np.float32,
+                np.asarray(codes, np.uint8))
+
+
+def f32_to_e4m3(f):
+    return _vec("or_f32_to_e4m3", np.uint8, np.asarray(f, np.float32))
+
+
+def e2m1_to_f32(codes):
+    return _vec("or_e2m1_to_f32", np.float32, np.asarray(codes, np.uint8))
+
+
+def f32_to_e2m1(f):
+    return _vec("or_f32_to_e2m1", np.uint8, np.asarray(f, np.float32))
+
+
+def e8m0_to_f32(e):
+    return _vec("or_e8m0_to_f32", np.float32, np.asarray(e, np.uint8))
+
+
+# ---- formats ---------------------------------------------------------------
+def w8a16_quantize(w):
+    w = _f32(w)
+    n, k = w.shape
+    q = np.empty((n, k), np.int8)
+    s = np.empty(n, np.float32)
+    sb = np.empty(n, np.uint16)
+    lib().or_w8a16_quantize(_p(w), n, k, _p(q), _p(s), _p(sb))
+    return q, s, sb
+
+
+def w8a16_dequant(q, scale):
+    q = np.ascontiguousarray(q, np.int8)
+    n, k = q.shape
+    is_bf16 = np.asarray(scale).dtype == np.uint16
+    scale = np.ascontiguousarray(scale, np.uint16 if is_bf16 else np.float32)
+    out = np.empty((n, k), np.float32)
+    lib().or_w8a16_dequant(_p(q), _p(scale), int(is_bf16), n, k, _p(out))
+    return out
+
+
+def q8_0_quantize(w):
+    w = _f32(w)
+    n, k = w.shape
+    out = np.empty((n, k // 32 * 34), np.uint8)
+    lib().or_q8_0_quantize(_p(w), n, k, _p(out))
+    return out
+
+
+def q8_0_dequant(blocks, n, k):
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    out = np.empty((n, k), np.float32)
+    lib().or_q8_0_dequant(_p(blocks), n, k, _p(out))
+    return out
+
+
+def q4_k_quantize(w):
+    w = _f32(w)
+    n, k = w.shape
+    out = np.empty((n, k // 256 * 144), np.uint8)
+    lib().or_q4_k_quantize(_p(w), n, k, _p(out))
+    return out
+
+
+def q4_k_dequant(blocks, n, k):
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    out = np.empty((n, k), np.float32)
+    lib().or_q4_k_dequant(_p(blocks), n, k, _p(out))
+    return out
+
+
+def fp8_row_dequant(q, scale):
+    q = np.ascontiguousarray(q, np.uint8)
+    n, k = q.shape
+    scale = np.ascontiguousarray(np.broadcast_to(np.asarray(scale, np.float32), (n,)))
+    out = np.empty((n, k), np.float32)
+    lib().or_fp8_row_dequant(_p(q), _p(scale), n, k, _p(out))
+    return out
+
+
+def fp8_block_quantize(w):
+    w = _f32(w)
+    n, k = w.shape
+    q = np.empty((n, k), np.uint8)
+    s = np.empty(((n + 127) // 128, (k + 127) // 128), np.float32)
+    lib().or_fp8_block_quantize(_p(w), n, k, _p(q), _p(s))
+    return q, s
+
+
+def fp8_block_dequant(q, s):
+    q = np.ascontiguousarray(q, np.uint8)
+    s = np.ascontiguousarray(s, np.float32)
+    n, k = q.shape
+    out = np.empty((n, k), np.float32)
+    lib().or_fp8_block_dequant(_p(q), _p(s), n, k, _p(out))
+    return out
+
+
+def nvfp4_dequant(packed, scales, global_scale, n, k, scales_are_e4m3=None):
+    packed = np.ascontiguousarray(packed, np.uint8).ravel()
+    scales = np.asarray(scales)
+    if scales_are_e4m3 is None:
+        scales_are_e4m3 = scales.dtype == np.uint8
+    scales = np.ascontiguousarray(scales, np.uint8 if scales_are_e4m3 else np.float32).ravel()
+    out = np.empty((n, k), np.float32)
+    err = C.create_string_buffer(256)
+    rc = lib().or_nvfp4_dequant(_p(packed), packed.size, _p(scales), scales.size,
+                                int(scales_are_e4m3), float(global_scale), n, k, _p(out), err, 256)
+    if rc != 0:
+        raise ValueError(err.value.decode())
+    return out
+
+
+def mxfp4_quantize(w):
+    w = _f32(w)
+    n, k = w.shape
+    packed = np.empty((n, k // 2), np.uint8)
+    scales = np.empty((n, k // 32), np.uint8)
+    lib().or_mxfp4_quantize(_p(w), n, k, _p(packed), _p(scales))
+    return packed, scales
+
+
+def mxfp4_dequant(packed, scales):
+    packed = np.ascontiguousarray(packed, np.uint8)
+    scales = np.ascontiguousarray(scales, np.uint8)
+    n = packed.shape[0]
+    k = packed.shape[1] * 2
+    out = np.empty((n, k), np.float32)
+    lib().or_mxfp4_dequant(_p(packed), _p(scales), n, k, _p(out))
+    return out
+
+
+def act_fp8_quantize(x):
+    x = _f32(x)
+    m, k = x.shape
+    q = np.empty((m, k), np.uint8)
+    s = np.empty(m, np.float32)
+    lib().or_act_fp8_quantize(_p(x), m, k, _p(q), _p(s))
+    return q, s
+
+
+def act_mxfp4_quantize(x):
+    return mxfp4_quantize(x)
+
+
+def matmul_f64(x, w):
+    x = _f32(x)
+    w = _f32(w)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float64)
+    lib().or_matmul_f64(_p(x), _p(w), m, n, k, _p(y))
+    return y
+
+
+def w8a16_linear(x, q, scale):
+    x = _f32(x)
+    q = np.ascontiguousarray(q, np.int8)
+    m, k = x.shape
+    n = q.shape[0]
+    is_bf16 = np.asarray(scale).dtype == np.uint16
+    scale = np.ascontiguousarray(scale, np.uint16 if is_bf16 else np.float32)
+    y = np.empty((m, n), np.float32)
+    lib().or_w8a16_linear(_p(x), _p(q), _p(scale), int(is_bf16), m, n, k, _p(y))
+    return y
+
+
+def local_q8_forward(x, q, scale):
+    x = _f32(x).ravel()
+    q = np.ascontiguousarray(q, np.int8)
+    n, k = q.shape
+    scale = np.ascontiguousarray(scale, np.float32)
+    y = np.empty(n, np.float32)
+    lib().or_local_q8_forward(_p(x), k, _p(q), _p(scale), n, _p(y))
+    return y
+
+
+# ---- CPU baseline (timed by bench.py's cpu_baseline leg) -----------------
+def cpu_w8a16_gemv(x_bf16, q, scale_bf16, threads):
+    x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
+    m, k = x_bf16.shape
+    n = q.shape[0]
+    y = np.empty((m, n), np.float32)
+    lib().cb_w8a16_gemv(_p(x_bf16), m, k, _p(q), _p(scale_bf16), n, _p(y), int(threads))
+    return y
+
+
+def cpu_q4_k_gemv(x_bf16, blocks, n, threads):
+    x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
+    m, k = x_bf16.shape
+    y = np.empty((m, n), np.float32)
+    lib().cb_q4_k_gemv(_p(x_bf16), m, k, _p(blocks), n, _p(y), int(threads))
+    return y
+
+
+# ---- helpers ---------------------------------------------------------------
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    den = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / (den if den > 0 else 1.0))
+
+
+def round_bf16(a) -> np.ndarray:
+    """Round f32 values to bf16 (RNE) and back to f32 -- vectorised mirror of
+    or_f32_to_bf16 for large arrays (checked against it in tests)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    rb = 0x8000
+    up = ((u & rb) != 0) & ((u & (3 * rb - 1)) != 0)
+    hi = (u >> 16) + up.astype(np.uint64)
+    hi = np.where(nan, (u >> 16) | 0x40, hi)
+    return (hi.astype(np.uint32) << 16).view(np.float32)
+
+
+def round_f16(a) -> np.ndarray:
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)

@@ -1,0 +1,240 @@
+"""GPU parity: every format's quantizer, repacker, dequantizer, decode GEMV
+and prefill GEMM, called through the C ABI, against the CPU oracle.
+
+Bars: integer / byte work (quantized codes, scales, dequantized weights, the
+local-q8 output) bit-exact; products within 1e-3 relative L2 (bf16 / f16
+outputs, weight-only paths) or 2e-3 (native fp8 / fp4 prefill, whose oracle
+applies the same activation quantizer) of the fp64 oracle product rounded to
+the output dtype."""
+import numpy as np
+import pytest
+
+import dialq as dq
+import oracle as O
+from helpers import (empty_out, exact_inputs, k_align, make_weight, reference_product, to_torch)
+
+pytestmark = pytest.mark.gpu
+
+ALL_FORMATS = [dq.W8A16, dq.Q8_0, dq.Q4_K, dq.FP8_ROW, dq.FP8_BLOCK, dq.NVFP4, dq.MXFP4]
+TOL_BF16 = 1e-3   # relative L2, weight-only products
+TOL_LOWP = 2e-3   # relative L2, native fp8 / fp4 prefill
+
+
+def _linear(fmt, n, k, seed=0, **kw):
+    raw, scales, ckw, deq = make_weight(fmt, n, k, seed, **kw)
+    lin = dq.Linear.create(fmt, n, k, raw, scales, **ckw)
+    return lin, raw, scales, deq
+
+
+def _run(lin, deq, m, x_dtype, y_dtype, path, dev, seed=1):
+    import torch
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 1, (m, lin.in_dim)).astype(np.float32)
+    xt = to_torch(x, x_dtype, dev)
+    yt = empty_out(m, lin.out_dim, y_dtype, dev)
+    lin.forward(xt, yt, path=path)
+    torch.cuda.synchronize()
+    ref = reference_product(exact_inputs(x, x_dtype), deq, y_dtype)
+    got = yt.float().cpu().numpy()
+    assert np.all(np.isfinite(got))
+    return O.rel_l2(got, ref)
+
+
+# ---- dequantizer: bit-exact ---------------------------------------------------
+@pytest.mark.parametrize("fmt", ALL_FORMATS, ids=lambda f: dq.FORMAT_NAMES[f])
+def test_dequant_bit_exact(fmt, torch_dev):
+    import torch
+    n, k = 77, 512
+    lin, raw, scales, deq = _linear(fmt, n, k, seed=fmt)
+    out = torch.empty(n, k, dtype=torch.float32, device=torch_dev)
+    lin.dequantize(out)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), deq.view(np.uint32)), fmt
+    for td, rnd in ((torch.float16, O.round_f16), (torch.bfloat16, O.round_bf16)):
+        o2 = torch.empty(n, k, dtype=td, device=torch_dev)
+        lin.dequantize(o2)
+        assert np.array_equal(o2.float().cpu().numpy(), rnd(deq))
+
+
+@pytest.mark.parametrize("fmt", ALL_FORMATS, ids=lambda f: dq.FORMAT_NAMES[f])
+def test_export_round_trip(fmt, torch_dev):
+    n, k = 50, 256
+    lin, raw, scales, deq = _linear(fmt, n, k, seed=10 + fmt)
+    w, s = lin.export()
+    raw = np.asarray(raw)
+    if fmt == dq.FP8_ROW:
+        raw = np.where((raw & 0x7F) == 0x7F, 0, raw)  # NaN codes are stored as 0
+    if fmt == dq.NVFP4:
+        scales = np.where((scales & 0x7F) == 0x7F, 0, scales)
+    assert np.array_equal(w.reshape(-1).view(np.uint8), raw.reshape(-1).view(np.uint8))
+    if scales is not None:
+        assert np.array_equal(np.asarray(s).reshape(-1).view(np.uint8),
+                              np.asarray(scales).reshape(-1).view(np.uint8))
+
+
+# ---- quantizers: bit-exact -----------------------------------------------------
+@pytest.mark.parametrize("dense_dtype", [dq.F32, dq.BF16, dq.F16])
+@pytest.mark.parametrize("scale_dtype", [dq.F32, dq.BF16])
+def test_w8a16_quantizer_bit_exact(dense_dtype, scale_dtype, torch_dev):
+    rng = np.random.default_rng(3)
+    n, k = 37, 200
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    w[3] = 0.0
+    w[5, :3] = [0.5, -0.5, 1.5]
+    wt = to_torch(w, dense_dtype, torch_dev)
+    lin = dq.Linear.quantize(dq.W8A16, wt, scale_dtype=scale_dtype)
+    q, s = lin.export()
+    q_ref, s32, sb = O.w8a16_quantize(exact_inputs(w, dense_dtype))
+    assert np.array_equal(q, q_ref)
+    assert np.array_equal(np.asarray(s), sb if scale_dtype == dq.BF16 else s32)
+
+
+@pytest.mark.parametrize("fmt", [dq.Q8_0, dq.Q4_K, dq.FP8_BLOCK, dq.MXFP4],
+                         ids=lambda f: dq.FORMAT_NAMES[f])
+def test_block_quantizers_bit_exact(fmt, torch_dev):
+    rng = np.random.default_rng(4)
+    n, k = 40, 512
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    w[1, :256] = 0.0
+    w[2, :256] = 0.003
+    lin = dq.Linear.quantize(fmt, to_torch(w, dq.F32, torch_dev))
+    got_w, got_s = lin.export()
+    if fmt == dq.Q8_0:
+        ref_w, ref_s = O.q8_0_quantize(w), None
+    elif fmt == dq.Q4_K:
+        ref_w, ref_s = O.q4_k_quantize(w), None
+    elif fmt == dq.FP8_BLOCK:
+        ref_w, ref_s = O.fp8_block_quantize(w)
+    else:
+        ref_w, ref_s = O.mxfp4_quantize(w)
+    assert np.array_equal(got_w.reshape(-1), ref_w.reshape(-1))
+    if ref_s is not None:
+        assert np.array_equal(np.asarray(got_s).reshape(-1).view(np.uint8),
+                              np.asarray(ref_s).reshape(-1).view(np.uint8))
+
+
+# ---- decode GEMV ---------------------------------------------------------------
+@pytest.mark.parametrize("x_dtype", [dq.BF16, dq.F16, dq.F32], ids=["bf16", "f16", "f32"])
+@pytest.mark.parametrize("fmt", ALL_FORMATS, ids=lambda f: dq.FORMAT_NAMES[f])
+def test_gemv_parity(fmt, x_dtype, torch_dev):
+    n, k = 200, 512
+    lin, _, _, deq = _linear(fmt, n, k, seed=20 + fmt)
+    for m in (1, 3, 8, 16, 33):
+        y_dtype = dq.F16 if x_dtype == dq.F16 else dq.BF16
+        rel = _run(lin, deq, m, x_dtype, y_dtype, dq.PATH_GEMV, torch_dev, seed=m)
+        assert rel <= TOL_BF16, (dq.FORMAT_NAMES[fmt], m, rel)
+
+
+@pytest.mark.parametrize("fmt", ALL_FORMATS, ids=lambda f: dq.FORMAT_NAMES[f])
+def test_gemv_f32_output(fmt, torch_dev):
+    n, k = 64, 256
+    lin, _, _, deq = _linear(fmt, n, k, seed=30 + fmt)
+    rel = _run(lin, deq, 4, dq.BF16, dq.F32, dq.PATH_GEMV, torch_dev)
+    assert rel <= 1e-5, rel
+
+
+# ---- prefill GEMM (weight-only) --------------------------------------------------
+@pytest.mark.parametrize("x_dtype", [dq.BF16, dq.F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("fmt", ALL_FORMATS, ids=lambda f: dq.FORMAT_NAMES[f])
+def test_gemm_parity(fmt, x_dtype, torch_dev):
+    n, k = 300, 512
+    lin, _, _, deq = _linear(fmt, n, k, seed=40 + fmt)
+    for m in (65, 130):
+        y_dtype = dq.F16 if x_dtype == dq.F16 else dq.BF16
+        rel = _run(lin, deq, m, x_dtype, y_dtype, dq.PATH_GEMM, torch_dev, seed=m)
+        assert rel <= TOL_BF16, (dq.FORMAT_NAMES[fmt], m, rel)
+
+
+def test_gemm_f32_activations(torch_dev):
+    lin, _, _, deq = _linear(dq.W8A16, 96, 256, seed=50)
+    rel = _run(lin, deq, 70, dq.F32, dq.F32, dq.PATH_GEMM, torch_dev)
+    assert rel <= 1e-5, rel
+
+
+# ---- native fp8 / fp4 prefill --------------------------------------------------
+def _native_ref(fmt, x, deq):
+    if fmt == dq.FP8_BLOCK:
+        q, s = O.act_fp8_quantize(x)
+        xh = O.e4m3_to_f32(q) * s[:, None]
+    else:
+        p, s = O.act_mxfp4_quantize(x)
+        xh = O.mxfp4_dequant(p, s)
+    return O.round_bf16(O.matmul_f64(xh, deq).astype(np.float32))
+
+
+@pytest.mark.parametrize("fmt", [dq.FP8_BLOCK, dq.MXFP4], ids=["fp8_block", "mxfp4"])
+def test_native_prefill_parity(fmt, torch_dev):
+    import torch
+    n, k = 300, 640
+    lin, _, _, deq = _linear(fmt, n, k, seed=60 + fmt)
+    for m in (100, 256):
+        rng = np.random.default_rng(m)
+        x = O.round_bf16(rng.normal(0, 1, (m, k)).astype(np.float32))
+        xt = to_torch(x, dq.BF16, torch_dev)
+        yt = empty_out(m, n, dq.BF16, torch_dev)
+        lin.forward(xt, yt, path=dq.PATH_GEMM_NATIVE)
+        torch.cuda.synchronize()
+        rel = O.rel_l2(yt.float().cpu().numpy(), _native_ref(fmt, x, deq))
+        assert rel <= TOL_LOWP, (dq.FORMAT_NAMES[fmt], m, rel)
+
+
+# ---- local q8 (W8A8 decode): bit-exact ---------------------------------------
+@pytest.mark.parametrize("k", [96, 512])
+def test_local_q8_bit_exact(k, torch_dev):
+    import torch
+    rng = np.random.default_rng(k)
+    n = 300
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    q, s, _ = O.w8a16_quantize(w)
+    lin = dq.Linear.create(dq.W8A16, n, k, q, s, scale_dtype=dq.F32)
+    x = rng.normal(0, 1, (1, k)).astype(np.float32)
+    y = torch.empty(1, n, dtype=torch.float32, device=torch_dev)
+    lin.local_q8(to_torch(x, dq.F32, torch_dev), y)
+    torch.cuda.synchronize()
+    want = O.local_q8_forward(x, q, s)
+    assert np.array_equal(y.cpu().numpy().ravel(), want)
+
+
+def test_local_q8_rejects_prefill(torch_dev):
+    lin, _, _, _ = _linear(dq.W8A16, 16, 64, scale_dtype=dq.F32)
+    import torch
+    x = torch.zeros(2, 64, device=torch_dev)
+    y = torch.zeros(2, 16, device=torch_dev)
+    with pytest.raises(dq.DialqError, match="expects decode"):
+        lin.local_q8(x, y)
+
+
+# ---- edge cases -------------------------------------------------------------
+def test_zero_rows_is_noop(torch_dev):
+    import torch
+    lin, _, _, _ = _linear(dq.W8A16, 32, 64)
+    x = torch.zeros(0, 64, dtype=torch.bfloat16, device=torch_dev)
+    y = torch.zeros(0, 32, dtype=torch.bfloat16, device=torch_dev)
+    lin.forward(x, y, rows=0)
+
+
+@pytest.mark.parametrize("fmt", [dq.W8A16, dq.FP8_ROW], ids=["w8a16", "fp8_row"])
+def test_tiny_and_ragged_shapes(fmt, torch_dev):
+    for n, k in ((1, 8), (17, 72), (37, 64), (129, 136)):
+        lin, _, _, deq = _linear(fmt, n, k, seed=n)
+        for m in (1, 5, 70):
+            rel = _run(lin, deq, m, dq.BF16, dq.F32, dq.PATH_AUTO, torch_dev, seed=m)
+            assert rel <= 1e-5, (n, k, m, rel)
+
+
+def test_host_io_forward(torch_dev):
+    lin, _, _, deq = _linear(dq.Q8_0, 64, 256)
+    x = np.random.default_rng(0).normal(size=(3, 256)).astype(np.float32)
+    y = np.empty((3, 64), np.float32)
+    lin.forward(x, y)
+    assert O.rel_l2(y, O.matmul_f64(x, deq)) < 1e-5
+
+
+def test_resident_bytes_reference_formulas(torch_dev):
+    # cuda_quant.rs:360-371 and worker_w8a16.rs:351
+    lin, _, _, _ = _linear(dq.NVFP4, 48, 64)
+    assert lin.resident_bytes() == 48 * 64 // 2 + 48 * 64 // 16 + 4
+    lin, _, _, _ = _linear(dq.FP8_ROW, 48, 64)
+    assert lin.resident_bytes() == 48 * 64 + 48 * 4
+    lin, _, _, _ = _linear(dq.W8A16, 48, 64, scale_dtype=dq.F32)
+    assert lin.resident_bytes() == 48 * 64 + 48 * 4

@@ -1,0 +1,239 @@
+"""Pin the oracle's format codecs with closed forms, independent library
+routines and invariants that a dropped term, a wrong index, a wrong rounding
+mode or a transposed operand would break."""
+import numpy as np
+import pytest
+import torch
+
+
+def test_w8a16_quantizer_invariants(O):
+    rng = np.random.default_rng(0)
+    w = np.zeros((6, 64), np.float32)
+    w[1, :4] = [127.0, 2.5, -2.5, 0.5]          # scale exactly 1.0 -> ties visible
+    w[2] = rng.normal(0, 0.02, 64)
+    w[3] = rng.normal(0, 1.0, 64) * 1e-30       # tiny but nonzero
+    w[4, 7] = -3.0                               # single spike
+    w[5] = np.linspace(-1, 1, 64)
+    q, s, sb = O.w8a16_quantize(w)
+    # zero row -> scale 1 and zero codes (worker_w8a16.rs:336)
+    assert s[0] == 1.0 and not q[0].any()
+    # half-away-from-zero rounding (Rust f32::round), not numpy's half-to-even
+    assert s[1] == 1.0
+    assert list(q[1, :4]) == [127, 3, -3, 1]
+    for r in range(2, 6):
+        amax = np.max(np.abs(w[r]))
+        assert s[r] == np.float32(amax / np.float32(127.0))
+        assert np.abs(q[r]).max() == 127
+        assert q[r, np.argmax(np.abs(w[r]))] == np.sign(w[r, np.argmax(np.abs(w[r]))]) * 127
+        err = np.abs(w[r].astype(np.float64) - q[r].astype(np.float64) * s[r])
+        assert np.all(err <= s[r] * 0.5 * (1 + 1e-5) + 1e-45)
+    # bf16 storage of the same scale, rounded by torch (RNE)
+    ref = torch.from_numpy(s).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(sb, ref)
+    # dequant: q * scale, both widths
+    d = O.w8a16_dequant(q, s)
+    assert np.array_equal(d, q.astype(np.float32) * s[:, None])
+    d2 = O.w8a16_dequant(q, sb)
+    assert np.array_equal(d2, q.astype(np.float32) * O.bf16_bits_to_f32(sb)[:, None])
+
+
+Q8_0_DT = np.dtype([("d", "<f2"), ("qs", "i1", 32)])
+
+
+def test_q8_0_block_layout_and_rounding(O):
+    rng = np.random.default_rng(1)
+    w = rng.normal(0, 0.02, (3, 128)).astype(np.float32)
+    w[0, :32] = 0.0
+    w[1, :4] = [127.0, 0.5, -0.5, 1.5]           # d = 1 exactly: ties away from zero
+    blocks = O.q8_0_quantize(w)
+    assert blocks.shape == (3, 4 * 34)
+    b = blocks.reshape(3, 4, 34).copy().view(Q8_0_DT).reshape(3, 4)
+    assert b["d"][0, 0] == 0 and not b["qs"][0, 0].any()
+    assert list(b["qs"][1, 0, :4]) == [127, 1, -1, 2]
+    for r in range(3):
+        for k in range(4):
+            x = w[r, 32 * k:32 * k + 32]
+            amax = np.abs(x).max()
+            d32 = np.float32(amax / np.float32(127.0))
+            assert b["d"][r, k] == np.float16(d32)          # numpy RNE to f16
+            if amax > 0:
+                assert np.abs(b["qs"][r, k]).max() == 127
+                assert np.all(np.abs(x - b["qs"][r, k] * d32) <= d32 * 0.5 * (1 + 1e-5))
+    deq = O.q8_0_dequant(blocks, 3, 128)
+    want = b["qs"].astype(np.float32) * b["d"].astype(np.float32)[..., None]
+    assert np.array_equal(deq, want.reshape(3, 128))
+
+
+def _pack_q4k_scales(sc, m):
+    """GGUF Q4_K 6-bit scale packing, written from the format definition
+    (llama.cpp block_q4_K): bytes 0-3 hold sc[0..3] with sc[4..7]>>4 in bits
+    6-7; bytes 4-7 hold m[0..3] with m[4..7]>>4 in bits 6-7; bytes 8-11 hold
+    the low nibbles of sc[4..7] and m[4..7]."""
+    out = np.zeros(12, np.uint8)
+    for j in range(4):
+        out[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        out[j + 4] = m[j] | ((m[j + 4] >> 4) << 6)
+        out[j + 8] = (sc[j + 4] & 15) | ((m[j + 4] & 15) << 4)
+    return out
+
+
+def test_q4_k_dequant_hand_built_block(O):
+    rng = np.random.default_rng(2)
+    sc = rng.integers(0, 64, 8)
+    m = rng.integers(0, 64, 8)
+    sc[5], m[6] = 63, 63                      # exercise all six bits
+    q = rng.integers(0, 16, 256)
+    d, dmin = np.float16(0.0123), np.float16(0.00456)
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([d]).view(np.uint8)
+    blk[2:4] = np.array([dmin]).view(np.uint8)
+    blk[4:16] = _pack_q4k_scales(sc, m)
+    # value p of the super-block: 64-group i = p // 64; first 32 values are the
+    # low nibbles of qs[32i .. 32i+32), the next 32 the high nibbles
+    qs = np.zeros(128, np.uint8)
+    for p in range(256):
+        i, within = divmod(p, 64)
+        byte = 32 * i + (within % 32)
+        qs[byte] |= q[p] << (4 if within >= 32 else 0)
+    blk[16:] = qs
+    for j in range(8):
+        s_, m_ = np.zeros(1, np.uint8), np.zeros(1, np.uint8)
+        import ctypes
+        a, b = ctypes.c_uint8(), ctypes.c_uint8()
+        O.lib().or_q4_k_scale_min(j, blk[4:16].ctypes.data_as(ctypes.c_void_p), ctypes.byref(a), ctypes.byref(b))
+        assert (a.value, b.value) == (sc[j], m[j])
+    deq = O.q4_k_dequant(blk[None, :], 1, 256)[0]
+    df, mf = np.float32(d), np.float32(dmin)
+    want = np.empty(256, np.float32)
+    for p in range(256):
+        j = p // 32
+        want[p] = np.float32(df * np.float32(sc[j])) * np.float32(q[p]) - np.float32(mf * np.float32(m[j]))
+    assert np.array_equal(deq, want)
+
+
+def test_q4_k_quantizer_round_trip(O):
+    # Parity unpinned for the exact bytes (candle's quantizer is not vendored);
+    # check the codec invariants and the round-trip error.
+    rng = np.random.default_rng(3)
+    w = rng.normal(0, 0.02, (8, 512)).astype(np.float32)
+    w[0, :256] = 0.0
+    w[1, :256] = 0.01                          # constant block
+    blocks = O.q4_k_quantize(w)
+    assert blocks.shape == (8, 2 * 144)
+    deq = O.q4_k_dequant(blocks, 8, 512)
+    assert np.all(deq[0, :256] == 0.0)
+    rel = np.linalg.norm(deq[2:] - w[2:]) / np.linalg.norm(w[2:])
+    assert rel < 0.12, rel
+    # each stored d / dmin is the f16 of max_scale/63, max_min/63 => some 6-bit
+    # scale equals 63 in every nonzero block
+    for r in range(2, 8):
+        for b in range(2):
+            blk = blocks[r, 144 * b:144 * (b + 1)]
+            import ctypes
+            scs = []
+            for j in range(8):
+                a, c = ctypes.c_uint8(), ctypes.c_uint8()
+                O.lib().or_q4_k_scale_min(j, blk[4:16].ctypes.data_as(ctypes.c_void_p), ctypes.byref(a), ctypes.byref(c))
+                scs.append(a.value)
+            assert max(scs) == 63
+
+
+def test_fp8_block_quantizer_matches_torch_cast(O):
+    rng = np.random.default_rng(4)
+    n, k = 200, 300                             # ragged: partial 128-blocks
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    w[:128, :128] = 0.0                         # zero block -> scale 1
+    q, s = O.fp8_block_quantize(w)
+    assert s.shape == (2, 3) and s[0, 0] == 1.0
+    for bn in range(2):
+        for bk in range(3):
+            blk = w[bn * 128:(bn + 1) * 128, bk * 128:(bk + 1) * 128]
+            amax = np.abs(blk).max()
+            if amax == 0:
+                continue
+            sc = np.float32(amax / np.float32(448.0))
+            assert s[bn, bk] == sc
+            inv = np.float32(1.0) / sc
+            ref = torch.from_numpy((blk * inv).astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+            got = q[bn * 128:(bn + 1) * 128, bk * 128:(bk + 1) * 128]
+            assert np.array_equal(O.e4m3_to_f32(got), O.e4m3_to_f32(ref))
+            assert np.abs(O.e4m3_to_f32(got)).max() == 448.0
+    deq = O.fp8_block_dequant(q, s)
+    want = O.e4m3_to_f32(q) * np.repeat(np.repeat(s, 128, 0), 128, 1)[:n, :k]
+    assert np.array_equal(deq, want)
+
+
+def test_mxfp4_quantizer_closed_form(O):
+    rng = np.random.default_rng(5)
+    w = rng.normal(0, 0.02, (4, 96)).astype(np.float32)
+    w[0, :32] = 0.0
+    w[1, :32] = np.linspace(-6, 6, 32)          # amax 6 -> shared exp 0
+    packed, scales = O.mxfp4_quantize(w)
+    assert packed.shape == (4, 48) and scales.shape == (4, 3)
+    assert scales[0, 0] == 0                     # zero block: shared = -127
+    assert scales[1, 0] == 127
+    for r in range(4):
+        for b in range(3):
+            x = w[r, 32 * b:32 * b + 32]
+            amax = np.abs(x).max()
+            if amax == 0:
+                continue
+            shared = np.frexp(np.float32(amax))[1] - 1 - 2
+            assert scales[r, b] == shared + 127
+            codes = packed[r, 16 * b:16 * b + 16]
+            lo, hi = codes & 15, codes >> 4
+            got = np.empty(32, np.uint8)
+            got[0::2], got[1::2] = lo, hi
+            want = O.f32_to_e2m1(np.ldexp(x, -shared).astype(np.float32))
+            assert np.array_equal(O.e2m1_to_f32(got), O.e2m1_to_f32(want))
+    deq = O.mxfp4_dequant(packed, scales)
+    codes = np.empty((4, 96), np.uint8)
+    codes[:, 0::2], codes[:, 1::2] = packed & 15, packed >> 4
+    want = O.e2m1_to_f32(codes) * np.repeat(2.0 ** (scales.astype(np.float64) - 127), 32, 1)
+    assert np.array_equal(deq, want.astype(np.float32))
+
+
+def test_act_fp8_per_token(O):
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 1, (5, 64)).astype(np.float32)
+    x[2] = 0
+    q, s = O.act_fp8_quantize(x)
+    assert s[2] == 1.0 and not q[2].any()
+    for r in (0, 1, 3, 4):
+        sc = np.float32(np.abs(x[r]).max() / np.float32(448.0))
+        assert s[r] == sc
+        ref = torch.from_numpy(x[r] * (np.float32(1.0) / sc)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert np.array_equal(O.e4m3_to_f32(q[r]), O.e4m3_to_f32(ref))
+
+
+def test_matmul_oracle_matches_numpy(O):
+    rng = np.random.default_rng(7)
+    x = rng.normal(size=(3, 40)).astype(np.float32)
+    w = rng.normal(size=(7, 40)).astype(np.float32)
+    y = O.matmul_f64(x, w)
+    assert np.allclose(y, x.astype(np.float64) @ w.astype(np.float64).T, rtol=1e-12, atol=1e-12)
+    # a transposed operand would fail here
+    assert y.shape == (3, 7)
+
+
+def test_w8a16_linear_oracle(O):
+    rng = np.random.default_rng(8)
+    w = rng.normal(0, 0.02, (9, 64)).astype(np.float32)
+    x = rng.normal(size=(2, 64)).astype(np.float32)
+    q, s, sb = O.w8a16_quantize(w)
+    y = O.w8a16_linear(x, q, s)
+    ref = (x.astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64)
+    assert np.allclose(y, ref, rtol=1e-5, atol=1e-7)
+
+
+def test_local_q8_integer_dot(O):
+    rng = np.random.default_rng(9)
+    w = rng.normal(0, 0.02, (33, 96)).astype(np.float32)
+    x = rng.normal(size=96).astype(np.float32)
+    q, s, _ = O.w8a16_quantize(w)
+    y = O.local_q8_forward(x, q, s)
+    xs = np.float32(np.abs(x).max() / np.float32(127.0))
+    xq = np.clip(np.sign(x * (np.float32(1) / xs)) * np.floor(np.abs(x * (np.float32(1) / xs)) + 0.5), -127, 127)
+    acc = q.astype(np.int64) @ xq.astype(np.int64)
+    want = (acc.astype(np.float32) * s) * xs
+    assert np.array_equal(y, want.astype(np.float32))
