@@ -84,6 +84,8 @@ struct Linear {
   int64_t n_strips = 0, k_chunks = 0, nbk = 0;
   DevBuf tiles, aux, row_scale, block_scale;
   DevBuf scratch;  // activation codes for native prefill / local q8
+  DevBuf gemv_ws;  // stream-K partials of the decode GEMV
+  DevBuf gemv_cnt; // per-strip arrival counters (zero between calls)
   std::mutex scratch_mu;
   float global = 1.0f;
 
@@ -207,6 +209,8 @@ Linear *alloc_linear(const dialq_linear_desc &d, int device) {
   if (d.format == DIALQ_FORMAT_NVFP4) {
     L->global = (d.flags & DIALQ_FLAG_GLOBAL_IS_DIVISOR) ? 1.0f / d.global_scale : d.global_scale;
   }
+  L->gemv_cnt.alloc((size_t)L->n_strips * sizeof(int));
+  hip_check(hipMemset(L->gemv_cnt.p, 0, L->gemv_cnt.n), "hipMemset");
   return L;
 }
 
@@ -248,7 +252,14 @@ void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, i
     else path = DIALQ_PATH_GEMM;
   }
   if (path == DIALQ_PATH_GEMV) {
-    hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, st), "GEMV launch");
+    if (L->tiles.n >= ((size_t)1 << 31))
+      fail("decode kernel addresses weights with 32-bit offsets: %zu resident bytes exceed 2 GiB; split the "
+           "output dimension", L->tiles.n);
+    std::lock_guard<std::mutex> lock(L->scratch_mu);
+    size_t need = gemv_workspace_bytes(w, rows);
+    if (L->gemv_ws.n < need) L->gemv_ws.alloc(need);
+    hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, (float *)L->gemv_ws.p, (int *)L->gemv_cnt.p, st),
+              "GEMV launch");
   } else if (path == DIALQ_PATH_GEMM) {
     hip_check(launch_gemm(w, x, x_dtype, rows, y, y_dtype, st), "GEMM launch");
   } else if (path == DIALQ_PATH_GEMM_NATIVE) {
@@ -464,7 +475,8 @@ uint64_t dialq_linear_resident_bytes(const void *linear) {
 uint64_t dialq_linear_device_bytes(const void *linear) {
   const Linear *L = (const Linear *)linear;
   if (!L) return 0;
-  return L->tiles.n + L->aux.n + L->row_scale.n + L->block_scale.n + L->scratch.n;
+  return L->tiles.n + L->aux.n + L->row_scale.n + L->block_scale.n + L->scratch.n + L->gemv_ws.n +
+         L->gemv_cnt.n;
 }
 
 int dialq_linear_describe(const void *linear, dialq_linear_desc *desc) {

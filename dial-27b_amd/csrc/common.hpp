@@ -112,10 +112,11 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t code) {
   return (code & 0x80u) ? -v : v;
 }
 
+// E2M1 table of quant.rs:16-18 (code 8 decodes to +0.0 there).
 __device__ __forceinline__ float e2m1_to_f32(uint32_t code) {
-  const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
-  float v = mag[code & 7u];
-  return (code & 8u) ? -v : v;
+  const float tab[16] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
+                         0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+  return tab[code & 15u];
 }
 
 __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {

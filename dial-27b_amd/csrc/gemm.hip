@@ -74,9 +74,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
     }
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-      int64_t s = s0 + j;
-      if (s < w.n_strips) wpre[j] = load_tile<FMT>(w.tiles, s * kc + c, lane);
-      else wpre[j] = RawTile{(u32x4){0, 0, 0, 0}, (u32x4){0, 0, 0, 0}};
+      const int s = (int)(s0 + j < w.n_strips ? s0 + j : w.n_strips - 1);
+      const uint8_t *tbase = w.tiles + (size_t)s * kc * (64 * T::LANE) + lane * T::LANE;
+      wpre[j] = load_tile_full<FMT>(w, tbase, s, (int)c, lane);
     }
   };
 
@@ -98,10 +98,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 
     BOps<FMT> o[NS];
 #pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      int64_t s = s0 + j < w.n_strips ? s0 + j : w.n_strips - 1;
-      o[j] = make_bops<FMT>(cur[j], w, s, c, lane);
-    }
+    for (int j = 0; j < NS; ++j) o[j] = make_bops<FMT>(cur[j]);
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
       XOp<ACT> xo[T::NX];
@@ -218,7 +215,7 @@ __global__ __launch_bounds__(256) void k_gemm_fp8(NativeParams p) {
     for (int j = 0; j < NS; ++j) {
       int64_t s = s0 + j;
       if (s < w.n_strips) wpre[j] = load_tile<DIALQ_FORMAT_FP8_BLOCK>(w.tiles, s * kc + c, lane);
-      else wpre[j] = RawTile{(u32x4){0, 0, 0, 0}, (u32x4){0, 0, 0, 0}};
+      else wpre[j].a = wpre[j].b = (u32x4){0, 0, 0, 0};
     }
   };
 
@@ -317,7 +314,7 @@ __global__ __launch_bounds__(256) void k_gemm_mxfp4(NativeParams p) {
     for (int j = 0; j < NS; ++j) {
       int64_t s = s0 + j;
       if (s < w.n_strips) wpre[j] = load_tile<DIALQ_FORMAT_MXFP4>(w.tiles, s * kc + c, lane);
-      else wpre[j] = RawTile{(u32x4){0, 0, 0, 0}, (u32x4){0, 0, 0, 0}};
+      else wpre[j].a = wpre[j].b = (u32x4){0, 0, 0, 0};
     }
   };
 

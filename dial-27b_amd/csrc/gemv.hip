@@ -1,5 +1,5 @@
-// Decode GEMV for quantized weights, gfx950: rows M = 1..16 per 16-row
-// group, up to 4 groups (64 rows) per launch.
+// Decode GEMV for quantized weights, gfx950: up to 16 rows of x per pass
+// (8 for the Q4_K row-packed policy); larger M runs several passes.
 //
 // Reference kernels replaced: dial_w8a16_decode_f16 (worker_w8a16.rs:146-184),
 // dial_nvfp4_decode_f16 / dial_fp8_decode_f16 (cuda_quant.rs:67-133) and
@@ -10,9 +10,23 @@
 // operands (tile_ops.hpp) and lets v_mfma_f32_16x16x32_bf16 accumulate; the
 // weight bytes are read exactly once per launch.
 //
-// A workgroup owns one 16-row strip.  Its W waves take interleaved k chunks
-// (wave w: chunks w, w+W, ...; U chunks in flight per wave) and reduce
-// through LDS at the end in a fixed order, so results are deterministic.
+// Work split: the n_strips * k_chunks tiles, in resident (strip-major)
+// order, are cut into G equal contiguous ranges, one per workgroup (stream-K
+// over the whole matrix, so every workgroup streams the same number of
+// bytes whatever the strip count).  The 4 waves of a workgroup take
+// interleaved tiles of its range; each keeps a register ring of U slots --
+// one weight tile, its scales and the activation operands it multiplies, all
+// fetched with raw buffer loads whose out-of-range offsets return zeros in
+// hardware (no branch, no traffic) -- and refills a slot as soon as it has
+// been multiplied, so loads stay in flight and the loop carries no memory
+// round trip and no barrier.  When a wave moves on to the next strip it
+// parks its accumulator for the finished one in LDS (one slot per strip and
+// wave).  After the range is done the waves add the parked slots of each
+// strip in wave order; a strip that lies wholly inside the range is written
+// out, one shared with neighbouring ranges (at most the first and the last)
+// leaves an f32 partial in the workspace, and the last contributor to arrive
+// (per-strip counter, reset by that contributor) adds the partials in range
+// order -- deterministic.
 #include "tile_ops.hpp"
 
 namespace dialq {
@@ -24,118 +38,431 @@ struct GemvParams {
   int64_t M;       // total rows of x / y
   int64_t m_base;  // first row handled by this launch
   int y_dtype;
+  int G;           // workgroups (tile ranges)
+  float *ws;       // [G][2][mrows][16] partials of shared strips
+  int *cnt;        // [n_strips] arrival counters (zero between launches)
 };
 
-template <int FMT, int ACT, int MG, int U>
-__global__ __launch_bounds__(1024) void k_gemv(GemvParams p) {
-  extern __shared__ float red[];
+constexpr int kGemvWaves = 4;  // waves per workgroup
+
+// ---------------------------------------------------------------------------
+// Per-format ring slot (policy).  fill() issues every global load of one
+// element unconditionally (buffer loads; `valid` = false turns them into
+// zero-returning out-of-range loads); compute() multiplies a filled slot
+// into the accumulator.
+// ---------------------------------------------------------------------------
+template <int FMT, int ACT>
+struct GenericPolicy {
   typedef FmtTraits<FMT> T;
-  const WeightView &w = p.w;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int W = blockDim.x >> 6;
-  const int g = lane >> 4, r = lane & 15;
-  const int64_t s = blockIdx.x;
-  const int64_t kc = w.k_chunks;
-
-  f32x4 acc[MG];
+  static constexpr int XACT = ACT;
+  static constexpr int NV = 4;  // accumulator values per lane
+  struct Slot {
+    RawTile t;
+    XRaw<ACT> x[T::NX];
+  };
+  struct Acc {
+    f32x4 v;
+  };
+  static __device__ __forceinline__ void zero(Acc &a) { a.v = (f32x4){0.0f, 0.0f, 0.0f, 0.0f}; }
+  static __device__ __forceinline__ void fill(Slot &sl, const GemvParams &p, rsrc_t rt, rsrc_t ra, rsrc_t rx,
+                                              int s, int c, bool valid, int lane) {
+    const WeightView &w = p.w;
+    const int r = lane & 15, g = lane >> 4;
+    const uint32_t tidx = (uint32_t)s * (uint32_t)w.k_chunks + (uint32_t)c;
+    const uint32_t off = valid ? tidx * (64 * T::LANE) + lane * T::LANE : kOOB;
+    sl.t.a = bload16(rt, off);
+    sl.t.b = (u32x4){0, 0, 0, 0};
+    if constexpr (T::LANE == 32) sl.t.b = bload16(rt, valid ? off + 16 : kOOB);
+    sl.t.s0 = 0;
+    sl.t.hdr = (u32x4){0, 0, 0, 0};
+    if constexpr (FMT == DIALQ_FORMAT_Q8_0) sl.t.s0 = bload4(ra, valid ? tidx * 64 + r * 4 : kOOB);
+    else if constexpr (FMT == DIALQ_FORMAT_Q4_K) sl.t.hdr = bload16(ra, valid ? tidx * 256 + r * 16 : kOOB);
+    else if constexpr (FMT == DIALQ_FORMAT_NVFP4) sl.t.s0 = bload2(ra, valid ? tidx * 128 + r * 8 + 2 * g : kOOB);
+    else if constexpr (FMT == DIALQ_FORMAT_MXFP4) sl.t.s0 = bload1(ra, valid ? tidx * 64 + r * 4 + g : kOOB);
+    else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK)
+      sl.t.s0 = bload4(ra, valid ? ((uint32_t)((s * 16) / 128) * (uint32_t)w.nbk + (uint32_t)c) * 4 : kOOB);
+    const int K = (int)w.K;
 #pragma unroll
-  for (int mg = 0; mg < MG; ++mg) acc[mg] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-
-  for (int64_t c0 = wave; c0 < kc; c0 += (int64_t)W * U) {
-    RawTile tl[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int64_t c = c0 + (int64_t)u * W;
-      if (c < kc) tl[u] = load_tile<FMT>(w.tiles, s * kc + c, lane);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int64_t c = c0 + (int64_t)u * W;
-      if (c < kc) {
-        XOp<ACT> xo[MG][T::NX];
-#pragma unroll
-        for (int mg = 0; mg < MG; ++mg)
-#pragma unroll
-          for (int t = 0; t < T::NX; ++t)
-            xo[mg][t] = load_x8<ACT>(p.x, p.m_base + mg * 16 + r, c * T::CHUNK + T::xk(t, g), p.M, w.K);
-        BOps<FMT> o = make_bops<FMT>(tl[u], w, s, c, lane);
-#pragma unroll
-        for (int mg = 0; mg < MG; ++mg) bops_mac<FMT, ACT>(o, xo[mg], acc[mg]);
-      }
+    for (int t = 0; t < T::NX; ++t) {
+      const int k = c * T::CHUNK + T::xk(t, g);
+      const uint32_t xo = ((uint32_t)r * (uint32_t)K + (uint32_t)k) * ActTraits<ACT>::BYTES;
+      sl.x[t] = xraw_load<ACT>(rx, (valid && k < K) ? xo : kOOB);
     }
   }
+  static __device__ __forceinline__ void compute(const Slot &sl, Acc &a) {
+    XOp<ACT> xo[T::NX];
+#pragma unroll
+    for (int t = 0; t < T::NX; ++t) xo[t] = xraw_to_op<ACT>(sl.x[t]);
+    bops_mac<FMT, ACT>(make_bops<FMT>(sl.t), xo, a.v);
+  }
+  static __device__ __forceinline__ void values(const Acc &a, float (&v)[NV], int (&mrow)[NV], int lane) {
+    const int g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a.v[i];
+      mrow[i] = 4 * g + i;
+    }
+  }
+};
 
-  // cross-wave reduction in a fixed order
-  float *mine = red + (size_t)wave * 64 * 4 * MG;
+// Q4_K, M <= 4*RP: rows of the A operand are (row m' = rho/4, sub-block
+// jj = rho%4) pairs, so MFMA t (sub-block t of the super-block) writes
+// partial dot products D_t[m'][n] into accumulator rows 4m' + t%4 (the other
+// lanes feed zeros), and every lane ends up owning one output (m' = l/16) and
+// four sub-blocks (i = 0..3, plus 4..7 in the second accumulator): the
+// per-sub-block scales cost 4 FMAs per accumulator instead of 4 per row group
+// per sub-block.  Weights enter as bf16(128 + q); the offset and the dmin*m
+// term use the per-sub-block activation sums X_t[m'] from a second MFMA with
+// a ones operand:  y += s1*D - (128*s1 + dmin*m)*X.  RP passes cover rows
+// 4*pass + m'.
+template <int ACT, int RP>
+struct Q4kRowsPolicy {
+  static constexpr int XACT = ACT;
+  static constexpr int NV = RP;
+  struct Slot {
+    RawTile t;
+    XRaw<ACT> x[RP][2];  // sub-blocks jj and jj + 4 of row 4q + mq
+  };
+  struct Acc {
+    float v[RP];
+  };
+  static __device__ __forceinline__ void zero(Acc &a) {
 #pragma unroll
-  for (int mg = 0; mg < MG; ++mg)
+    for (int q = 0; q < RP; ++q) a.v[q] = 0.0f;
+  }
+  static __device__ __forceinline__ void fill(Slot &sl, const GemvParams &p, rsrc_t rt, rsrc_t ra, rsrc_t rx,
+                                              int s, int c, bool valid, int lane) {
+    const WeightView &w = p.w;
+    const int r = lane & 15, g = lane >> 4, mq = r >> 2, jj = r & 3;
+    const uint32_t tidx = (uint32_t)s * (uint32_t)w.k_chunks + (uint32_t)c;
+    const uint32_t off = valid ? tidx * 2048 + lane * 32 : kOOB;
+    sl.t.a = bload16(rt, off);
+    sl.t.b = bload16(rt, valid ? off + 16 : kOOB);
+    sl.t.s0 = 0;
+    sl.t.hdr = bload16(ra, valid ? tidx * 256 + r * 16 : kOOB);
+    const int K = (int)w.K;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mine[(mg * 4 + i) * 64 + lane] = acc[mg][i];
-  __syncthreads();
-  if (wave == 0) {
-    const int64_t n = s * 16 + r;
-    const float scale = epilogue_scale<FMT>(w, n);
+    for (int q = 0; q < RP; ++q)
 #pragma unroll
-    for (int mg = 0; mg < MG; ++mg)
+      for (int h = 0; h < 2; ++h) {
+        const int k = c * 256 + 32 * (jj + 4 * h) + 8 * g;
+        const uint32_t xo = ((uint32_t)(4 * q + mq) * (uint32_t)K + (uint32_t)k) * ActTraits<ACT>::BYTES;
+        sl.x[q][h] = xraw_load<ACT>(rx, (valid && k < K) ? xo : kOOB);
+      }
+  }
+  static __device__ __forceinline__ void compute(const Slot &sl, Acc &acc) {
+    const int lane = threadIdx.x & 63, jj = lane & 3;
+    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    const u32x4 hd = sl.t.hdr;
+    const float d = f16_bits_to_f32(hd[0] & 0xffffu), dmin = f16_bits_to_f32(hd[0] >> 16);
+    const uint32_t sc_lo = hd[1] & 0x3f3f3f3fu;                                   // sc[0..3]
+    const uint32_t m_lo = hd[2] & 0x3f3f3f3fu;                                    // m[0..3]
+    const uint32_t sc_hi = (hd[3] & 0x0f0f0f0fu) | ((hd[1] >> 2) & 0x30303030u);  // sc[4..7]
+    const uint32_t m_hi = ((hd[3] >> 4) & 0x0f0f0f0fu) | ((hd[2] >> 2) & 0x30303030u);
+    const uint32_t qd[8] = {sl.t.a[0], sl.t.a[1], sl.t.a[2], sl.t.a[3], sl.t.b[0], sl.t.b[1], sl.t.b[2], sl.t.b[3]};
+#pragma unroll
+    for (int q = 0; q < RP; ++q) {
+      const XOp<ACT> xa = xraw_to_op<ACT>(sl.x[q][0]), xb = xraw_to_op<ACT>(sl.x[q][1]);
+      f32x4 cq[2] = {zero, zero}, cx[2] = {zero, zero};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const u32x4 wb = nib8_to_bf16_off128(qd[2 * (t >> 1)], qd[2 * (t >> 1) + 1], (t & 1) ? 4 : 0);
+        const bool on = (jj == (t & 3));
+        const XOp<ACT> &src = (t < 4) ? xa : xb;
+        XOp<ACT> a;
+        a.hi = on ? src.hi : (u32x4){0, 0, 0, 0};
+        if constexpr (ActTraits<ACT>::PARTS == 2) a.lo = on ? src.lo : (u32x4){0, 0, 0, 0};
+        cq[t >> 2] = mfma_x<ACT>(a, wb, cq[t >> 2]);
+        cx[t >> 2] = mfma_x<ACT>(a, ones, cx[t >> 2]);
+      }
+      // lane (g, r) holds rows 4g+i: m' = g, sub-block i (+4 in [1])
+      float sum = acc.v[q];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float v = 0.0f;
-        for (int ww = 0; ww < W; ++ww) v += red[(size_t)ww * 64 * 4 * MG + (mg * 4 + i) * 64 + lane];
-        int64_t m = p.m_base + mg * 16 + g * 4 + i;
-        if (m < p.M && n < w.N) store_out(p.y, m * w.N + n, p.y_dtype, v * scale);
+        const float s1a = d * (float)((sc_lo >> (8 * i)) & 0xffu);
+        const float s2a = __builtin_fmaf(128.0f, s1a, dmin * (float)((m_lo >> (8 * i)) & 0xffu));
+        const float s1b = d * (float)((sc_hi >> (8 * i)) & 0xffu);
+        const float s2b = __builtin_fmaf(128.0f, s1b, dmin * (float)((m_hi >> (8 * i)) & 0xffu));
+        sum = __builtin_fmaf(s1a, cq[0][i], __builtin_fmaf(-s2a, cx[0][i], sum));
+        sum = __builtin_fmaf(s1b, cq[1][i], __builtin_fmaf(-s2b, cx[1][i], sum));
       }
+      acc.v[q] = sum;
+    }
   }
+  static __device__ __forceinline__ void values(const Acc &a, float (&v)[NV], int (&mrow)[NV], int lane) {
+    const int g = lane >> 4;
+#pragma unroll
+    for (int q = 0; q < RP; ++q) {
+      v[q] = a.v[q];
+      mrow[q] = 4 * q + g;
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// The GEMV kernel.  LDS holds part[j][wave][m][16]: the accumulator of wave
+// `wave` for the j-th strip of the range, rows m < mrows only.
+// ---------------------------------------------------------------------------
+template <typename Pol>
+__device__ __forceinline__ void park(float *part, int j, int wave, int mrows, const typename Pol::Acc &acc) {
+  constexpr int NV = Pol::NV;
+  const int lane = threadIdx.x & 63, r = lane & 15;
+  float v[NV];
+  int mrow[NV];
+  Pol::values(acc, v, mrow, lane);
+  float *dst = part + (size_t)(j * kGemvWaves + wave) * mrows * 16;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (mrow[i] < mrows) dst[mrow[i] * 16 + r] = v[i];
+}
+
+template <int FMT, typename Pol, int U>
+__global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
+  extern __shared__ float part[];
+  constexpr int W = kGemvWaves;
+  const WeightView &w = p.w;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = blockIdx.x;
+  const int kc = (int)w.k_chunks;
+  const int64_t total = w.n_strips * w.k_chunks;
+  const int lo = (int)(((int64_t)b * total) / p.G), hi = (int)(((int64_t)(b + 1) * total) / p.G);
+  const int s_first = lo / kc;
+  const int nseg = (hi > lo) ? (hi - 1) / kc - s_first + 1 : 0;
+  const int mrows = (int)((p.M - p.m_base) < 16 ? (p.M - p.m_base) : 16);
+  const int slot_floats = mrows * 16;
+
+  // each wave clears its own parking slots (a wave may skip a strip)
+  for (int j = 0; j < nseg; ++j)
+    for (int e = lane; e < slot_floats; e += 64) part[(size_t)(j * W + wave) * slot_floats + e] = 0.0f;
+
+  rsrc_t rt = make_rsrc(w.tiles, (uint32_t)(total * 64 * FmtTraits<FMT>::LANE));
+  rsrc_t ra = rt;
+  if constexpr (FMT == DIALQ_FORMAT_Q8_0 || FMT == DIALQ_FORMAT_MXFP4)
+    ra = make_rsrc(w.aux, (uint32_t)(total * 64));
+  else if constexpr (FMT == DIALQ_FORMAT_Q4_K)
+    ra = make_rsrc(w.aux, (uint32_t)(total * 256));
+  else if constexpr (FMT == DIALQ_FORMAT_NVFP4)
+    ra = make_rsrc(w.aux, (uint32_t)(total * 128));
+  else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK)
+    ra = make_rsrc(w.block_scale, (uint32_t)(((w.N + 127) / 128) * w.nbk * 4));
+  const int es = ActTraits<Pol::XACT>::BYTES;
+  rsrc_t rx = make_rsrc((const uint8_t *)p.x + p.m_base * w.K * es, (uint32_t)(mrows * w.K * es));
+
+  // fill cursor: tile t = strip s, chunk c
+  int t = lo + wave;
+  int s = t / kc, c = t - (t / kc) * kc;
+  typename Pol::Slot ring[U];
+  int slot_s[U];  // strip of the tile in each slot, -1 = none
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const bool valid = t < hi;
+    Pol::fill(ring[u], p, rt, ra, rx, s, c, valid, lane);
+    slot_s[u] = valid ? s : -1;
+    t += W;
+    c += W;
+    while (c >= kc) {
+      c -= kc;
+      ++s;
+    }
+  }
+  typename Pol::Acc acc;
+  Pol::zero(acc);
+  int cur = slot_s[0];
+  while (slot_s[0] >= 0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (slot_s[u] >= 0) {
+        if (slot_s[u] != cur) {
+          park<Pol>(part, cur - s_first, wave, mrows, acc);
+          Pol::zero(acc);
+          cur = slot_s[u];
+        }
+        Pol::compute(ring[u], acc);
+      }
+      const bool valid = t < hi;
+      Pol::fill(ring[u], p, rt, ra, rx, s, c, valid, lane);
+      slot_s[u] = valid ? s : -1;
+      t += W;
+      c += W;
+      while (c >= kc) {
+        c -= kc;
+        ++s;
+      }
+    }
+  }
+  if (cur >= 0) park<Pol>(part, cur - s_first, wave, mrows, acc);
+  __syncthreads();
+
+  // finish: wave j % W takes strip j of the range
+  const int r = lane & 15;
+  for (int j = wave; j < nseg; j += W) {
+    const int sj = s_first + j;
+    const int t0 = sj * kc;
+    const int64_t n = (int64_t)sj * 16 + r;
+    const float scale = epilogue_scale<FMT>(w, n < w.N ? n : w.N - 1);
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = lane + 64 * q;
+      float a = 0.0f;
+      if (e < slot_floats)
+        for (int ww = 0; ww < W; ++ww) a += part[(size_t)(j * W + ww) * slot_floats + e];
+      v[q] = a;
+    }
+    if (lo <= t0 && t0 + kc <= hi) {  // whole strip
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = lane + 64 * q, m = e >> 4;
+        if (e < slot_floats && n < w.N) store_out(p.y, (p.m_base + m) * w.N + n, p.y_dtype, v[q] * scale);
+      }
+      continue;
+    }
+    // Shared strip.  Partials go to the device-coherent level with
+    // agent-scope relaxed atomic stores; waiting for them (vmcnt 0) before
+    // the counter increment orders them without the L2 write-back that an
+    // agent-scope release fence costs on a multi-XCD part.  The last
+    // arriver reads them with agent-scope loads.
+    const int slot = (j == 0) ? 0 : 1;
+    float *mine = p.ws + ((size_t)b * 2 + slot) * slot_floats;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = lane + 64 * q;
+      if (e < slot_floats) __hip_atomic_store(&mine[e], v[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    // contributors: ranges owning the strip's first .. last tile
+    const int bf = (int)((((int64_t)t0 + 1) * p.G - 1) / total);
+    const int bl = (int)((((int64_t)t0 + kc) * p.G - 1) / total);
+    int last = 0;
+    if (lane == 0) last = (__hip_atomic_fetch_add(&p.cnt[sj], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == bl - bf);
+    last = __shfl(last, 0);
+    if (!last) continue;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = lane + 64 * q, m = e >> 4;
+      if (e >= slot_floats) continue;
+      float a = 0.0f;
+      for (int bb = bf; bb <= bl; ++bb) {
+        const int sl = ((((int64_t)bb * total) / p.G) < t0) ? 1 : 0;  // bb started in an earlier strip
+        a += __hip_atomic_load(&p.ws[((size_t)bb * 2 + sl) * slot_floats + e], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (n < w.N) store_out(p.y, (p.m_base + m) * w.N + n, p.y_dtype, a * scale);
+    }
+    if (lane == 0) __hip_atomic_store(&p.cnt[sj], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host dispatch
+// ---------------------------------------------------------------------------
+static int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
+// Ring depth: ~96 VGPRs of in-flight weights, scales and activations.
+constexpr int ring_depth(int slot_vgprs) {
+  return (96 / slot_vgprs) >= 8 ? 8
+       : ((96 / slot_vgprs) >= 6 ? 6 : ((96 / slot_vgprs) >= 4 ? 4 : ((96 / slot_vgprs) >= 3 ? 3 : 2)));
+}
+
+constexpr int kGemvWgPerCu = 2;     // target ranges per CU
+constexpr int kGemvLdsBytes = 32768;  // parking LDS per workgroup
+
+// Ranges for one pass of mrows rows: kGemvWgPerCu per CU, more when a range
+// would span more strips than its parking LDS holds, never more than tiles.
+static int gemv_grid(const WeightView &w, int64_t mrows) {
+  const int64_t total = w.n_strips * w.k_chunks;
+  const int64_t seg_cap = kGemvLdsBytes / (kGemvWaves * mrows * 16 * 4);  // strips per range
+  int64_t g = (int64_t)kGemvWgPerCu * device_cus();
+  // a range of ceil(total/g) tiles spans at most ceil(total/g)/kc + 2 strips
+  const int64_t need = (w.n_strips + seg_cap - 3) / (seg_cap - 2);
+  if (g < need) g = need;
+  if (g > total) g = total;
+  return (int)(g < 1 ? 1 : g);
+}
+
+template <int FMT, typename Pol, int U>
+static hipError_t launch_ranges(GemvParams &p, hipStream_t st) {
+  const int64_t mrows = (p.M - p.m_base) < 16 ? (p.M - p.m_base) : 16;
+  p.G = gemv_grid(p.w, mrows);
+  const int64_t total = p.w.n_strips * p.w.k_chunks;
+  const int64_t per = (total + p.G - 1) / p.G;
+  const int64_t nseg = per / p.w.k_chunks + 2;
+  const size_t lds = (size_t)nseg * kGemvWaves * mrows * 16 * sizeof(float);
+  if (lds > (size_t)kGemvLdsBytes) return hipErrorInvalidConfiguration;
+  k_gemv<FMT, Pol, U><<<(unsigned)p.G, 64 * kGemvWaves, lds, st>>>(p);
+  return hipGetLastError();
 }
 
 template <int FMT, int ACT>
 static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype,
-                                hipStream_t st) {
-  // Waves per workgroup: enough strips x waves to cover the 256 CUs several
-  // times over, without giving a wave fewer than ~8 chunks.
-  int waves = 4;
-  while (waves < 16 && w.n_strips * waves < 4096 && w.k_chunks >= (int64_t)waves * 16) waves *= 2;
-  dim3 grid((unsigned)w.n_strips), block((unsigned)(64 * waves));
-  for (int64_t mb = 0; mb < M; mb += 64) {
-    GemvParams p{w, x, y, M, mb, y_dtype};
-    int64_t rem = M - mb;
-    if (rem <= 16) {
-      size_t lds = (size_t)waves * 64 * 4 * 1 * sizeof(float);
-      k_gemv<FMT, ACT, 1, 4><<<grid, block, lds, st>>>(p);
-    } else if (rem <= 32) {
-      size_t lds = (size_t)waves * 64 * 4 * 2 * sizeof(float);
-      k_gemv<FMT, ACT, 2, 2><<<grid, block, lds, st>>>(p);
+                                float *ws, int *cnt, hipStream_t st) {
+  typedef FmtTraits<FMT> T;
+  constexpr int XV = (ACT == DIALQ_F32) ? 8 : 4;
+  const int rows_per_pass = (FMT == DIALQ_FORMAT_Q4_K && M <= 8) ? 8 : 16;
+  for (int64_t mb = 0; mb < M; mb += rows_per_pass) {
+    const int64_t rem = M - mb;
+    GemvParams p{w, x, y, M, mb, y_dtype, 1, ws, cnt};
+    hipError_t e;
+    constexpr int generic_u = ring_depth(T::LANE / 4 + ((FMT == DIALQ_FORMAT_Q4_K) ? 4 : 1) + T::NX * XV);
+    if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
+      if (rem <= 4)
+        e = launch_ranges<FMT, Q4kRowsPolicy<ACT, 1>, ring_depth(8 + 4 + 2 * XV)>(p, st);
+      else if (rem <= 8)
+        e = launch_ranges<FMT, Q4kRowsPolicy<ACT, 2>, ring_depth(8 + 4 + 4 * XV)>(p, st);
+      else
+        e = launch_ranges<FMT, GenericPolicy<FMT, ACT>, generic_u>(p, st);
     } else {
-      size_t lds = (size_t)waves * 64 * 4 * 4 * sizeof(float);
-      k_gemv<FMT, ACT, 4, 1><<<grid, block, lds, st>>>(p);
+      e = launch_ranges<FMT, GenericPolicy<FMT, ACT>, generic_u>(p, st);
     }
-    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
 }
 
+size_t gemv_workspace_bytes(const WeightView &w, int64_t M) {
+  size_t most = 0;
+  for (int64_t mrows = 1; mrows <= 16 && mrows <= M; ++mrows) {
+    const size_t b = (size_t)gemv_grid(w, mrows) * 2 * (size_t)mrows * 16 * sizeof(float);
+    if (b > most) most = b;
+  }
+  return most;
+}
+
 template <int FMT>
 static hipError_t gemv_act(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                           int y_dtype, hipStream_t st) {
+                           int y_dtype, float *ws, int *cnt, hipStream_t st) {
   switch (x_dtype) {
-    case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, st);
-    case DIALQ_F16: return gemv_dispatch<FMT, DIALQ_F16>(w, x, M, y, y_dtype, st);
-    case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, st);
+    case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, ws, cnt, st);
+    case DIALQ_F16: return gemv_dispatch<FMT, DIALQ_F16>(w, x, M, y, y_dtype, ws, cnt, st);
+    case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, ws, cnt, st);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                       int y_dtype, hipStream_t st) {
+                       int y_dtype, float *ws, int *cnt, hipStream_t st) {
   switch (w.fmt) {
-    case DIALQ_FORMAT_W8A16: return gemv_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_FP8_ROW: return gemv_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_Q8_0: return gemv_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, st);
+    case DIALQ_FORMAT_W8A16: return gemv_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
+    case DIALQ_FORMAT_FP8_ROW: return gemv_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
+    case DIALQ_FORMAT_Q8_0: return gemv_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
     case DIALQ_FORMAT_FP8_BLOCK:
-      return gemv_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, st);
+      return gemv_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
+    case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
+    case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
+    case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
   }
   return hipErrorInvalidValue;
 }

@@ -45,9 +45,13 @@ hipError_t launch_act_fp8(const void *x, int dtype, int64_t M, int64_t K, int64_
 hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad,
                             uint8_t *packed, uint8_t *scales, hipStream_t st);
 
-// Decode GEMV: y[M,N] = x[M,K] W^T for any M (row groups of 16 per pass).
+// Decode GEMV: y[M,N] = x[M,K] W^T for any M (16 rows per pass).
+// ws: gemv_workspace_bytes(w, M) of scratch; cnt: n_strips ints that are
+// zero before the call and are left zero after it.  The resident tiles must
+// be smaller than 2 GiB (32-bit buffer offsets).
+size_t gemv_workspace_bytes(const WeightView &w, int64_t M);
 hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                       int y_dtype, hipStream_t st);
+                       int y_dtype, float *ws, int *cnt, hipStream_t st);
 // Prefill GEMM with weight-only dequantization (bf16 / f16 MFMA operands).
 hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
                        int y_dtype, hipStream_t st);

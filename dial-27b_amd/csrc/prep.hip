@@ -355,10 +355,11 @@ __device__ __forceinline__ int64_t raw_index_aux(const RepackGeom &g, int64_t i)
   return -1;
 }
 
-// E4M3 bytes that encode NaN decode to 0 in the reference's CUDA path; the
-// resident copy stores them as +0 so hardware converters can be used.
+// E4M3 bytes that encode NaN decode to (signed) 0 in the reference's CUDA
+// path (cuda_quant.rs:35-36,40); the resident copy stores them as the zero of
+// the same sign so hardware converters can be used.
 __device__ __forceinline__ uint8_t sanitize_e4m3(uint8_t v) {
-  return ((v & 0x7f) == 0x7f) ? (uint8_t)0 : v;
+  return ((v & 0x7f) == 0x7f) ? (uint8_t)(v & 0x80) : v;
 }
 
 __global__ void k_repack_tiles(RepackGeom g, const uint8_t *raw, uint8_t *tiles, int64_t total,

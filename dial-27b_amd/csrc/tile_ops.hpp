@@ -38,6 +38,10 @@ struct XOp {
   u32x4 hi;
   u32x4 lo;
 };
+template <>
+struct XOp<DIALQ_BF16> {
+  u32x4 hi;
+};
 
 template <int ACT>
 struct ActTraits {
@@ -57,7 +61,6 @@ __device__ __forceinline__ XOp<ACT> x8_from_global(const void *x, int64_t idx) {
   XOp<ACT> r;
   if constexpr (ACT == DIALQ_BF16) {
     r.hi = *(const u32x4 *)((const uint16_t *)x + idx);
-    r.lo = (u32x4){0, 0, 0, 0};
   } else if constexpr (ACT == DIALQ_F16) {
     u32x4 raw = *(const u32x4 *)((const uint16_t *)x + idx);
 #pragma unroll
@@ -88,7 +91,21 @@ __device__ __forceinline__ XOp<ACT> load_x8(const void *x, int64_t m, int64_t k,
   if (m < M && k < K) return x8_from_global<ACT>(x, m * K + k);
   XOp<ACT> r;
   r.hi = (u32x4){0, 0, 0, 0};
-  r.lo = (u32x4){0, 0, 0, 0};
+  if constexpr (ACT != DIALQ_BF16) r.lo = (u32x4){0, 0, 0, 0};
+  return r;
+}
+
+// Unconditional variant: always loads (from a clamped, valid address) and
+// zeroes the result for rows >= M or k >= K, so no branch surrounds the load.
+template <int ACT>
+__device__ __forceinline__ XOp<ACT> load_x8_clamped(const void *x, int64_t m, int64_t k, int64_t M,
+                                                    int64_t K) {
+  const bool ok = (m < M) && (k < K);
+  const int64_t mc = m < M ? m : M - 1, kcl = k < K ? k : K - 8;
+  XOp<ACT> r = x8_from_global<ACT>(x, mc * K + kcl);
+  const u32x4 z = {0, 0, 0, 0};
+  r.hi = ok ? r.hi : z;
+  if constexpr (ACT != DIALQ_BF16) r.lo = ok ? r.lo : z;
   return r;
 }
 
@@ -97,6 +114,71 @@ __device__ __forceinline__ f32x4 mfma_x(const XOp<ACT> &a, u32x4 b, f32x4 c) {
   c = mfma_bf16(a.hi, b, c);
   if constexpr (ACT != DIALQ_BF16) c = mfma_bf16(a.lo, b, c);
   return c;
+}
+
+// ---- buffer loads -----------------------------------------------------------
+// Raw buffer loads through a resource descriptor whose size is the valid byte
+// range: an offset at or past the end returns zeros without a memory access,
+// so masked-off lanes, rows >= M and chunks past a segment need no branch.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOOB = 0x80000000u;  // offset guaranteed out of range
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload1(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
+}
+
+// Raw activation bytes for one 8-element operand (16 B for bf16/f16, 32 B
+// for f32), converted to operand parts at use time.
+template <int ACT>
+struct XRaw {
+  u32x4 a;
+  u32x4 b;  // f32 only
+};
+template <int ACT>
+__device__ __forceinline__ XRaw<ACT> xraw_load(rsrc_t r, uint32_t off) {
+  XRaw<ACT> v;
+  v.a = bload16(r, off);
+  if constexpr (ACT == DIALQ_F32) v.b = bload16(r, off + 16);
+  return v;
+}
+template <int ACT>
+__device__ __forceinline__ XOp<ACT> xraw_to_op(const XRaw<ACT> &v) {
+  XOp<ACT> o;
+  if constexpr (ACT == DIALQ_BF16) {
+    o.hi = v.a;
+  } else if constexpr (ACT == DIALQ_F16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t h0, l0, h1, l1;
+      split_f32(f16_bits_to_f32(v.a[i] & 0xffffu), h0, l0);
+      split_f32(f16_bits_to_f32(v.a[i] >> 16), h1, l1);
+      o.hi[i] = h0 | (h1 << 16);
+      o.lo[i] = l0 | (l1 << 16);
+    }
+  } else {
+    const uint32_t f[8] = {v.a[0], v.a[1], v.a[2], v.a[3], v.b[0], v.b[1], v.b[2], v.b[3]};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t h0, l0, h1, l1;
+      split_f32(__uint_as_float(f[2 * i]), h0, l0);
+      split_f32(__uint_as_float(f[2 * i + 1]), h1, l1);
+      o.hi[i] = h0 | (h1 << 16);
+      o.lo[i] = l0 | (l1 << 16);
+    }
+  }
+  return o;
 }
 
 // ---- weight code -> exact bf16 --------------------------------------------
@@ -137,6 +219,17 @@ __device__ __forceinline__ u32x4 e2m1x8_to_bf16(uint32_t d, float scale) {
   r[1] = pack_bf16_trunc(v1[0] * scale, v1[1] * scale);
   r[2] = pack_bf16_trunc(v2[0] * scale, v2[1] * scale);
   r[3] = pack_bf16_trunc(v3[0] * scale, v3[1] * scale);
+  return r;
+}
+
+// 8 E2M1 codes times a power-of-two scale (an E8M0 value) -> bf16, one
+// v_cvt_scalef32_pk_bf16_fp4 per pair (exact: 2 significant bits).
+__device__ __forceinline__ u32x4 e2m1x8_pow2_to_bf16(uint32_t d, float scale) {
+  u32x4 r;
+  r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 0));
+  r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 1));
+  r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 2));
+  r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 3));
   return r;
 }
 
@@ -194,8 +287,22 @@ struct FmtTraits<DIALQ_FORMAT_Q4_K> {
 
 struct RawTile {
   u32x4 a;
-  u32x4 b;  // second 16 bytes (LANE == 32 formats)
+  u32x4 b;       // second 16 bytes (LANE == 32 formats)
+  uint32_t s0;   // per-lane scale bits: Q8_0 d pair, NVFP4 E4M3 pair,
+                 // MXFP4 E8M0, FP8_BLOCK f32 block scale
+  u32x4 hdr;     // Q4_K super-block header {d, dmin, scales[12]}
 };
+
+template <int LANE>
+__device__ __forceinline__ RawTile load_tile_at(const uint8_t *p) {
+  RawTile r;
+  r.a = __builtin_nontemporal_load((const u32x4 *)p);
+  if constexpr (LANE == 32)
+    r.b = __builtin_nontemporal_load((const u32x4 *)(p + 16));
+  else
+    r.b = (u32x4){0, 0, 0, 0};
+  return r;
+}
 
 template <int FMT>
 __device__ __forceinline__ RawTile load_tile(const uint8_t *tiles, int64_t tile_idx, int lane) {
@@ -210,6 +317,32 @@ __device__ __forceinline__ RawTile load_tile(const uint8_t *tiles, int64_t tile_
   return r;
 }
 
+// All global loads of one tile for one lane (weights and the k-varying
+// scales of the lane's row), issued unconditionally so the compiler can
+// count outstanding loads statically; callers pass a valid (clamped) chunk.
+template <int FMT>
+__device__ __forceinline__ RawTile load_tile_full(const WeightView &w, const uint8_t *tbase, int s,
+                                                  int c, int lane) {
+  constexpr int LANE = FmtTraits<FMT>::LANE;
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t tidx = (uint32_t)s * (uint32_t)w.k_chunks + (uint32_t)c;
+  RawTile t = load_tile_at<LANE>(tbase + (uint32_t)c * (64 * LANE));
+  t.s0 = 0;
+  t.hdr = (u32x4){0, 0, 0, 0};
+  if constexpr (FMT == DIALQ_FORMAT_Q8_0) {
+    t.s0 = *(const uint32_t *)(w.aux + tidx * 64 + r * 4);
+  } else if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
+    t.hdr = *(const u32x4 *)(w.aux + tidx * 256 + r * 16);
+  } else if constexpr (FMT == DIALQ_FORMAT_NVFP4) {
+    t.s0 = *(const uint16_t *)(w.aux + tidx * 128 + r * 8 + 2 * g);
+  } else if constexpr (FMT == DIALQ_FORMAT_MXFP4) {
+    t.s0 = w.aux[tidx * 64 + r * 4 + g];
+  } else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK) {
+    t.s0 = __float_as_uint(w.block_scale[(uint32_t)((s * 16) / 128) * (uint32_t)w.nbk + (uint32_t)c]);
+  }
+  return t;
+}
+
 // B operands of one tile plus the lane row's scale factors.
 template <int FMT>
 struct BOps {
@@ -218,11 +351,9 @@ struct BOps {
   float s2[FmtTraits<FMT>::NX];  // Q4_K: 128*d*sc + dmin*m
 };
 
+// `t` must come from load_tile_full (scales included).
 template <int FMT>
-__device__ __forceinline__ BOps<FMT> make_bops(const RawTile &t, const WeightView &w, int64_t s,
-                                               int64_t c, int lane) {
-  const int r = lane & 15, g = lane >> 4;
-  const int64_t tidx = s * w.k_chunks + c;
+__device__ __forceinline__ BOps<FMT> make_bops(const RawTile &t) {
   BOps<FMT> o;
   if constexpr (FMT == DIALQ_FORMAT_W8A16) {
     o.b[0] = i8x8_to_bf16(t.a[0], t.a[1]);
@@ -231,30 +362,30 @@ __device__ __forceinline__ BOps<FMT> make_bops(const RawTile &t, const WeightVie
     o.b[0] = e4m3x8_to_bf16(t.a[0], t.a[1]);
     o.b[1] = e4m3x8_to_bf16(t.a[2], t.a[3]);
   } else if constexpr (FMT == DIALQ_FORMAT_Q8_0) {
-    uint32_t dd = *(const uint32_t *)(w.aux + tidx * 64 + r * 4);
+    const uint32_t dd = t.s0;
     o.s1[0] = f16_bits_to_f32(dd & 0xffffu);
     o.s1[1] = f16_bits_to_f32(dd >> 16);
     o.b[0] = i8x8_to_bf16(t.a[0], t.a[1]);
     o.b[1] = i8x8_to_bf16(t.a[2], t.a[3]);
   } else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK) {
-    o.s1[0] = w.block_scale[((s * 16) / 128) * w.nbk + c];
+    o.s1[0] = __uint_as_float(t.s0);
     o.b[0] = e4m3x8_to_bf16(t.a[0], t.a[1]);
     o.b[1] = e4m3x8_to_bf16(t.a[2], t.a[3]);
     o.b[2] = e4m3x8_to_bf16(t.b[0], t.b[1]);
     o.b[3] = e4m3x8_to_bf16(t.b[2], t.b[3]);
   } else if constexpr (FMT == DIALQ_FORMAT_NVFP4) {
-    uint32_t sb = *(const uint16_t *)(w.aux + tidx * 128 + r * 8 + 2 * g);
+    const uint32_t sb = t.s0;
     float g0 = e4m3_to_f32(sb & 0xffu), g1 = e4m3_to_f32(sb >> 8);
     o.b[0] = e2m1x8_to_bf16(t.a[0], g0);
     o.b[1] = e2m1x8_to_bf16(t.a[1], g0);
     o.b[2] = e2m1x8_to_bf16(t.a[2], g1);
     o.b[3] = e2m1x8_to_bf16(t.a[3], g1);
   } else if constexpr (FMT == DIALQ_FORMAT_MXFP4) {
-    float sc = e8m0_to_f32(w.aux[tidx * 64 + r * 4 + g]);
+    float sc = e8m0_to_f32(t.s0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o.b[i] = e2m1x8_to_bf16(t.a[i], sc);
+    for (int i = 0; i < 4; ++i) o.b[i] = e2m1x8_pow2_to_bf16(t.a[i], sc);
   } else if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
-    u32x4 h = *(const u32x4 *)(w.aux + tidx * 256 + r * 16);
+    const u32x4 h = t.hdr;
     float d = f16_bits_to_f32(h[0] & 0xffffu), dmin = f16_bits_to_f32(h[0] >> 16);
     uint32_t sc8[12];
 #pragma unroll

@@ -46,6 +46,15 @@ def _load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"{LIB_PATH} is not built; run `python dial-27b_amd/build.py` "
                           "(or __graft_entry__.build()) first")
+    # One HIP runtime per process: torch ships its own libamdhip64.so.7.  Load
+    # it first so libdialq's libamdhip64.so.7 dependency resolves to the same
+    # runtime (device pointers and streams are shared with the caller).  A
+    # caller without torch gets /opt/rocm's runtime through the library's
+    # RUNPATH.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = C.CDLL(LIB_PATH)
     P, I64, I32, SZ, CH = C.c_void_p, C.c_int64, C.c_int32, C.c_size_t, C.c_char_p
     sigs = {

@@ -62,10 +62,10 @@ def test_export_round_trip(fmt, torch_dev):
     lin, raw, scales, deq = _linear(fmt, n, k, seed=10 + fmt)
     w, s = lin.export()
     raw = np.asarray(raw)
-    if fmt == dq.FP8_ROW:
-        raw = np.where((raw & 0x7F) == 0x7F, 0, raw)  # NaN codes are stored as 0
+    if fmt == dq.FP8_ROW:  # NaN codes are stored as the zero of the same sign
+        raw = np.where((raw & 0x7F) == 0x7F, raw & 0x80, raw)
     if fmt == dq.NVFP4:
-        scales = np.where((scales & 0x7F) == 0x7F, 0, scales)
+        scales = np.where((scales & 0x7F) == 0x7F, scales & 0x80, scales)
     assert np.array_equal(w.reshape(-1).view(np.uint8), raw.reshape(-1).view(np.uint8))
     if scales is not None:
         assert np.array_equal(np.asarray(s).reshape(-1).view(np.uint8),
