@@ -258,7 +258,7 @@ void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, i
     std::lock_guard<std::mutex> lock(L->scratch_mu);
     size_t need = gemv_workspace_bytes(w, rows);
     if (L->gemv_ws.n < need) L->gemv_ws.alloc(need);
-    hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, (float *)L->gemv_ws.p, (int *)L->gemv_cnt.p, st),
+    hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, (float *)L->gemv_ws.p, L->gemv_ws.n, (int *)L->gemv_cnt.p, st),
               "GEMV launch");
   } else if (path == DIALQ_PATH_GEMM) {
     hip_check(launch_gemm(w, x, x_dtype, rows, y, y_dtype, st), "GEMM launch");

@@ -40,59 +40,110 @@ struct GemvParams {
   int y_dtype;
   int G;           // workgroups (tile ranges)
   float *ws;       // [G][2][mrows][16] partials of shared strips
+  size_t ws_bytes;
+  int x_pitch;     // bytes per staged activation row (0: not staged)
   int *cnt;        // [n_strips] arrival counters (zero between launches)
 };
 
 constexpr int kGemvWaves = 4;  // waves per workgroup
 
 // ---------------------------------------------------------------------------
-// Per-format ring slot (policy).  fill() issues every global load of one
-// element unconditionally (buffer loads; `valid` = false turns them into
-// zero-returning out-of-range loads); compute() multiplies a filled slot
-// into the accumulator.
+// Activation source.  Small activations (XL) are staged once per workgroup
+// into LDS with buffer->LDS DMA, as raw rows of the input dtype at a padded
+// row pitch, plus a zero block that lanes whose row is >= mrows read; the
+// ring then carries weights only.  Larger ones are fetched per tile into the
+// ring (buffer loads, rows >= mrows and k >= K out of range -> zeros).
 // ---------------------------------------------------------------------------
-template <int FMT, int ACT>
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+struct Ctx {
+  rsrc_t rt, ra, rx;
+  const lds_u8 *xl;    // staged rows (XL)
+  const lds_u8 *zero;  // 32 zero bytes (XL)
+  int pitch;           // bytes per staged row
+  int mrows, K;
+};
+
+template <int ACT, bool XL>
+__device__ __forceinline__ XRaw<ACT> x_fetch(const Ctx &cx, int row, int k, bool valid) {
+  constexpr int BY = ActTraits<ACT>::BYTES;
+  XRaw<ACT> v;
+  if constexpr (XL) {
+    const lds_u8 *src = (row < cx.mrows) ? cx.xl + row * cx.pitch + k * BY : cx.zero;
+    v.a = *(const u32x4 __attribute__((address_space(3))) *)src;
+    if constexpr (ACT == DIALQ_F32) v.b = *(const u32x4 __attribute__((address_space(3))) *)(src + 16);
+  } else {
+    const uint32_t xo = ((uint32_t)row * (uint32_t)cx.K + (uint32_t)k) * BY;
+    v = xraw_load<ACT>(cx.rx, (valid && k < cx.K) ? xo : kOOB);
+  }
+  return v;
+}
+
+// Weight tile and its scales for tile (strip s, chunk c): every load issued
+// unconditionally (`valid` = false turns them into out-of-range loads).
+template <int FMT>
+__device__ __forceinline__ void tile_fill(RawTile &t, const WeightView &w, const Ctx &cx, int s, int c, bool valid,
+                                          int lane) {
+  typedef FmtTraits<FMT> T;
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t tidx = (uint32_t)s * (uint32_t)w.k_chunks + (uint32_t)c;
+  const uint32_t off = valid ? tidx * (64 * T::LANE) + lane * T::LANE : kOOB;
+  t.a = sload16(cx.rt, off);
+  t.b = (u32x4){0, 0, 0, 0};
+  if constexpr (T::LANE == 32) t.b = sload16(cx.rt, valid ? off + 16 : kOOB);
+  t.s0 = 0;
+  t.hdr = (u32x4){0, 0, 0, 0};
+  if constexpr (FMT == DIALQ_FORMAT_Q8_0) t.s0 = sload4(cx.ra, valid ? tidx * 64 + r * 4 : kOOB);
+  else if constexpr (FMT == DIALQ_FORMAT_Q4_K) t.hdr = sload16(cx.ra, valid ? tidx * 256 + r * 16 : kOOB);
+  else if constexpr (FMT == DIALQ_FORMAT_NVFP4) t.s0 = sload2(cx.ra, valid ? tidx * 128 + r * 8 + 2 * g : kOOB);
+  else if constexpr (FMT == DIALQ_FORMAT_MXFP4) t.s0 = sload1(cx.ra, valid ? tidx * 64 + r * 4 + g : kOOB);
+  else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK)  // shared by 8 strips: default cache policy
+    t.s0 = bload4(cx.ra, valid ? ((uint32_t)((s * 16) / 128) * (uint32_t)w.nbk + (uint32_t)c) * 4 : kOOB);
+}
+
+template <int ACT, int N, bool XL>
+struct XRing {
+  XRaw<ACT> v[N];
+};
+template <int ACT, int N>
+struct XRing<ACT, N, true> {};
+
+// ---------------------------------------------------------------------------
+// Per-format ring slot (policy): fill() issues the loads of one tile,
+// compute() multiplies a filled slot into the accumulator.
+// ---------------------------------------------------------------------------
+template <int FMT, int ACT, bool XL>
 struct GenericPolicy {
   typedef FmtTraits<FMT> T;
   static constexpr int XACT = ACT;
   static constexpr int NV = 4;  // accumulator values per lane
   struct Slot {
     RawTile t;
-    XRaw<ACT> x[T::NX];
+    int c;
+    XRing<ACT, T::NX, XL> x;
   };
   struct Acc {
     f32x4 v;
   };
   static __device__ __forceinline__ void zero(Acc &a) { a.v = (f32x4){0.0f, 0.0f, 0.0f, 0.0f}; }
-  static __device__ __forceinline__ void fill(Slot &sl, const GemvParams &p, rsrc_t rt, rsrc_t ra, rsrc_t rx,
-                                              int s, int c, bool valid, int lane) {
-    const WeightView &w = p.w;
-    const int r = lane & 15, g = lane >> 4;
-    const uint32_t tidx = (uint32_t)s * (uint32_t)w.k_chunks + (uint32_t)c;
-    const uint32_t off = valid ? tidx * (64 * T::LANE) + lane * T::LANE : kOOB;
-    sl.t.a = bload16(rt, off);
-    sl.t.b = (u32x4){0, 0, 0, 0};
-    if constexpr (T::LANE == 32) sl.t.b = bload16(rt, valid ? off + 16 : kOOB);
-    sl.t.s0 = 0;
-    sl.t.hdr = (u32x4){0, 0, 0, 0};
-    if constexpr (FMT == DIALQ_FORMAT_Q8_0) sl.t.s0 = bload4(ra, valid ? tidx * 64 + r * 4 : kOOB);
-    else if constexpr (FMT == DIALQ_FORMAT_Q4_K) sl.t.hdr = bload16(ra, valid ? tidx * 256 + r * 16 : kOOB);
-    else if constexpr (FMT == DIALQ_FORMAT_NVFP4) sl.t.s0 = bload2(ra, valid ? tidx * 128 + r * 8 + 2 * g : kOOB);
-    else if constexpr (FMT == DIALQ_FORMAT_MXFP4) sl.t.s0 = bload1(ra, valid ? tidx * 64 + r * 4 + g : kOOB);
-    else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK)
-      sl.t.s0 = bload4(ra, valid ? ((uint32_t)((s * 16) / 128) * (uint32_t)w.nbk + (uint32_t)c) * 4 : kOOB);
-    const int K = (int)w.K;
+  static __device__ __forceinline__ void fill(Slot &sl, const WeightView &w, const Ctx &cx, int s, int c, bool valid,
+                                              int lane) {
+    tile_fill<FMT>(sl.t, w, cx, s, c, valid, lane);
+    sl.c = c;
+    if constexpr (!XL) {
+      const int r = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int t = 0; t < T::NX; ++t) {
-      const int k = c * T::CHUNK + T::xk(t, g);
-      const uint32_t xo = ((uint32_t)r * (uint32_t)K + (uint32_t)k) * ActTraits<ACT>::BYTES;
-      sl.x[t] = xraw_load<ACT>(rx, (valid && k < K) ? xo : kOOB);
+      for (int t = 0; t < T::NX; ++t) sl.x.v[t] = x_fetch<ACT, false>(cx, r, c * T::CHUNK + T::xk(t, g), valid);
     }
   }
-  static __device__ __forceinline__ void compute(const Slot &sl, Acc &a) {
+  static __device__ __forceinline__ void compute(const Slot &sl, Acc &a, const Ctx &cx) {
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
     XOp<ACT> xo[T::NX];
 #pragma unroll
-    for (int t = 0; t < T::NX; ++t) xo[t] = xraw_to_op<ACT>(sl.x[t]);
+    for (int t = 0; t < T::NX; ++t) {
+      if constexpr (XL) xo[t] = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, r, sl.c * T::CHUNK + T::xk(t, g), true));
+      else xo[t] = xraw_to_op<ACT>(sl.x.v[t]);
+    }
     bops_mac<FMT, ACT>(make_bops<FMT>(sl.t), xo, a.v);
   }
   static __device__ __forceinline__ void values(const Acc &a, float (&v)[NV], int (&mrow)[NV], int lane) {
@@ -115,13 +166,14 @@ struct GenericPolicy {
 // term use the per-sub-block activation sums X_t[m'] from a second MFMA with
 // a ones operand:  y += s1*D - (128*s1 + dmin*m)*X.  RP passes cover rows
 // 4*pass + m'.
-template <int ACT, int RP>
+template <int ACT, int RP, bool XL>
 struct Q4kRowsPolicy {
   static constexpr int XACT = ACT;
   static constexpr int NV = RP;
   struct Slot {
     RawTile t;
-    XRaw<ACT> x[RP][2];  // sub-blocks jj and jj + 4 of row 4q + mq
+    int c;
+    XRing<ACT, 2 * RP, XL> x;  // [q][h]: sub-blocks jj and jj + 4 of row 4q + mq
   };
   struct Acc {
     float v[RP];
@@ -130,28 +182,23 @@ struct Q4kRowsPolicy {
 #pragma unroll
     for (int q = 0; q < RP; ++q) a.v[q] = 0.0f;
   }
-  static __device__ __forceinline__ void fill(Slot &sl, const GemvParams &p, rsrc_t rt, rsrc_t ra, rsrc_t rx,
-                                              int s, int c, bool valid, int lane) {
-    const WeightView &w = p.w;
-    const int r = lane & 15, g = lane >> 4, mq = r >> 2, jj = r & 3;
-    const uint32_t tidx = (uint32_t)s * (uint32_t)w.k_chunks + (uint32_t)c;
-    const uint32_t off = valid ? tidx * 2048 + lane * 32 : kOOB;
-    sl.t.a = bload16(rt, off);
-    sl.t.b = bload16(rt, valid ? off + 16 : kOOB);
-    sl.t.s0 = 0;
-    sl.t.hdr = bload16(ra, valid ? tidx * 256 + r * 16 : kOOB);
-    const int K = (int)w.K;
-#pragma unroll
-    for (int q = 0; q < RP; ++q)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int k = c * 256 + 32 * (jj + 4 * h) + 8 * g;
-        const uint32_t xo = ((uint32_t)(4 * q + mq) * (uint32_t)K + (uint32_t)k) * ActTraits<ACT>::BYTES;
-        sl.x[q][h] = xraw_load<ACT>(rx, (valid && k < K) ? xo : kOOB);
-      }
+  static __device__ __forceinline__ int xk(int c, int h, int lane) {
+    return c * 256 + 32 * ((lane & 3) + 4 * h) + 8 * (lane >> 4);
   }
-  static __device__ __forceinline__ void compute(const Slot &sl, Acc &acc) {
-    const int lane = threadIdx.x & 63, jj = lane & 3;
+  static __device__ __forceinline__ void fill(Slot &sl, const WeightView &w, const Ctx &cx, int s, int c, bool valid,
+                                              int lane) {
+    tile_fill<DIALQ_FORMAT_Q4_K>(sl.t, w, cx, s, c, valid, lane);
+    sl.c = c;
+    if constexpr (!XL) {
+      const int mq = (lane & 15) >> 2;
+#pragma unroll
+      for (int q = 0; q < RP; ++q)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) sl.x.v[2 * q + h] = x_fetch<ACT, false>(cx, 4 * q + mq, xk(c, h, lane), valid);
+    }
+  }
+  static __device__ __forceinline__ void compute(const Slot &sl, Acc &acc, const Ctx &cx) {
+    const int lane = threadIdx.x & 63, jj = lane & 3, mq = (lane & 15) >> 2;
     const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     const u32x4 hd = sl.t.hdr;
@@ -163,18 +210,25 @@ struct Q4kRowsPolicy {
     const uint32_t qd[8] = {sl.t.a[0], sl.t.a[1], sl.t.a[2], sl.t.a[3], sl.t.b[0], sl.t.b[1], sl.t.b[2], sl.t.b[3]};
 #pragma unroll
     for (int q = 0; q < RP; ++q) {
-      const XOp<ACT> xa = xraw_to_op<ACT>(sl.x[q][0]), xb = xraw_to_op<ACT>(sl.x[q][1]);
-      f32x4 cq[2] = {zero, zero}, cx[2] = {zero, zero};
+      XOp<ACT> xa, xb;
+      if constexpr (XL) {
+        xa = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, 4 * q + mq, xk(sl.c, 0, lane), true));
+        xb = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, 4 * q + mq, xk(sl.c, 1, lane), true));
+      } else {
+        xa = xraw_to_op<ACT>(sl.x.v[2 * q]);
+        xb = xraw_to_op<ACT>(sl.x.v[2 * q + 1]);
+      }
+      f32x4 cq[2] = {zero, zero}, cs[2] = {zero, zero};
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const u32x4 wb = nib8_to_bf16_off128(qd[2 * (t >> 1)], qd[2 * (t >> 1) + 1], (t & 1) ? 4 : 0);
         const bool on = (jj == (t & 3));
         const XOp<ACT> &src = (t < 4) ? xa : xb;
-        XOp<ACT> a;
-        a.hi = on ? src.hi : (u32x4){0, 0, 0, 0};
-        if constexpr (ActTraits<ACT>::PARTS == 2) a.lo = on ? src.lo : (u32x4){0, 0, 0, 0};
-        cq[t >> 2] = mfma_x<ACT>(a, wb, cq[t >> 2]);
-        cx[t >> 2] = mfma_x<ACT>(a, ones, cx[t >> 2]);
+        XOp<ACT> av;
+        av.hi = on ? src.hi : (u32x4){0, 0, 0, 0};
+        if constexpr (ActTraits<ACT>::PARTS == 2) av.lo = on ? src.lo : (u32x4){0, 0, 0, 0};
+        cq[t >> 2] = mfma_x<ACT>(av, wb, cq[t >> 2]);
+        cs[t >> 2] = mfma_x<ACT>(av, ones, cs[t >> 2]);
       }
       // lane (g, r) holds rows 4g+i: m' = g, sub-block i (+4 in [1])
       float sum = acc.v[q];
@@ -184,8 +238,8 @@ struct Q4kRowsPolicy {
         const float s2a = __builtin_fmaf(128.0f, s1a, dmin * (float)((m_lo >> (8 * i)) & 0xffu));
         const float s1b = d * (float)((sc_hi >> (8 * i)) & 0xffu);
         const float s2b = __builtin_fmaf(128.0f, s1b, dmin * (float)((m_hi >> (8 * i)) & 0xffu));
-        sum = __builtin_fmaf(s1a, cq[0][i], __builtin_fmaf(-s2a, cx[0][i], sum));
-        sum = __builtin_fmaf(s1b, cq[1][i], __builtin_fmaf(-s2b, cx[1][i], sum));
+        sum = __builtin_fmaf(s1a, cq[0][i], __builtin_fmaf(-s2a, cs[0][i], sum));
+        sum = __builtin_fmaf(s1b, cq[1][i], __builtin_fmaf(-s2b, cs[1][i], sum));
       }
       acc.v[q] = sum;
     }
@@ -201,8 +255,9 @@ struct Q4kRowsPolicy {
 };
 
 // ---------------------------------------------------------------------------
-// The GEMV kernel.  LDS holds part[j][wave][m][16]: the accumulator of wave
-// `wave` for the j-th strip of the range, rows m < mrows only.
+// The GEMV kernel.  Dynamic LDS: [staged x: mrows * pitch][32 zero bytes]
+// [part[j][wave][m][16]: the accumulator of wave `wave` for the j-th strip
+// of the range, rows m < mrows only].
 // ---------------------------------------------------------------------------
 template <typename Pol>
 __device__ __forceinline__ void park(float *part, int j, int wave, int mrows, const typename Pol::Acc &acc) {
@@ -217,10 +272,18 @@ __device__ __forceinline__ void park(float *part, int j, int wave, int mrows, co
     if (mrow[i] < mrows) dst[mrow[i] * 16 + r] = v[i];
 }
 
-template <int FMT, typename Pol, int U>
+// Barrier that orders LDS only (no wait on outstanding global loads).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int FMT, typename Pol, int U, bool XL>
 __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
-  extern __shared__ float part[];
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int W = kGemvWaves;
+  constexpr int BY = ActTraits<Pol::XACT>::BYTES;
   const WeightView &w = p.w;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -233,22 +296,42 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
   const int mrows = (int)((p.M - p.m_base) < 16 ? (p.M - p.m_base) : 16);
   const int slot_floats = mrows * 16;
 
+  Ctx cx;
+  cx.mrows = mrows;
+  cx.K = (int)w.K;
+  cx.pitch = p.x_pitch;
+  cx.xl = (const lds_u8 *)smem;
+  cx.zero = (const lds_u8 *)smem + (XL ? mrows * p.x_pitch : 0);
+  float *part = (float *)(smem + (XL ? mrows * p.x_pitch + 32 : 0));
+  cx.rt = make_rsrc(w.tiles, (uint32_t)(total * 64 * FmtTraits<FMT>::LANE));
+  cx.ra = cx.rt;
+  if constexpr (FMT == DIALQ_FORMAT_Q8_0 || FMT == DIALQ_FORMAT_MXFP4)
+    cx.ra = make_rsrc(w.aux, (uint32_t)(total * 64));
+  else if constexpr (FMT == DIALQ_FORMAT_Q4_K)
+    cx.ra = make_rsrc(w.aux, (uint32_t)(total * 256));
+  else if constexpr (FMT == DIALQ_FORMAT_NVFP4)
+    cx.ra = make_rsrc(w.aux, (uint32_t)(total * 128));
+  else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK)
+    cx.ra = make_rsrc(w.block_scale, (uint32_t)(((w.N + 127) / 128) * w.nbk * 4));
+  cx.rx = make_rsrc((const uint8_t *)p.x + p.m_base * w.K * BY, (uint32_t)(mrows * w.K * BY));
+
+  if constexpr (XL) {
+    // Stage x: 1 KB per DMA instruction (lane l -> bytes 16l..16l+15 of the
+    // block); bytes at or past K*BY read as zeros, which pads every row.
+    const int row_bytes = w.K * BY;
+    const int blocks = p.x_pitch >> 10;  // 1 KB blocks per row (pitch = blocks KB + 64)
+    for (int i = wave; i < mrows * blocks; i += W) {
+      const int m = i / blocks, kb = (i - m * blocks) << 10;
+      const int col = kb + lane * 16;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(cx.rx, (__attribute__((address_space(3))) void *)(smem + m * p.x_pitch + kb),
+                                                16, col < row_bytes ? m * row_bytes + col : (int)kOOB, 0, 0, 0);
+    }
+    if (threadIdx.x < 2) *(u32x4 __attribute__((address_space(3))) *)(smem + mrows * p.x_pitch + 16 * threadIdx.x) = (u32x4){0, 0, 0, 0};
+  }
   // each wave clears its own parking slots (a wave may skip a strip)
   for (int j = 0; j < nseg; ++j)
     for (int e = lane; e < slot_floats; e += 64) part[(size_t)(j * W + wave) * slot_floats + e] = 0.0f;
-
-  rsrc_t rt = make_rsrc(w.tiles, (uint32_t)(total * 64 * FmtTraits<FMT>::LANE));
-  rsrc_t ra = rt;
-  if constexpr (FMT == DIALQ_FORMAT_Q8_0 || FMT == DIALQ_FORMAT_MXFP4)
-    ra = make_rsrc(w.aux, (uint32_t)(total * 64));
-  else if constexpr (FMT == DIALQ_FORMAT_Q4_K)
-    ra = make_rsrc(w.aux, (uint32_t)(total * 256));
-  else if constexpr (FMT == DIALQ_FORMAT_NVFP4)
-    ra = make_rsrc(w.aux, (uint32_t)(total * 128));
-  else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK)
-    ra = make_rsrc(w.block_scale, (uint32_t)(((w.N + 127) / 128) * w.nbk * 4));
-  const int es = ActTraits<Pol::XACT>::BYTES;
-  rsrc_t rx = make_rsrc((const uint8_t *)p.x + p.m_base * w.K * es, (uint32_t)(mrows * w.K * es));
+  __builtin_amdgcn_sched_barrier(0);
 
   // fill cursor: tile t = strip s, chunk c
   int t = lo + wave;
@@ -258,7 +341,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const bool valid = t < hi;
-    Pol::fill(ring[u], p, rt, ra, rx, s, c, valid, lane);
+    Pol::fill(ring[u], w, cx, s, c, valid, lane);
     slot_s[u] = valid ? s : -1;
     t += W;
     c += W;
@@ -267,6 +350,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
       ++s;
     }
   }
+  if constexpr (XL) lds_barrier();  // staged x visible to all waves
   typename Pol::Acc acc;
   Pol::zero(acc);
   int cur = slot_s[0];
@@ -279,10 +363,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
           Pol::zero(acc);
           cur = slot_s[u];
         }
-        Pol::compute(ring[u], acc);
+        Pol::compute(ring[u], acc, cx);
       }
       const bool valid = t < hi;
-      Pol::fill(ring[u], p, rt, ra, rx, s, c, valid, lane);
+      Pol::fill(ring[u], w, cx, s, c, valid, lane);
       slot_s[u] = valid ? s : -1;
       t += W;
       c += W;
@@ -293,7 +377,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
     }
   }
   if (cur >= 0) park<Pol>(part, cur - s_first, wave, mrows, acc);
-  __syncthreads();
+  lds_barrier();
 
   // finish: wave j % W takes strip j of the range
   const int r = lane & 15;
@@ -323,7 +407,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
     // agent-scope relaxed atomic stores; waiting for them (vmcnt 0) before
     // the counter increment orders them without the L2 write-back that an
     // agent-scope release fence costs on a multi-XCD part.  The last
-    // arriver reads them with agent-scope loads.
+    // arriver reads them back with device-coherent (sc1) buffer loads,
+    // eight contributors per batch so the round trips overlap.
     const int slot = (j == 0) ? 0 : 1;
     float *mine = p.ws + ((size_t)b * 2 + slot) * slot_floats;
 #pragma unroll
@@ -339,17 +424,31 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
     if (lane == 0) last = (__hip_atomic_fetch_add(&p.cnt[sj], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == bl - bf);
     last = __shfl(last, 0);
     if (!last) continue;
+    const rsrc_t rw = make_rsrc(p.ws, (uint32_t)p.ws_bytes);
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b0 = bf; b0 <= bl; b0 += 8) {
+      float pv[8][4];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int bb = b0 + i;
+        // slot of strip sj in range bb: 1 if bb started in an earlier strip
+        const int sl = ((((int64_t)bb * total) / p.G) < t0) ? 1 : 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int e = lane + 64 * q;
+          const uint32_t off = (bb <= bl && e < slot_floats) ? (uint32_t)((((size_t)bb * 2 + sl) * slot_floats + e) * 4) : kOOB;
+          pv[i][q] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, (int)off, 0, kSC1));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[q] += pv[i][q];
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int e = lane + 64 * q, m = e >> 4;
-      if (e >= slot_floats) continue;
-      float a = 0.0f;
-      for (int bb = bf; bb <= bl; ++bb) {
-        const int sl = ((((int64_t)bb * total) / p.G) < t0) ? 1 : 0;  // bb started in an earlier strip
-        a += __hip_atomic_load(&p.ws[((size_t)bb * 2 + sl) * slot_floats + e], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (n < w.N) store_out(p.y, (p.m_base + m) * w.N + n, p.y_dtype, a * scale);
+      if (e < slot_floats && n < w.N) store_out(p.y, (p.m_base + m) * w.N + n, p.y_dtype, a[q] * scale);
     }
     if (lane == 0) __hip_atomic_store(&p.cnt[sj], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -377,14 +476,15 @@ constexpr int ring_depth(int slot_vgprs) {
        : ((96 / slot_vgprs) >= 6 ? 6 : ((96 / slot_vgprs) >= 4 ? 4 : ((96 / slot_vgprs) >= 3 ? 3 : 2)));
 }
 
-constexpr int kGemvWgPerCu = 2;     // target ranges per CU
-constexpr int kGemvLdsBytes = 32768;  // parking LDS per workgroup
+constexpr int kGemvWgPerCu = 2;          // target ranges per CU
+constexpr int kGemvParkBytes = 16384;    // parking LDS per workgroup
+constexpr int kGemvStageBytes = 65536;   // staged-activation LDS per workgroup
 
 // Ranges for one pass of mrows rows: kGemvWgPerCu per CU, more when a range
 // would span more strips than its parking LDS holds, never more than tiles.
 static int gemv_grid(const WeightView &w, int64_t mrows) {
   const int64_t total = w.n_strips * w.k_chunks;
-  const int64_t seg_cap = kGemvLdsBytes / (kGemvWaves * mrows * 16 * 4);  // strips per range
+  const int64_t seg_cap = kGemvParkBytes / (kGemvWaves * mrows * 16 * 4);  // strips per range
   int64_t g = (int64_t)kGemvWgPerCu * device_cus();
   // a range of ceil(total/g) tiles spans at most ceil(total/g)/kc + 2 strips
   const int64_t need = (w.n_strips + seg_cap - 3) / (seg_cap - 2);
@@ -393,39 +493,64 @@ static int gemv_grid(const WeightView &w, int64_t mrows) {
   return (int)(g < 1 ? 1 : g);
 }
 
-template <int FMT, typename Pol, int U>
+// Bytes per staged activation row: whole 1 KB DMA blocks covering the padded
+// k range, plus 64 bytes so that rows start in different LDS banks.
+static int stage_pitch(const WeightView &w, int by, int chunk) {
+  const int64_t kpad_bytes = w.k_chunks * chunk * by;
+  return (int)(((kpad_bytes + 1023) / 1024) * 1024 + 64);
+}
+
+template <int FMT, typename Pol, int U, bool XL>
 static hipError_t launch_ranges(GemvParams &p, hipStream_t st) {
   const int64_t mrows = (p.M - p.m_base) < 16 ? (p.M - p.m_base) : 16;
   p.G = gemv_grid(p.w, mrows);
   const int64_t total = p.w.n_strips * p.w.k_chunks;
   const int64_t per = (total + p.G - 1) / p.G;
   const int64_t nseg = per / p.w.k_chunks + 2;
-  const size_t lds = (size_t)nseg * kGemvWaves * mrows * 16 * sizeof(float);
-  if (lds > (size_t)kGemvLdsBytes) return hipErrorInvalidConfiguration;
-  k_gemv<FMT, Pol, U><<<(unsigned)p.G, 64 * kGemvWaves, lds, st>>>(p);
+  const size_t park = (size_t)nseg * kGemvWaves * mrows * 16 * sizeof(float);
+  if (park > (size_t)kGemvParkBytes) return hipErrorInvalidConfiguration;
+  if ((size_t)p.G * 2 * mrows * 16 * sizeof(float) > p.ws_bytes) return hipErrorInvalidValue;
+  const size_t lds = park + (XL ? (size_t)mrows * p.x_pitch + 32 : 0);
+  k_gemv<FMT, Pol, U, XL><<<(unsigned)p.G, 64 * kGemvWaves, lds, st>>>(p);
   return hipGetLastError();
 }
 
+template <int FMT, int ACT, template <int, int, bool> class PolT, int A, int U_XL, int U_X>
+static hipError_t launch_pol(GemvParams &p, int64_t mrows, hipStream_t st) {
+  constexpr int BY = ActTraits<ACT>::BYTES;
+  p.x_pitch = stage_pitch(p.w, BY, FmtTraits<FMT>::CHUNK);
+  if (mrows * p.x_pitch + 32 <= kGemvStageBytes)
+    return launch_ranges<FMT, PolT<A, ACT, true>, U_XL, true>(p, st);
+  p.x_pitch = 0;
+  return launch_ranges<FMT, PolT<A, ACT, false>, U_X, false>(p, st);
+}
+
+// Adapters so both policies take <first, ACT, XL> template arguments.
+template <int FMT, int ACT, bool XL>
+using GenericPol = GenericPolicy<FMT, ACT, XL>;
+template <int RP, int ACT, bool XL>
+using Q4kRowsPol = Q4kRowsPolicy<ACT, RP, XL>;
+
 template <int FMT, int ACT>
 static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype,
-                                float *ws, int *cnt, hipStream_t st) {
+                                float *ws, size_t ws_bytes, int *cnt, hipStream_t st) {
   typedef FmtTraits<FMT> T;
-  constexpr int XV = (ACT == DIALQ_F32) ? 8 : 4;
+  constexpr int XV = (ACT == DIALQ_F32) ? 8 : 4;  // VGPRs per 8-element activation operand
+  constexpr int TV = T::LANE / 4 + ((FMT == DIALQ_FORMAT_Q4_K) ? 4 : 1) + 1;  // tile + scales + chunk
   const int rows_per_pass = (FMT == DIALQ_FORMAT_Q4_K && M <= 8) ? 8 : 16;
   for (int64_t mb = 0; mb < M; mb += rows_per_pass) {
-    const int64_t rem = M - mb;
-    GemvParams p{w, x, y, M, mb, y_dtype, 1, ws, cnt};
+    const int64_t rem = M - mb, mrows = rem < 16 ? rem : 16;
+    GemvParams p{w, x, y, M, mb, y_dtype, 1, ws, ws_bytes, 0, cnt};
     hipError_t e;
-    constexpr int generic_u = ring_depth(T::LANE / 4 + ((FMT == DIALQ_FORMAT_Q4_K) ? 4 : 1) + T::NX * XV);
     if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
       if (rem <= 4)
-        e = launch_ranges<FMT, Q4kRowsPolicy<ACT, 1>, ring_depth(8 + 4 + 2 * XV)>(p, st);
+        e = launch_pol<FMT, ACT, Q4kRowsPol, 1, ring_depth(TV), ring_depth(TV + 2 * XV)>(p, mrows, st);
       else if (rem <= 8)
-        e = launch_ranges<FMT, Q4kRowsPolicy<ACT, 2>, ring_depth(8 + 4 + 4 * XV)>(p, st);
+        e = launch_pol<FMT, ACT, Q4kRowsPol, 2, ring_depth(TV), ring_depth(TV + 4 * XV)>(p, mrows, st);
       else
-        e = launch_ranges<FMT, GenericPolicy<FMT, ACT>, generic_u>(p, st);
+        e = launch_pol<FMT, ACT, GenericPol, FMT, ring_depth(TV), ring_depth(TV + T::NX * XV)>(p, mrows, st);
     } else {
-      e = launch_ranges<FMT, GenericPolicy<FMT, ACT>, generic_u>(p, st);
+      e = launch_pol<FMT, ACT, GenericPol, FMT, ring_depth(TV), ring_depth(TV + T::NX * XV)>(p, mrows, st);
     }
     if (e != hipSuccess) return e;
   }
@@ -443,26 +568,26 @@ size_t gemv_workspace_bytes(const WeightView &w, int64_t M) {
 
 template <int FMT>
 static hipError_t gemv_act(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                           int y_dtype, float *ws, int *cnt, hipStream_t st) {
+                           int y_dtype, float *ws, size_t ws_bytes, int *cnt, hipStream_t st) {
   switch (x_dtype) {
-    case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, ws, cnt, st);
-    case DIALQ_F16: return gemv_dispatch<FMT, DIALQ_F16>(w, x, M, y, y_dtype, ws, cnt, st);
-    case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, ws, cnt, st);
+    case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    case DIALQ_F16: return gemv_dispatch<FMT, DIALQ_F16>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, st);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                       int y_dtype, float *ws, int *cnt, hipStream_t st) {
+                       int y_dtype, float *ws, size_t ws_bytes, int *cnt, hipStream_t st) {
   switch (w.fmt) {
-    case DIALQ_FORMAT_W8A16: return gemv_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
-    case DIALQ_FORMAT_FP8_ROW: return gemv_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
-    case DIALQ_FORMAT_Q8_0: return gemv_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
+    case DIALQ_FORMAT_W8A16: return gemv_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    case DIALQ_FORMAT_FP8_ROW: return gemv_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    case DIALQ_FORMAT_Q8_0: return gemv_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
     case DIALQ_FORMAT_FP8_BLOCK:
-      return gemv_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
-    case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
-    case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
-    case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, ws, cnt, st);
+      return gemv_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
   }
   return hipErrorInvalidValue;
 }

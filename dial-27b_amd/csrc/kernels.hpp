@@ -51,7 +51,7 @@ hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int6
 // be smaller than 2 GiB (32-bit buffer offsets).
 size_t gemv_workspace_bytes(const WeightView &w, int64_t M);
 hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                       int y_dtype, float *ws, int *cnt, hipStream_t st);
+                       int y_dtype, float *ws, size_t ws_bytes, int *cnt, hipStream_t st);
 // Prefill GEMM with weight-only dequantization (bf16 / f16 MFMA operands).
 hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
                        int y_dtype, hipStream_t st);

@@ -138,6 +138,24 @@ __device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ uint32_t bload1(rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
 }
+// Streaming variants (cache policy nt) for data read once per launch: the
+// resident weight tiles and their scales.
+constexpr int kNT = 2;
+// Device-coherent read (cache policy sc1) of data other workgroups wrote
+// with agent-scope stores.
+constexpr int kSC1 = 16;
+__device__ __forceinline__ u32x4 sload16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kNT));
+}
+__device__ __forceinline__ uint32_t sload4(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kNT);
+}
+__device__ __forceinline__ uint32_t sload2(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, kNT);
+}
+__device__ __forceinline__ uint32_t sload1(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, kNT);
+}
 
 // Raw activation bytes for one 8-element operand (16 B for bf16/f16, 32 B
 // for f32), converted to operand parts at use time.
