@@ -85,7 +85,7 @@ struct Linear {
   DevBuf tiles, aux, row_scale, block_scale;
   DevBuf scratch;  // activation codes for native prefill / local q8
   DevBuf gemv_ws;  // stream-K partials of the decode GEMV
-  DevBuf gemv_cnt; // per-strip arrival counters (zero between calls)
+  DevBuf gemv_cnt; // per-strip piece counters + work-queue head/exit count (zero between calls)
   std::mutex scratch_mu;
   float global = 1.0f;
 
@@ -209,7 +209,7 @@ Linear *alloc_linear(const dialq_linear_desc &d, int device) {
   if (d.format == DIALQ_FORMAT_NVFP4) {
     L->global = (d.flags & DIALQ_FLAG_GLOBAL_IS_DIVISOR) ? 1.0f / d.global_scale : d.global_scale;
   }
-  L->gemv_cnt.alloc((size_t)L->n_strips * sizeof(int));
+  L->gemv_cnt.alloc((size_t)(L->n_strips + 2) * sizeof(int));  // strips, queue head, exit count
   hip_check(hipMemset(L->gemv_cnt.p, 0, L->gemv_cnt.n), "hipMemset");
   return L;
 }

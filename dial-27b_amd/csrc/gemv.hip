@@ -39,6 +39,7 @@ struct GemvParams {
   int64_t m_base;  // first row handled by this launch
   int y_dtype;
   int G;           // workgroups (tile ranges)
+  int spw;         // > 0: range b = strips b*spw .. (b+1)*spw-1 (no strip shared)
   float *ws;       // [G][2][mrows][16] partials of shared strips
   size_t ws_bytes;
   int x_pitch;     // bytes per staged activation row (0: not staged)
@@ -290,7 +291,14 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
   const int b = blockIdx.x;
   const int kc = (int)w.k_chunks;
   const int64_t total = w.n_strips * w.k_chunks;
-  const int lo = (int)(((int64_t)b * total) / p.G), hi = (int)(((int64_t)(b + 1) * total) / p.G);
+  int lo, hi;
+  if (p.spw > 0) {
+    lo = b * p.spw * kc;
+    hi = (int)((int64_t)(b + 1) * p.spw * kc < total ? (int64_t)(b + 1) * p.spw * kc : total);
+  } else {
+    lo = (int)(((int64_t)b * total) / p.G);
+    hi = (int)(((int64_t)(b + 1) * total) / p.G);
+  }
   const int s_first = lo / kc;
   const int nseg = (hi > lo) ? (hi - 1) / kc - s_first + 1 : 0;
   const int mrows = (int)((p.M - p.m_base) < 16 ? (p.M - p.m_base) : 16);
@@ -455,6 +463,330 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Dynamic GEMV kernel.  Work is cut into units -- piece p of strip s, the
+// chunks [p*cpp, min((p+1)*cpp, kc)) with cpp <= W*U, i.e. at most one ring
+// cycle per wave -- handed out at run time, so faster CUs take more units and
+// every CU finishes together.  A workgroup has W compute waves and one
+// control wave.  The compute waves stream their units' tiles through the
+// ring and, after each unit, park their accumulators in LDS and bump the
+// unit's LDS counter; they wait on nothing but their own loads and the LDS
+// unit queue.  The control wave keeps the queue kDynQueue units ahead (the
+// first kDynQueue units of workgroup b are b + j*G, later ones come from a
+// global atomic counter) and closes finished units: it adds the W parked
+// accumulators in wave order and writes the strip (one piece per strip) or
+// publishes the piece's partial; the last piece of a strip to be published
+// adds all pieces in piece order and writes the strip -- deterministic.  All
+// waits are bounded (kSpinLimit polls), so no wave can hang.
+//
+// LDS: [ctl: q[kDynQueue], ng, done[kDynQueue]][staged x][32 zero bytes]
+//      [park[kDynQueue][W][mrows][16] floats]
+// ---------------------------------------------------------------------------
+constexpr int kDynWaves = 4;   // compute waves per workgroup (plus one control wave)
+constexpr int kDynQueue = 8;   // units queued ahead per workgroup
+constexpr int kDynCtlBytes = 128;
+constexpr int kSpinLimit = 1 << 22;
+
+struct DynParams {
+  WeightView w;
+  const void *x;
+  void *y;
+  int64_t M;       // total rows of x / y
+  int64_t m_base;  // first row handled by this launch
+  int y_dtype;
+  int P;           // pieces per strip
+  int cpp;         // chunks per piece
+  int NU;          // units: n_strips * P
+  int G;           // workgroups
+  int x_pitch;     // bytes per staged activation row (0: not staged)
+  float *ws;       // [n_strips][P][mrows][16] piece partials (P > 1)
+  size_t ws_bytes;
+  int *cnt;        // [n_strips] piece counters, then queue head and exit count
+};
+
+__device__ __forceinline__ int lds_load(const int *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_store(int *p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local"); }
+__device__ __forceinline__ void lds_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local"); }
+
+// Unit u -> strip, chunk range.
+__device__ __forceinline__ void unit_range(const DynParams &p, int u, int &s, int &c0, int &c1) {
+  s = u / p.P;
+  c0 = (u - s * p.P) * p.cpp;
+  const int e = c0 + p.cpp, kc = (int)p.w.k_chunks;
+  c1 = e < kc ? e : kc;
+}
+
+// Control wave: add the W parked accumulators of park slot k (wave order).
+__device__ __forceinline__ void reduce_park(const float *park_k, int slot_floats, float (&v)[4]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = lane + 64 * q;
+    float a = 0.0f;
+    if (e < slot_floats)
+      for (int ww = 0; ww < kDynWaves; ++ww) a += park_k[ww * slot_floats + e];
+    v[q] = a;
+  }
+}
+
+// Control wave: write rows m < mrows of strip s (16 outputs per row).
+template <int FMT>
+__device__ __forceinline__ void store_strip(const DynParams &p, int s, int slot_floats, const float (&v)[4]) {
+  const WeightView &w = p.w;
+  const int lane = threadIdx.x & 63, r = lane & 15;
+  const int64_t n = (int64_t)s * 16 + r;
+  const float scale = epilogue_scale<FMT>(w, n < w.N ? n : w.N - 1);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = lane + 64 * q, m = e >> 4;
+    if (e < slot_floats && n < w.N) store_out(p.y, (p.m_base + m) * w.N + n, p.y_dtype, v[q] * scale);
+  }
+}
+
+// Control wave: all P pieces of strip s are published -- add them in piece
+// order (device-coherent loads, eight pieces per batch), write the strip and
+// rearm its counter.
+template <int FMT>
+__device__ void finish_strip(const DynParams &p, int s, int slot_floats) {
+  const int lane = threadIdx.x & 63;
+  const rsrc_t rw = make_rsrc(p.ws + (size_t)s * p.P * slot_floats, (uint32_t)((size_t)p.P * slot_floats * 4));
+  float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int b0 = 0; b0 < p.P; b0 += 8) {
+    float pv[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = lane + 64 * q;
+        const uint32_t off = (b0 + i < p.P && e < slot_floats) ? (uint32_t)(((b0 + i) * slot_floats + e) * 4) : kOOB;
+        pv[i][q] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, (int)off, 0, kSC1));
+      }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[q] += pv[i][q];
+  }
+  store_strip<FMT>(p, s, slot_floats, a);
+  if (lane == 0) __hip_atomic_store(&p.cnt[s], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Control wave main loop.  Each round: close every unit all compute waves
+// have finished (in queue order): one piece per strip -> write the strip;
+// otherwise publish the piece's partial with agent-scope stores.  Then, in
+// one memory round trip after the stores have completed, count the
+// published pieces in (one lane per piece) and grab as many units as there
+// are free queue slots; the last piece of a strip to be counted adds up the
+// strip.
+template <int FMT>
+__device__ void control_wave(const DynParams &p, int *q, int *ng, int *done, const float *park, int mrows) {
+  constexpr int W = kDynWaves, QD = kDynQueue;
+  const int lane = threadIdx.x & 63;
+  const int slot_floats = mrows * 16;
+  int *head = p.cnt + p.w.n_strips, *exits = head + 1;
+  int nq = QD, nclosed = 0, spin = 0;
+  bool exhausted = false, end = false;
+  for (int j = 0; j < QD; ++j) exhausted = exhausted || (lds_load(&q[j]) < 0);
+  int pend = -1, npend = 0;  // lane i < npend holds the strip of published piece i
+  while (true) {
+    bool prog = false;
+    while (!end && nclosed < nq) {
+      const int k = nclosed % QD;
+      const int u = lds_load(&q[k]);
+      if (u < 0) {
+        end = true;
+        break;
+      }
+      if (lds_load(&done[k]) != W) break;
+      lds_acquire();
+      float v[4];
+      reduce_park(park + (size_t)k * W * slot_floats, slot_floats, v);
+      const int s = u / p.P;
+      if (p.P == 1) {
+        store_strip<FMT>(p, s, slot_floats, v);
+      } else {
+        float *mine = p.ws + ((size_t)u) * slot_floats;  // u = s * P + piece
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int e = lane + 64 * qq;
+          if (e < slot_floats) __hip_atomic_store(&mine[e], v[qq], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        pend = (lane == npend) ? s : pend;
+        ++npend;
+      }
+      lds_store(&done[k], 0);
+      ++nclosed;
+      prog = true;
+    }
+    const int want = exhausted ? 0 : nclosed + QD - nq;
+    if (npend > 0 || want > 0) {
+      __builtin_amdgcn_s_waitcnt(0);  // published partials have landed
+      int old = 0;
+      if (lane < npend) old = __hip_atomic_fetch_add(&p.cnt[pend], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 63 && want > 0) old = __hip_atomic_fetch_add(head, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (want > 0) {
+        const int h = __builtin_amdgcn_readlane(old, 63) + QD * p.G;
+        for (int j = 0; j < want; ++j) {
+          int u = h + j;
+          if (u >= p.NU) {
+            u = -1;
+            exhausted = true;
+          }
+          lds_store(&q[nq % QD], u);
+          ++nq;
+          if (u < 0) break;
+        }
+        lds_release();
+        lds_store(ng, nq);
+      }
+      for (int i = 0; i < npend; ++i)
+        if (__builtin_amdgcn_readlane(old, i) == p.P - 1) finish_strip<FMT>(p, __builtin_amdgcn_readlane(pend, i), slot_floats);
+      npend = 0;
+      pend = -1;
+      prog = true;
+    }
+    if (end && npend == 0) break;
+    if (prog) {
+      spin = 0;
+    } else {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spin > kSpinLimit) break;
+    }
+  }
+  // The last workgroup out resets the queue for the next launch.
+  if (lane == 0 && __hip_atomic_fetch_add(exits, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.G - 1) {
+    __hip_atomic_store(head, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(exits, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <int FMT, typename Pol, int U, bool XL>
+__global__ __launch_bounds__(64 * (kDynWaves + 1)) void k_gemv_dyn(DynParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int W = kDynWaves, QD = kDynQueue;
+  constexpr int BY = ActTraits<Pol::XACT>::BYTES;
+  const WeightView &w = p.w;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = blockIdx.x;
+  const int mrows = (int)((p.M - p.m_base) < 16 ? (p.M - p.m_base) : 16);
+  const int slot_floats = mrows * 16;
+  int *q = (int *)smem;       // [QD] unit of each queued ordinal (-1: no more)
+  int *ng = q + QD;           // ordinals queued so far
+  int *done = q + QD + 1;     // [QD] waves finished with the unit in each slot
+  uint8_t *xbase = smem + kDynCtlBytes;
+  float *park = (float *)(xbase + (XL ? mrows * p.x_pitch + 32 : 0));
+
+  Ctx cx;
+  cx.mrows = mrows;
+  cx.K = (int)w.K;
+  cx.pitch = p.x_pitch;
+  cx.xl = (const lds_u8 *)xbase;
+  cx.zero = (const lds_u8 *)xbase + (XL ? mrows * p.x_pitch : 0);
+  const int64_t total = w.n_strips * w.k_chunks;
+  cx.rt = make_rsrc(w.tiles, (uint32_t)(total * 64 * FmtTraits<FMT>::LANE));
+  cx.ra = cx.rt;
+  if constexpr (FMT == DIALQ_FORMAT_Q8_0 || FMT == DIALQ_FORMAT_MXFP4)
+    cx.ra = make_rsrc(w.aux, (uint32_t)(total * 64));
+  else if constexpr (FMT == DIALQ_FORMAT_Q4_K)
+    cx.ra = make_rsrc(w.aux, (uint32_t)(total * 256));
+  else if constexpr (FMT == DIALQ_FORMAT_NVFP4)
+    cx.ra = make_rsrc(w.aux, (uint32_t)(total * 128));
+  else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK)
+    cx.ra = make_rsrc(w.block_scale, (uint32_t)(((w.N + 127) / 128) * w.nbk * 4));
+  cx.rx = make_rsrc((const uint8_t *)p.x + p.m_base * w.K * BY, (uint32_t)(mrows * w.K * BY));
+
+  // Queue the statically assigned first units; clear the counters.
+  if (threadIdx.x < QD) {
+    const int u = b + (int)threadIdx.x * p.G;
+    lds_store(&q[threadIdx.x], u < p.NU ? u : -1);
+    lds_store(&done[threadIdx.x], 0);
+  }
+  if (threadIdx.x == 0) lds_store(ng, QD);
+  if constexpr (XL) {
+    if (wave < W) {
+      // Stage x: 1 KB per DMA instruction (lane l -> bytes 16l..16l+15 of the
+      // block); bytes at or past K*BY read as zeros, which pads every row.
+      const int row_bytes = w.K * BY;
+      const int blocks = p.x_pitch >> 10;
+      for (int i = wave; i < mrows * blocks; i += W) {
+        const int m = i / blocks, kb = (i - m * blocks) << 10;
+        const int col = kb + lane * 16;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(cx.rx, (__attribute__((address_space(3))) void *)(xbase + m * p.x_pitch + kb),
+                                                  16, col < row_bytes ? m * row_bytes + col : (int)kOOB, 0, 0, 0);
+      }
+    }
+    if (threadIdx.x < 2) *(u32x4 __attribute__((address_space(3))) *)(xbase + mrows * p.x_pitch + 16 * threadIdx.x) = (u32x4){0, 0, 0, 0};
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  lds_barrier();  // queue and counters initialised
+
+  if (wave == W) {
+    lds_barrier();  // pairs with the compute waves' second barrier
+    control_wave<FMT>(p, q, ng, done, park, mrows);
+    return;
+  }
+
+  // ---- compute waves ---------------------------------------------------
+  typename Pol::Slot ring[U];
+  bool valid[U];
+  int cur = lds_load(&q[0]);
+  {
+    int s = 0, c0 = 0, c1 = 0;
+    if (cur >= 0) unit_range(p, cur, s, c0, c1);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + wave + W * u;
+      valid[u] = cur >= 0 && c < c1;
+      Pol::fill(ring[u], w, cx, s, valid[u] ? c : 0, valid[u], lane);
+    }
+  }
+  lds_barrier();  // staged x visible (waits for this wave's DMA, not its ring)
+  typename Pol::Acc acc;
+  Pol::zero(acc);
+  int ord = 0;
+  while (cur >= 0) {
+    // next unit: wait until the control wave has queued ordinal ord + 1
+    int spin = 0;
+    while (lds_load(ng) <= ord + 1) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spin > kSpinLimit) break;
+    }
+    lds_acquire();
+    const int nxt = (spin > kSpinLimit) ? -1 : lds_load(&q[(ord + 1) % QD]);
+    int s = 0, c0 = 0, c1 = 0;
+    if (nxt >= 0) unit_range(p, nxt, s, c0, c1);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (valid[u]) Pol::compute(ring[u], acc, cx);
+      const int c = c0 + wave + W * u;
+      valid[u] = nxt >= 0 && c < c1;
+      Pol::fill(ring[u], w, cx, s, valid[u] ? c : 0, valid[u], lane);
+    }
+    // park this wave's share of unit `cur` and count it in
+    {
+      constexpr int NV = Pol::NV;
+      const int r = lane & 15;
+      float v[NV];
+      int mrow[NV];
+      Pol::values(acc, v, mrow, lane);
+      float *dst = park + ((size_t)(ord % QD) * W + wave) * slot_floats;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (mrow[i] < mrows) dst[mrow[i] * 16 + r] = v[i];
+      lds_release();
+      if (lane == 0) __hip_atomic_fetch_add(&done[ord % QD], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    Pol::zero(acc);
+    cur = nxt;
+    ++ord;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host dispatch
 // ---------------------------------------------------------------------------
 static int device_cus() {
@@ -500,29 +832,67 @@ static int stage_pitch(const WeightView &w, int by, int chunk) {
   return (int)(((kpad_bytes + 1023) / 1024) * 1024 + 64);
 }
 
+// Whole strips per range when there are enough strips to give every CU
+// about kGemvWgPerCu ranges of equal size (no strip is shared, so no
+// cross-workgroup fix-up); 0 selects equal tile ranges (stream-K).
+static int gemv_spw(const WeightView &w, int64_t mrows) {
+  const int64_t target = (int64_t)kGemvWgPerCu * device_cus();
+  if (w.n_strips < device_cus()) return 0;
+  int64_t spw = (w.n_strips + target / 2) / target;
+  if (spw < 1) spw = 1;
+  const int64_t seg_cap = kGemvParkBytes / (kGemvWaves * mrows * 16 * 4);
+  if (spw > seg_cap) spw = seg_cap;
+  return (int)spw;
+}
+
 template <int FMT, typename Pol, int U, bool XL>
 static hipError_t launch_ranges(GemvParams &p, hipStream_t st) {
   const int64_t mrows = (p.M - p.m_base) < 16 ? (p.M - p.m_base) : 16;
-  p.G = gemv_grid(p.w, mrows);
   const int64_t total = p.w.n_strips * p.w.k_chunks;
-  const int64_t per = (total + p.G - 1) / p.G;
-  const int64_t nseg = per / p.w.k_chunks + 2;
+  p.spw = gemv_spw(p.w, mrows);
+  p.G = p.spw > 0 ? (int)((p.w.n_strips + p.spw - 1) / p.spw) : gemv_grid(p.w, mrows);
+  const int64_t per = p.spw > 0 ? p.spw * p.w.k_chunks : (total + p.G - 1) / p.G;
+  const int64_t nseg = p.spw > 0 ? p.spw : per / p.w.k_chunks + 2;
   const size_t park = (size_t)nseg * kGemvWaves * mrows * 16 * sizeof(float);
   if (park > (size_t)kGemvParkBytes) return hipErrorInvalidConfiguration;
-  if ((size_t)p.G * 2 * mrows * 16 * sizeof(float) > p.ws_bytes) return hipErrorInvalidValue;
+  if (p.spw == 0 && (size_t)p.G * 2 * mrows * 16 * sizeof(float) > p.ws_bytes) return hipErrorInvalidValue;
   const size_t lds = park + (XL ? (size_t)mrows * p.x_pitch + 32 : 0);
   k_gemv<FMT, Pol, U, XL><<<(unsigned)p.G, 64 * kGemvWaves, lds, st>>>(p);
   return hipGetLastError();
 }
 
+template <int FMT, typename Pol, int U, bool XL>
+static hipError_t launch_dyn(DynParams &p, int64_t mrows, hipStream_t st) {
+  const int kc = (int)p.w.k_chunks;
+  p.P = (kc + kDynWaves * U - 1) / (kDynWaves * U);
+  p.cpp = (kc + p.P - 1) / p.P;
+  p.NU = (int)(p.w.n_strips * p.P);
+  p.G = kGemvWgPerCu * device_cus();
+  if (p.G > p.NU) p.G = p.NU;
+  const size_t need = p.P > 1 ? (size_t)p.w.n_strips * p.P * mrows * 16 * sizeof(float) : 0;
+  if (need > p.ws_bytes) return hipErrorInvalidValue;
+  const size_t lds = kDynCtlBytes + (XL ? (size_t)mrows * p.x_pitch + 32 : 0) +
+                     (size_t)kDynQueue * kDynWaves * mrows * 16 * sizeof(float);
+  k_gemv_dyn<FMT, Pol, U, XL><<<(unsigned)p.G, 64 * (kDynWaves + 1), lds, st>>>(p);
+  return hipGetLastError();
+}
+
+// Matrices with at least one strip per CU: static whole-strip ranges (no
+// strip shared between workgroups).  Smaller ones: the dynamic kernel, whose
+// small units keep every CU busy.
 template <int FMT, int ACT, template <int, int, bool> class PolT, int A, int U_XL, int U_X>
-static hipError_t launch_pol(GemvParams &p, int64_t mrows, hipStream_t st) {
+static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
   constexpr int BY = ActTraits<ACT>::BYTES;
-  p.x_pitch = stage_pitch(p.w, BY, FmtTraits<FMT>::CHUNK);
-  if (mrows * p.x_pitch + 32 <= kGemvStageBytes)
-    return launch_ranges<FMT, PolT<A, ACT, true>, U_XL, true>(p, st);
-  p.x_pitch = 0;
-  return launch_ranges<FMT, PolT<A, ACT, false>, U_X, false>(p, st);
+  const bool xl = mrows * stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) + 32 <= kGemvStageBytes;
+  if (d.w.n_strips >= device_cus()) {
+    GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
+    p.x_pitch = xl ? stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) : 0;
+    if (xl) return launch_ranges<FMT, PolT<A, ACT, true>, U_XL, true>(p, st);
+    return launch_ranges<FMT, PolT<A, ACT, false>, U_X, false>(p, st);
+  }
+  d.x_pitch = xl ? stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) : 0;
+  if (xl) return launch_dyn<FMT, PolT<A, ACT, true>, U_XL, true>(d, mrows, st);
+  return launch_dyn<FMT, PolT<A, ACT, false>, U_X, false>(d, mrows, st);
 }
 
 // Adapters so both policies take <first, ACT, XL> template arguments.
@@ -540,7 +910,7 @@ static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, v
   const int rows_per_pass = (FMT == DIALQ_FORMAT_Q4_K && M <= 8) ? 8 : 16;
   for (int64_t mb = 0; mb < M; mb += rows_per_pass) {
     const int64_t rem = M - mb, mrows = rem < 16 ? rem : 16;
-    GemvParams p{w, x, y, M, mb, y_dtype, 1, ws, ws_bytes, 0, cnt};
+    DynParams p{w, x, y, M, mb, y_dtype, 1, 1, 1, 1, 0, ws, ws_bytes, cnt};
     hipError_t e;
     if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
       if (rem <= 4)
@@ -558,12 +928,10 @@ static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, v
 }
 
 size_t gemv_workspace_bytes(const WeightView &w, int64_t M) {
-  size_t most = 0;
-  for (int64_t mrows = 1; mrows <= 16 && mrows <= M; ++mrows) {
-    const size_t b = (size_t)gemv_grid(w, mrows) * 2 * (size_t)mrows * 16 * sizeof(float);
-    if (b > most) most = b;
-  }
-  return most;
+  // pieces per strip are at most ceil(k_chunks / (kDynWaves * 2)) (ring depth >= 2)
+  const int64_t mrows = M < 16 ? M : 16;
+  const int64_t pmax = (w.k_chunks + kDynWaves * 2 - 1) / (kDynWaves * 2);
+  return (size_t)w.n_strips * pmax * mrows * 16 * sizeof(float);
 }
 
 template <int FMT>

@@ -46,7 +46,7 @@ hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int6
                             uint8_t *packed, uint8_t *scales, hipStream_t st);
 
 // Decode GEMV: y[M,N] = x[M,K] W^T for any M (16 rows per pass).
-// ws: gemv_workspace_bytes(w, M) of scratch; cnt: n_strips ints that are
+// ws: gemv_workspace_bytes(w, M) of scratch; cnt: n_strips + 2 ints that are
 // zero before the call and are left zero after it.  The resident tiles must
 // be smaller than 2 GiB (32-bit buffer offsets).
 size_t gemv_workspace_bytes(const WeightView &w, int64_t M);

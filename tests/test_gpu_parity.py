@@ -126,6 +126,19 @@ def test_gemv_parity(fmt, x_dtype, torch_dev):
 
 
 @pytest.mark.parametrize("fmt", ALL_FORMATS, ids=lambda f: dq.FORMAT_NAMES[f])
+def test_gemv_parity_whole_strip_ranges(fmt, torch_dev):
+    """Enough 16-row strips (301, the last one ragged) that every workgroup
+    takes whole strips, for staged (small K) and ring-fetched (large M)
+    activations."""
+    n, k = 16 * 300 + 7, 512
+    lin, _, _, deq = _linear(fmt, n, k, seed=25 + fmt)
+    for m, x_dtype in ((1, dq.BF16), (2, dq.F32), (5, dq.F16), (16, dq.BF16), (17, dq.BF16)):
+        y_dtype = dq.F16 if x_dtype == dq.F16 else dq.BF16
+        rel = _run(lin, deq, m, x_dtype, y_dtype, dq.PATH_GEMV, torch_dev, seed=m)
+        assert rel <= TOL_BF16, (dq.FORMAT_NAMES[fmt], m, rel)
+
+
+@pytest.mark.parametrize("fmt", ALL_FORMATS, ids=lambda f: dq.FORMAT_NAMES[f])
 def test_gemv_f32_output(fmt, torch_dev):
     n, k = 64, 256
     lin, _, _, deq = _linear(fmt, n, k, seed=30 + fmt)
