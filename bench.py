@@ -7,13 +7,18 @@ are N(0, 0.02), quantized on the GPU by the library's own quantizers;
 activations are bf16 N(0, 1).
 
 A step is one decode pass (M = 1) over the layer's seven linears in W8A16
-(int8 per row + bf16 scale).  Layer copies rotate so the weight working set
-(COPIES x 341 MB) exceeds the 256 MB Infinity Cache and the figure measures
-HBM.  `value` = algorithmic weight bytes streamed / wall time of the timed
-steps, in GB/s.  Extra keys report the same decode for Q4_K / FP8-128 /
-MXFP4, the prefill GEMM TFLOP/s (W8A16 and Q4_K at M = 2048, FP8-128 and
-MXFP4 native at M = 1024), the roofline of the dominant kernel and the CPU
-baseline.
+(int8 per row + bf16 scale), captured once per layer copy in a HIP graph
+and replayed (the serving loop's launch path; no host work per linear).
+Layer copies rotate so the weight working set (COPIES x 341 MB) exceeds the
+256 MB Infinity Cache and the figure measures HBM.  `value` = algorithmic
+weight bytes streamed / wall time of the timed steps, in GB/s.  Extra keys
+report the same decode for Q4_K / FP8-128 / MXFP4, the prefill GEMM TFLOP/s
+(W8A16 and Q4_K at M = 2048, FP8-128 and MXFP4 native at M = 1024), the
+roofline of the dominant kernel and the CPU baseline.
+
+`--profile` runs only the dominant kernel (W8A16 gate GEMV, eager launches
+over rotating copies) plus a 256 MiB device-to-device copy used to scale the
+HBM byte counters; it is the program the committed rocprofv3 summaries run.
 """
 from __future__ import annotations
 
@@ -44,7 +49,38 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--sweep", default="w8a16,q4_k,fp8_block,mxfp4",
                     help="formats for the extra decode / prefill numbers ('' = none)")
+    ap.add_argument("--profile", action="store_true",
+                    help="only the dominant kernel's launches and the calibration copy (for rocprofv3)")
+    ap.add_argument("--profile-launches", type=int, default=50)
     return ap.parse_args()
+
+
+DOM = ("gate", 17408, 5120)   # the layer's largest linear (gate/up/down tie on bytes)
+DOM_COPIES = 6                # 6 x 89 MB rotated: beyond the 256 MB Infinity Cache
+
+
+def capture(torch, fn):
+    """Capture fn(stream) into a HIP graph (torch.cuda.CUDAGraph)."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn(torch.cuda.current_stream())
+    return g
+
+
+def read_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed PMC
+    summary (profiles/gemv_w8a16_gate_17408x5120_traffic.txt), if present."""
+    path = os.path.join(ROOT, "profiles", "gemv_w8a16_gate_17408x5120_traffic.txt")
+    try:
+        vals = {}
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch") or line.startswith("fetch_bytes") or \
+               line.startswith("write_bytes"):
+                k, v = line.split("=", 1)
+                vals[k.strip()] = float(v.split()[0])
+        return vals
+    except (OSError, ValueError):
+        return None
 
 
 def build_layers(dq, torch, fmt, copies, dev, seed=0):
@@ -71,38 +107,79 @@ def decode_pass(dq, lins, xs, ys, stream):
 
 
 def time_decode(dq, torch, layers, steps, warmup, dev):
-    """Wall time of `steps` decode passes (rotating layer copies)."""
-    stream = torch.cuda.current_stream()
+    """Wall time of `steps` decode passes, one HIP-graph replay per pass,
+    rotating layer copies."""
     xs = [torch.randn(1, k, device=dev).to(torch.bfloat16) for _, n, k in LAYER_27B]
     ys = [torch.empty(1, n, device=dev, dtype=torch.bfloat16) for _, n, k in LAYER_27B]
+    stream = torch.cuda.current_stream()
+    for lins in layers:  # eager first: sizes the GEMV workspaces outside capture
+        decode_pass(dq, lins, xs, ys, stream)
+    torch.cuda.synchronize()
+    graphs = [capture(torch, lambda st, l=lins: decode_pass(dq, l, xs, ys, st)) for lins in layers]
     for i in range(warmup):
-        decode_pass(dq, layers[i % len(layers)], xs, ys, stream)
+        graphs[i % len(graphs)].replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        decode_pass(dq, layers[i % len(layers)], xs, ys, stream)
+        graphs[i % len(graphs)].replay()
     torch.cuda.synchronize()
     return time.perf_counter() - t0
 
 
-def time_per_linear(dq, torch, layers, dev, reps=60):
-    """Average device time of each linear's GEMV launch (HIP events on the
-    stream the kernels are launched on)."""
+def time_launches(dq, torch, lins, k, n, dev, reps=60):
+    """Average device time of one GEMV launch: `reps` launches over the
+    rotating `lins` captured in a graph, bracketed by HIP events on the
+    stream the graph (and so every kernel) runs on."""
+    x = torch.randn(1, k, device=dev).to(torch.bfloat16)
+    y = torch.empty(1, n, device=dev, dtype=torch.bfloat16)
     stream = torch.cuda.current_stream()
+    for lin in lins:
+        lin.forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+    torch.cuda.synchronize()
+
+    def body(st):
+        for i in range(reps):
+            lins[i % len(lins)].forward(x, y, rows=1, path=dq.PATH_GEMV, stream=st)
+    g = capture(torch, body)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    g.replay()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e-3  # seconds per launch
+
+
+def time_per_linear(dq, torch, layers, dev):
     out = {}
     for li, (name, n, k) in enumerate(LAYER_27B):
-        x = torch.randn(1, k, device=dev).to(torch.bfloat16)
-        y = torch.empty(1, n, device=dev, dtype=torch.bfloat16)
-        for i in range(5):
-            layers[i % len(layers)][li].forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(reps):
-            layers[i % len(layers)][li].forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
-        e1.record(stream)
-        e1.synchronize()
-        out[name] = e0.elapsed_time(e1) / reps * 1e-3  # seconds per launch
+        out[name] = time_launches(dq, torch, [l[li] for l in layers], k, n, dev)
     return out
+
+
+def profile_run(dq, torch, dev, launches):
+    """Dominant kernel only, eager launches, plus the calibration copy."""
+    name, n, k = DOM
+    g = torch.Generator(device=dev).manual_seed(7)
+    lins = []
+    for _ in range(DOM_COPIES):
+        w = torch.randn(n, k, device=dev, generator=g, dtype=torch.float32) * 0.02
+        lins.append(dq.Linear.quantize(dq.W8A16, w, scale_dtype=dq.BF16))
+        del w
+    x = torch.randn(1, k, device=dev).to(torch.bfloat16)
+    y = torch.empty(1, n, device=dev, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream()
+    for i in range(launches):
+        lins[i % DOM_COPIES].forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+    torch.cuda.synchronize()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"# profile: {launches} launches of W8A16 {name} [{n}x{k}] M=1; 3 copies of 256 MiB "
+          "(calibration: 268435456 bytes read and written per copy)", flush=True)
 
 
 def time_prefill(dq, torch, lins, m, iters, dev, path):
@@ -159,6 +236,9 @@ def main():
     import dialq as dq
 
     dev = torch.device("cuda:0")
+    if a.profile:
+        profile_run(dq, torch, dev, a.profile_launches)
+        return
     fmt_of = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}
 
     # ---- headline: W8A16 decode over the 27B layer -----------------------
@@ -167,11 +247,21 @@ def main():
     lbytes = layer_bytes(dq, dq.W8A16)
     value = lbytes * a.steps / secs / 1e9
     per = time_per_linear(dq, torch, layers, dev)
-    # dominant kernel: the GEMV launch with the largest device time per layer
-    dom = max(per, key=per.get)
-    dn, dk = [(n, k) for name, n, k in LAYER_27B if name == dom][0]
-    dbytes = dq.raw_weight_bytes(dq.W8A16, dn, dk)
-    achieved = dbytes / per[dom] / 1e9
+    # dominant kernel: the gate GEMV (the largest linear), timed over
+    # DOM_COPIES rotating copies so no launch finds its weight in the cache
+    dom, dn, dk = DOM
+    gd = torch.Generator(device=dev).manual_seed(11)
+    dlins = []
+    for _ in range(DOM_COPIES):
+        w = torch.randn(dn, dk, device=dev, generator=gd, dtype=torch.float32) * 0.02
+        dlins.append(dq.Linear.quantize(dq.W8A16, w, scale_dtype=dq.BF16))
+        del w
+    dom_secs = time_launches(dq, torch, dlins, dk, dn, dev)
+    del dlins
+    # algorithmic bytes per launch: int8 codes + bf16 row scales + x + y
+    dbytes = dq.raw_weight_bytes(dq.W8A16, dn, dk) + 2 * dk + 2 * dn
+    achieved = dbytes / dom_secs / 1e9
+    traffic = read_traffic()
     print(f"# w8a16 decode: {value:.1f} GB/s over the layer; per-launch us: "
           + ", ".join(f"{k}={v * 1e6:.1f}" for k, v in per.items()), file=sys.stderr, flush=True)
 
@@ -227,12 +317,14 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"k_gemv<W8A16> ({dom} {dn}x{dk}, M=1)",
+            "kernel": f"k_gemv W8A16 bf16 ({dom} {dn}x{dk}, M=1)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": (round(traffic["traffic_bytes_per_launch"]) if traffic else None),
+            "algorithmic_bytes": dbytes,
+            "us_per_launch": round(dom_secs * 1e6, 2),
         },
         "cpu_baseline": cpu,
         **extra,

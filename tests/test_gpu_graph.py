@@ -1,0 +1,46 @@
+"""Decode GEMV launches captured in a HIP graph (torch.cuda.CUDAGraph) and
+replayed, as a serving loop runs them: every replay must reproduce the eager
+result bit for bit, with unrelated eager work and synchronisations between
+the replays.  Covers the whole-strip kernel (>= one strip per CU) and the
+work-queue kernel (small matrices), whose queue and piece counters are reset
+by the kernels themselves (no memset nodes in the graph)."""
+import numpy as np
+import pytest
+
+import dialq as dq
+from helpers import make_weight
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("fmt", [dq.W8A16, dq.Q4_K, dq.MXFP4], ids=lambda f: dq.FORMAT_NAMES[f])
+@pytest.mark.parametrize("n", [200, 16 * 300 + 7], ids=["queue", "whole_strips"])
+def test_graph_replay_matches_eager(fmt, n, torch_dev):
+    import torch
+    k = 1024
+    raw, scales, ckw, _ = make_weight(fmt, n, k, 60 + fmt)
+    lin = dq.Linear.create(fmt, n, k, raw, scales, **ckw)
+    other = dq.Linear.create(fmt, n, k, raw, scales, **ckw)
+    for m in (1, 5):
+        x = torch.randn(m, k, device=torch_dev).to(torch.bfloat16)
+        y_eager = torch.empty(m, n, device=torch_dev, dtype=torch.bfloat16)
+        y_graph = torch.empty_like(y_eager)
+        y_other = torch.empty_like(y_eager)
+        stream = torch.cuda.current_stream()
+        lin.forward(x, y_eager, path=dq.PATH_GEMV, stream=stream)
+        lin.forward(x, y_graph, path=dq.PATH_GEMV, stream=stream)  # sizes the workspace
+        torch.cuda.synchronize()
+        ref = y_eager.cpu()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            lin.forward(x, y_graph, path=dq.PATH_GEMV, stream=torch.cuda.current_stream())
+        for rep in range(4):
+            y_graph.fill_(float("nan"))
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y_graph.cpu(), ref), (dq.FORMAT_NAMES[fmt], n, m, rep)
+            # eager work between replays, on the same weights' workspace and others
+            lin.forward(x * 2, y_other, path=dq.PATH_GEMV, stream=stream)
+            other.forward(x, y_other, path=dq.PATH_GEMV, stream=stream)
+            torch.cuda.synchronize()
+            assert np.isfinite(y_other.float().cpu().numpy()).all()
