@@ -1,7 +1,8 @@
-"""Build libdialq.so (the HIP kernels + C ABI) for gfx950, in-tree.
+"""Build libdialq.so (the HIP kernels + C ABI) for gfx950, in-tree, and the
+host operator layer above it (dial-27b_amd/host, C++ with a pybind11 module).
 
 Usage: python dial-27b_amd/build.py [--jobs N]
-Output: dial-27b_amd/lib/libdialq.so
+Output: dial-27b_amd/lib/libdialq.so, dial-27b_amd/lib/dialq_host<ext-suffix>
 """
 from __future__ import annotations
 
@@ -63,8 +64,31 @@ def build(jobs: int = 0) -> str:
     return LIB
 
 
+def build_host() -> str:
+    """g++ build of host/dial_host.cpp + host/bind.cpp into the pybind11
+    module dialq_host, linked against libdialq.so, the HIP runtime and
+    rocBLAS (RUNPATH: the library directory, then /opt/rocm/lib)."""
+    import sysconfig
+    import pybind11
+    suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    out = os.path.join(OUT, "dialq_host" + suffix)
+    host = os.path.join(HERE, "host")
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__",
+           "-I", os.path.join(HERE, "..", "include"), "-I", "/opt/rocm/include",
+           "-I", pybind11.get_include(), "-I", sysconfig.get_paths()["include"],
+           os.path.join(host, "dial_host.cpp"), os.path.join(host, "bind.cpp"),
+           "-o", out + ".tmp", "-L", OUT, "-ldialq", "-L", "/opt/rocm/lib", "-lamdhip64", "-lrocblas",
+           "-Wl,-rpath,$ORIGIN:/opt/rocm/lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host layer build failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(out + ".tmp", out)
+    return out
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=0)
     a = ap.parse_args()
     print(build(a.jobs))
+    print(build_host())

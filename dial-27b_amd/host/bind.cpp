@@ -1,0 +1,132 @@
+// Python bindings of the host operator layer (dial_host.hpp), for tests.
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include "dial_host.hpp"
+
+namespace py = pybind11;
+using namespace dial;
+
+namespace {
+
+DType dtype_of_array(const py::array &a, std::optional<DType> hint) {
+  if (hint) return *hint;
+  const py::dtype d = a.dtype();
+  if (d.is(py::dtype::of<float>())) return DType::F32;
+  if (d.kind() == 'f' && d.itemsize() == 2) return DType::F16;
+  if (d.is(py::dtype::of<uint8_t>())) return DType::U8;
+  throw Error("pass dtype= for host arrays of " + std::string(py::str(d)));
+}
+
+Tensor tensor_from_numpy(const py::array &a, std::optional<DType> dtype) {
+  const DType t = dtype_of_array(a, dtype);
+  py::array c = py::array::ensure(a, py::array::c_style);
+  if ((size_t)c.itemsize() != dtype_size(t)) throw Error("array item size does not match the dtype");
+  std::vector<int64_t> dims(c.shape(), c.shape() + c.ndim());
+  return Tensor::from_host(c.data(), t, dims);
+}
+
+py::array tensor_to_numpy(const Tensor &t) {
+  const std::vector<uint8_t> b = t.host_bytes();
+  std::vector<py::ssize_t> shape(t.dims().begin(), t.dims().end());
+  py::dtype d = t.dtype() == DType::F32  ? py::dtype::of<float>()
+                : t.dtype() == DType::F16 ? py::dtype("float16")
+                : t.dtype() == DType::U8  ? py::dtype::of<uint8_t>()
+                                          : py::dtype::of<uint16_t>();  // BF16 bits
+  py::array out(d, shape);
+  if (!b.empty()) std::memcpy(out.mutable_data(), b.data(), b.size());
+  return out;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(dialq_host, m) {
+  m.doc() = "Host operator layer of DIAL's quantized linear (C++ above the dialq C ABI)";
+  py::register_exception<Error>(m, "DialError", PyExc_RuntimeError);
+
+  py::enum_<DType>(m, "DType")
+      .value("F32", DType::F32)
+      .value("F16", DType::F16)
+      .value("BF16", DType::BF16)
+      .value("U8", DType::U8);
+
+  py::class_<Device>(m, "Device")
+      .def_static("cpu", &Device::cpu)
+      .def_static("rocm", &Device::rocm, py::arg("ordinal") = 0)
+      .def("is_rocm", &Device::is_rocm)
+      .def("__repr__", &Device::debug);
+
+  py::class_<Tensor>(m, "Tensor")
+      .def_static("from_numpy", &tensor_from_numpy, py::arg("array"), py::arg("dtype") = py::none())
+      .def("to_device", &Tensor::to_device)
+      .def("numpy", &tensor_to_numpy)
+      .def_property_readonly("dims", [](const Tensor &t) { return t.dims(); })
+      .def_property_readonly("dtype", &Tensor::dtype)
+      .def_property_readonly("device", &Tensor::device)
+      .def("reshape", &Tensor::reshape);
+
+  py::class_<Linear>(m, "Linear")
+      .def(py::init<Tensor>())
+      .def("forward", &Linear::forward)
+      .def("weight", &Linear::weight);
+
+  py::class_<VarStore>(m, "VarStore")
+      .def(py::init<DType, Device>())
+      .def("insert", &VarStore::insert)
+      .def("pp", &VarStore::pp)
+      .def("contains_tensor", &VarStore::contains_tensor)
+      .def_property_readonly("prefix", &VarStore::prefix);
+
+  py::class_<RocmQuantLinear, std::shared_ptr<RocmQuantLinear>>(m, "RocmQuantLinear")
+      .def_static("nvfp4", &RocmQuantLinear::nvfp4)
+      .def_static("fp8", &RocmQuantLinear::fp8)
+      .def("resident_bytes", &RocmQuantLinear::resident_bytes)
+      .def("forward", &RocmQuantLinear::forward);
+
+  py::enum_<Qwen38QuantLinear>(m, "Qwen38QuantLinear")
+      .value("Dense", Qwen38QuantLinear::Dense)
+      .value("Auto", Qwen38QuantLinear::Auto)
+      .value("Rocm", Qwen38QuantLinear::Rocm);
+
+  py::class_<QuantLinear>(m, "QuantLinear")
+      .def("forward", &QuantLinear::forward)
+      .def("is_quantized_rocm", &QuantLinear::is_quantized_rocm)
+      .def("dense_weight", [](const QuantLinear &q) { return q.dense_linear().weight(); });
+
+  m.def("configure_quant_linear", &configure_quant_linear);
+  m.def("quant_linear_summary", &quant_linear_summary);
+  m.def("linear_no_bias", &linear_no_bias);
+
+  py::class_<W8A16Linear, std::shared_ptr<W8A16Linear>>(m, "W8A16Linear")
+      .def_static("from_linear", &W8A16Linear::from_linear)
+      .def("forward", &W8A16Linear::forward)
+      .def("resident_bytes", &W8A16Linear::resident_bytes);
+
+  py::class_<GgufMatMul, std::shared_ptr<GgufMatMul>> gg(m, "GgufMatMul");
+  py::enum_<GgufMatMul::Kind>(gg, "Kind").value("Q8_0", GgufMatMul::Q8_0).value("Q4_K", GgufMatMul::Q4_K);
+  gg.def_static("from_blocks", &GgufMatMul::from_blocks)
+      .def_static("quantize", &GgufMatMul::quantize)
+      .def("forward", &GgufMatMul::forward)
+      .def("dequantize_f16", &GgufMatMul::dequantize_f16);
+
+  py::class_<TextLinear>(m, "TextLinear")
+      .def_static("from_dense", &TextLinear::from_dense)
+      .def_static("gguf", &TextLinear::gguf)
+      .def("forward", &TextLinear::forward)
+      .def("gguf_dequantize_f16_weight", &TextLinear::gguf_dequantize_f16_weight)
+      .def("with_gguf_fp16_prefill", &TextLinear::with_gguf_fp16_prefill)
+      .def("is_w8a16", &TextLinear::is_w8a16)
+      .def("is_gguf", &TextLinear::is_gguf)
+      .def("is_dense", &TextLinear::is_dense);
+
+  m.def("configure_worker_w8a16_from_args", &configure_worker_w8a16_from_args);
+  m.def("worker_w8a16_enabled", &worker_w8a16_enabled);
+  m.def("worker_w8a16_summary", &worker_w8a16_summary);
+  m.def("set_worker_gguf_enabled", &set_worker_gguf_enabled);
+  m.def("worker_gguf_enabled", &worker_gguf_enabled);
+  m.def("worker_gguf_prefill_for_dims", &worker_gguf_prefill_for_dims);
+  m.def("forward_worker_gguf", &forward_worker_gguf);
+  m.def("build_worker_gguf_fp16_prefill_linear", &build_worker_gguf_fp16_prefill_linear);
+  m.def("last_warning", &last_warning);
+}

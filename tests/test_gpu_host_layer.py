@@ -1,0 +1,191 @@
+"""Host operator layer on the GPU: the reference's own tests for this path,
+run through the C++ layer (which calls the C ABI; dense fallbacks multiply
+with rocBLAS).
+
+  quant.rs:527-537, 545-680   linear_no_bias loads and decodes (dense mode)
+  cuda_quant.rs:507-552       NVFP4 / FP8 quantized linears vs dense, rows {1, 7}
+  worker_w8a16.rs:483-516     W8A16 TextLinear vs dense, rows {1, 9}
+  worker_gguf.rs:636-752      Q4_K decode keeps F16; fused FP16 prefill ==
+                              separate; hybrid keeps Q4_K for one token
+"""
+import numpy as np
+import pytest
+
+import dialq.host as H
+
+pytestmark = pytest.mark.gpu
+ROCM = H.Device.rocm(0)
+
+
+def _t(a, dtype=None):
+    return H.Tensor.from_numpy(np.ascontiguousarray(a), dtype)
+
+
+def _dense_values(q):
+    return q.dense_weight().numpy().astype(np.float32).ravel().tolist()
+
+
+def _nvfp4_store(compressed, dtype=H.DType.F32):
+    vb = H.VarStore(dtype, ROCM)
+    if compressed:
+        vb.insert("layer.weight_packed", _t(np.full((1, 8), 0x92, np.uint8)))
+        vb.insert("layer.weight_global_scale", _t(np.array([4.0], np.float32)))
+    else:
+        vb.insert("layer.weight", _t(np.full((1, 8), 0x92, np.uint8)))
+        vb.insert("layer.weight_scale_2", _t(np.array([4.0], np.float32)))
+    vb.insert("layer.weight_scale", _t(np.array([[2.0]], np.float32)))
+    return vb
+
+
+def test_linear_no_bias_dense_loads(torch_dev):
+    H.configure_quant_linear(H.Qwen38QuantLinear.Dense, ROCM, H.DType.F32)
+    # quant.rs:564-594 (ModelOpt NVFP4)
+    q = H.linear_no_bias(16, 1, _nvfp4_store(False).pp("layer"))
+    assert not q.is_quantized_rocm()
+    assert _dense_values(q) == [8.0, -4.0] * 8
+    # quant.rs:650-680 (compressed-tensors, reciprocal global)
+    q = H.linear_no_bias(16, 1, _nvfp4_store(True).pp("layer"))
+    assert _dense_values(q) == [0.5, -0.25] * 8
+    # quant.rs:596-619 (FP8 with per-output scale)
+    vb = H.VarStore(H.DType.F32, ROCM)
+    vb.insert("layer.weight", _t(np.array([[1, 2], [3, 4]], np.float32)))
+    vb.insert("layer.weight_scale", _t(np.array([2.0, 0.5], np.float32)))
+    q = H.linear_no_bias(2, 2, vb.pp("layer"))
+    assert _dense_values(q) == [2.0, 4.0, 1.5, 2.0]
+    # quant.rs:621-648 (f32 scales with an F16 runtime)
+    vb = H.VarStore(H.DType.F16, ROCM)
+    vb.insert("layer.weight", _t(np.array([[1, 2], [3, 4]], np.float32)))
+    vb.insert("layer.weight_scale", _t(np.array([2.0, 0.5], np.float32)))
+    q = H.linear_no_bias(2, 2, vb.pp("layer"))
+    assert q.dense_weight().dtype == H.DType.F16
+    assert _dense_values(q) == [2.0, 4.0, 1.5, 2.0]
+    # a plain dense weight
+    vb = H.VarStore(H.DType.F32, ROCM)
+    vb.insert("layer.weight", _t(np.array([[1, 2], [3, 4]], np.float32)))
+    q = H.linear_no_bias(2, 2, vb.pp("layer"))
+    assert _dense_values(q) == [1.0, 2.0, 3.0, 4.0]
+
+
+def test_decodes_low_nibble_before_high_nibble_and_applies_group_scales(torch_dev):
+    # quant.rs:527-537: packed[0] = 0x92, packed[8] = 0x65, scales [2, 0.5], global 4
+    H.configure_quant_linear(H.Qwen38QuantLinear.Dense, ROCM, H.DType.F32)
+    packed = np.zeros((1, 16), np.uint8)
+    packed[0, 0], packed[0, 8] = 0x92, 0x65
+    vb = H.VarStore(H.DType.F32, ROCM)
+    vb.insert("l.weight", _t(packed))
+    vb.insert("l.weight_scale", _t(np.array([[2.0, 0.5]], np.float32)))
+    vb.insert("l.weight_scale_2", _t(np.array([4.0], np.float32)))
+    d = H.linear_no_bias(32, 1, vb.pp("l")).dense_weight().numpy().ravel()
+    assert (d[0], d[1], d[16], d[17]) == (8.0, -4.0, 6.0, 8.0)
+
+
+def test_auto_mode_keeps_quantized_and_matches_dense(torch_dev):
+    for compressed in (False, True):
+        H.configure_quant_linear(H.Qwen38QuantLinear.Dense, ROCM, H.DType.F16)
+        dense = H.linear_no_bias(16, 1, _nvfp4_store(compressed, H.DType.F16).pp("layer"))
+        H.configure_quant_linear(H.Qwen38QuantLinear.Auto, ROCM, H.DType.F16)
+        quant = H.linear_no_bias(16, 1, _nvfp4_store(compressed, H.DType.F16).pp("layer"))
+        assert quant.is_quantized_rocm()
+        assert H.quant_linear_summary()[0] == 1
+        x = _t(np.cos(np.arange(3 * 16) * 0.3).astype(np.float16).reshape(3, 16)).to_device(ROCM)
+        a = quant.forward(x).numpy().astype(np.float32)
+        b = dense.forward(x).numpy().astype(np.float32)
+        assert np.abs(a - b).max() <= 1e-2 * max(1.0, np.abs(b).max())
+    H.configure_quant_linear(H.Qwen38QuantLinear.Dense, ROCM, H.DType.F16)
+
+
+def test_required_mode_raises_instead_of_falling_back(torch_dev):
+    H.configure_quant_linear(H.Qwen38QuantLinear.Rocm, ROCM, H.DType.F16)
+    vb = H.VarStore(H.DType.F16, ROCM)
+    vb.insert("layer.weight", _t(np.zeros((1, 7), np.uint8)))  # wrong packed length
+    vb.insert("layer.weight_scale", _t(np.array([[0x38]], np.uint8)))
+    vb.insert("layer.weight_scale_2", _t(np.array([1.0], np.float32)))
+    with pytest.raises(H.DialError, match="invalid NVFP4 packed weight length 7"):
+        H.linear_no_bias(16, 1, vb.pp("layer"))
+    # Auto mode falls back to dense with a warning (and the length error of
+    # the dense decoder)
+    H.configure_quant_linear(H.Qwen38QuantLinear.Auto, ROCM, H.DType.F16)
+    with pytest.raises(H.DialError, match="expected 8"):
+        H.linear_no_bias(16, 1, vb.pp("layer"))
+    assert "using dense fallback" in H.last_warning()
+    H.configure_quant_linear(H.Qwen38QuantLinear.Dense, ROCM, H.DType.F16)
+
+
+def test_quant_linears_match_dense_reference(torch_dev):
+    # cuda_quant.rs:507-552
+    in_dim, out_dim = 32, 3
+    nvfp4 = H.RocmQuantLinear.nvfp4([0x22] * (out_dim * in_dim // 2), [0x38] * (out_dim * in_dim // 16),
+                                    0.5, in_dim, out_dim, ROCM)
+    fp8 = H.RocmQuantLinear.fp8([0x38] * (out_dim * in_dim), [0.5] * out_dim, in_dim, out_dim, ROCM)
+    assert nvfp4.resident_bytes() == out_dim * in_dim // 2 + out_dim * in_dim // 16 + 4
+    assert fp8.resident_bytes() == out_dim * in_dim + 4 * out_dim
+    dense = H.Linear(_t(np.full((out_dim, in_dim), 0.5, np.float16)).to_device(ROCM))
+    for rows in (1, 7):
+        x = _t(np.sin(np.arange(rows * in_dim) * 0.07).astype(np.float16).reshape(rows, in_dim)).to_device(ROCM)
+        expected = dense.forward(x).numpy().astype(np.float32)
+        for lin in (nvfp4, fp8):
+            actual = lin.forward(x).numpy().astype(np.float32)
+            assert np.abs(expected - actual).max() < 0.02
+
+
+def test_w8a16_text_linear_matches_dense_for_decode_and_prefill(torch_dev):
+    # worker_w8a16.rs:483-516
+    in_dim, out_dim = 64, 37
+    idx = np.arange(out_dim * in_dim, dtype=np.float32)
+    w = (np.sin(idx * 0.037) * 0.25 + ((idx % 11) - 5.0) * 0.002).astype(np.float16).reshape(out_dim, in_dim)
+    dense = H.Linear(_t(w).to_device(ROCM))
+    H.set_worker_gguf_enabled(False, False)
+    H.configure_worker_w8a16_from_args(True, True, ROCM, H.DType.F16)
+    lin = H.TextLinear.from_dense("test.linear", dense)
+    assert lin.is_w8a16()
+    for rows in (1, 9):
+        x = _t(np.cos(np.arange(rows * in_dim) * 0.071).astype(np.float32) * 0.5).reshape([1, rows, in_dim])
+        x = _t(x.numpy().astype(np.float16)).to_device(ROCM)
+        expected = dense.forward(x).numpy().astype(np.float32)
+        actual = lin.forward(x).numpy().astype(np.float32)
+        assert actual.shape == (1, rows, out_dim)
+        assert np.abs(expected - actual).max() < 0.04, rows
+    # W8A16 rejects F32 activations like the reference
+    with pytest.raises(H.DialError, match="W8A16 expects F16 activation, got F32"):
+        lin.forward(_t(np.zeros((1, in_dim), np.float32)).to_device(ROCM))
+    H.configure_worker_w8a16_from_args(False, True, ROCM, H.DType.F16)
+    assert H.TextLinear.from_dense("test.dense", dense).is_dense()
+
+
+def _q4k_linear(offset):
+    # worker_gguf.rs:636-647: Q4_K (2, 256) of (((i + off) % 37) - 18) / 19
+    v = ((((np.arange(512) + offset) % 37).astype(np.float32) - 18.0) / 19.0).reshape(2, 256)
+    return H.TextLinear.gguf(f"test.{offset}", H.GgufMatMul.quantize(H.GgufMatMul.Kind.Q4_K, _t(v), ROCM))
+
+
+def test_q4k_decode_keeps_f16_activations(torch_dev):
+    v = (((np.arange(512) % 37).astype(np.float32) - 18.0) / 19.0).reshape(2, 256)
+    mm = H.GgufMatMul.quantize(H.GgufMatMul.Kind.Q4_K, _t(v), ROCM)
+    x = _t(((np.arange(256) % 29 - 14.0) / 15.0).astype(np.float16).reshape(1, 1, 256)).to_device(ROCM)
+    out = H.forward_worker_gguf(mm, x)
+    assert out.dtype == H.DType.F16 and out.dims == [1, 1, 2]
+    assert np.isfinite(out.numpy().astype(np.float32)).all()
+
+
+def test_fused_fp16_prefill_matches_separate_dequantized_q4k_projections(torch_dev):
+    first, second = _q4k_linear(0), _q4k_linear(11)
+    first_dense = H.Linear(first.gguf_dequantize_f16_weight())
+    second_dense = H.Linear(second.gguf_dequantize_f16_weight())
+    fused = H.build_worker_gguf_fp16_prefill_linear("test.fused", [first, second])
+    x = _t(((np.arange(768) % 23 - 11.0) / 12.0).astype(np.float16).reshape(1, 3, 256)).to_device(ROCM)
+    expected = np.concatenate([first_dense.forward(x).numpy(), second_dense.forward(x).numpy()], axis=-1)
+    actual = fused.forward(x).numpy()
+    assert np.array_equal(actual.view(np.uint16), expected.view(np.uint16))
+
+
+def test_hybrid_linear_keeps_q4k_for_single_token_decode(torch_dev):
+    linear = _q4k_linear(7)
+    fp16 = H.Linear(linear.gguf_dequantize_f16_weight())
+    hybrid = linear.with_gguf_fp16_prefill(fp16)
+    x = _t(((np.arange(256) % 29 - 14.0) / 15.0).astype(np.float16).reshape(1, 1, 256)).to_device(ROCM)
+    expected = linear.forward(x).numpy()
+    actual = hybrid.forward(x).numpy()
+    assert np.array_equal(actual.view(np.uint16), expected.view(np.uint16))
+    # several tokens take the dense FP16 copy
+    x3 = _t(((np.arange(768) % 29 - 14.0) / 15.0).astype(np.float16).reshape(1, 3, 256)).to_device(ROCM)
+    assert np.array_equal(hybrid.forward(x3).numpy().view(np.uint16), fp16.forward(x3).numpy().view(np.uint16))

@@ -1,0 +1,93 @@
+"""Host operator layer (C++ above the C ABI), CPU-only checks: the mode gates,
+the GGUF hybrid routing rule and the error paths of linear_no_bias that fail
+before any device work.  Mirrors the reference's own tests where it has them:
+worker_gguf.rs:628-634 (hybrid routing), quant.rs:539-543 (NVFP4 length
+error); the mode gates follow quant.rs:27-62 and worker_w8a16.rs:15-44."""
+import numpy as np
+import pytest
+
+import dialq.host as H
+
+
+def test_quant_linear_mode_gate():
+    # quant.rs:27-62: the device-resident mode needs the GPU runtime
+    with pytest.raises(H.DialError, match="requires a ROCm device and --dtype f16 or bf16"):
+        H.configure_quant_linear(H.Qwen38QuantLinear.Rocm, H.Device.cpu(), H.DType.F16)
+    with pytest.raises(H.DialError, match=r"dtype=F32"):
+        H.configure_quant_linear(H.Qwen38QuantLinear.Rocm, H.Device.rocm(0), H.DType.F32)
+    H.configure_quant_linear(H.Qwen38QuantLinear.Auto, H.Device.cpu(), H.DType.F16)
+    assert H.quant_linear_summary() is None  # Auto on a CPU runtime is dense
+    H.configure_quant_linear(H.Qwen38QuantLinear.Auto, H.Device.rocm(0), H.DType.BF16)
+    assert H.quant_linear_summary() == (0, 0)
+    H.configure_quant_linear(H.Qwen38QuantLinear.Dense, H.Device.rocm(0), H.DType.F16)
+    assert H.quant_linear_summary() is None
+
+
+def test_worker_w8a16_gate():
+    # worker_w8a16.rs:15-44: GGUF takes precedence; master mode, non-GPU
+    # devices and unsupported dtypes keep dense weights
+    H.set_worker_gguf_enabled(True, False)
+    H.configure_worker_w8a16_from_args(True, True, H.Device.rocm(0), H.DType.F16)
+    assert not H.worker_w8a16_enabled()
+    assert "GGUF takes precedence" in H.last_warning()
+    H.set_worker_gguf_enabled(False, False)
+    H.configure_worker_w8a16_from_args(True, False, H.Device.rocm(0), H.DType.F16)
+    assert not H.worker_w8a16_enabled()
+    H.configure_worker_w8a16_from_args(True, True, H.Device.cpu(), H.DType.F16)
+    assert not H.worker_w8a16_enabled()
+    assert "non-ROCm device" in H.last_warning()
+    H.configure_worker_w8a16_from_args(True, True, H.Device.rocm(0), H.DType.F32)
+    assert not H.worker_w8a16_enabled()
+    assert "got F32" in H.last_warning()
+    H.configure_worker_w8a16_from_args(True, True, H.Device.rocm(0), H.DType.F16)
+    assert H.worker_w8a16_enabled()
+    assert H.worker_w8a16_summary() is not None
+    H.configure_worker_w8a16_from_args(False, True, H.Device.rocm(0), H.DType.F16)
+    assert not H.worker_w8a16_enabled()
+
+
+def test_hybrid_routing_uses_fp16_only_for_multi_token_inputs():
+    # worker_gguf.rs:628-634
+    assert not H.worker_gguf_prefill_for_dims([1, 1, 4096])
+    assert H.worker_gguf_prefill_for_dims([1, 2, 4096])
+    assert H.worker_gguf_prefill_for_dims([1, 224, 4096])
+    assert not H.worker_gguf_prefill_for_dims([1, 4096])
+
+
+def _vb(dtype=H.DType.F32):
+    return H.VarStore(dtype, H.Device.rocm(0))
+
+
+def test_rejects_invalid_nvfp4_shapes():
+    # quant.rs:539-543: 7 packed bytes for a 1 x 16 weight
+    H.configure_quant_linear(H.Qwen38QuantLinear.Dense, H.Device.rocm(0), H.DType.F32)
+    vb = _vb()
+    vb.insert("layer.weight", H.Tensor.from_numpy(np.zeros((1, 7), np.uint8)))
+    vb.insert("layer.weight_scale", H.Tensor.from_numpy(np.ones((1, 1), np.float32)))
+    vb.insert("layer.weight_scale_2", H.Tensor.from_numpy(np.ones(1, np.float32)))
+    with pytest.raises(H.DialError, match="expected 8"):
+        H.linear_no_bias(16, 1, vb.pp("layer"))
+
+
+def test_fp8_scale_count_and_representability_errors():
+    H.configure_quant_linear(H.Qwen38QuantLinear.Dense, H.Device.rocm(0), H.DType.F32)
+    vb = _vb()
+    vb.insert("layer.weight", H.Tensor.from_numpy(np.array([[1, 2], [3, 4]], np.float32)))
+    vb.insert("layer.weight_scale", H.Tensor.from_numpy(np.array([1, 2, 3], np.float32)))
+    with pytest.raises(H.DialError, match="contains 3 values, expected 1 or 2"):
+        H.linear_no_bias(2, 2, vb.pp("layer"))
+    vb2 = _vb()
+    vb2.insert("layer.weight", H.Tensor.from_numpy(np.array([[0.3, 2], [3, 4]], np.float32)))
+    vb2.insert("layer.weight_scale", H.Tensor.from_numpy(np.array([1.0], np.float32)))
+    with pytest.raises(H.DialError, match="not representable in E4M3"):
+        H.linear_no_bias(2, 2, vb2.pp("layer"))
+
+
+def test_compressed_tensors_zero_global_is_rejected():
+    H.configure_quant_linear(H.Qwen38QuantLinear.Dense, H.Device.rocm(0), H.DType.F32)
+    vb = _vb()
+    vb.insert("layer.weight_packed", H.Tensor.from_numpy(np.full((1, 8), 0x92, np.uint8)))
+    vb.insert("layer.weight_scale", H.Tensor.from_numpy(np.array([[2.0]], np.float32)))
+    vb.insert("layer.weight_global_scale", H.Tensor.from_numpy(np.array([0.0], np.float32)))
+    with pytest.raises(H.DialError, match="weight_global_scale for layer is zero"):
+        H.linear_no_bias(16, 1, vb.pp("layer"))
