@@ -14,11 +14,10 @@
 // activations and weights are prefetched into registers while the current
 // one is multiplied.
 //
-// Native kernels (k_gemm_fp8 / k_gemm_mxfp4): activations are quantized
-// first (per-token E4M3 with an f32 scale; per-32 MXFP4 with E8M0 scales)
-// and the product runs on v_mfma_scale_f32_16x16x128_f8f6f4: FP8 with unit
-// E8M0 scales and the f32 128x128 weight scale applied per chunk; MXFP4
-// with the E8M0 scales of both operands applied by the instruction.
+// Native kernel (k_gemm_native, FP8_BLOCK and MXFP4): activations are
+// quantized first (per-token E4M3 with an f32 scale; per-32 MXFP4 with E8M0
+// scales) and the product runs on v_mfma_scale_f32_32x32x64_f8f6f4, with the
+// E8M0 scales of both operands applied by the instruction.
 #include "tile_ops.hpp"
 
 namespace dialq {
@@ -40,7 +39,7 @@ struct GemmShape {
   static constexpr int KS = (CHUNK == 64 && FMT != DIALQ_FORMAT_Q8_0) ? 2 : 1;
   static constexpr int SK = KS * CHUNK;                // k per stage
   static constexpr int STRIDE = SK + 8;                // bf16 elements per LDS row
-  static constexpr int MS = (FMT == DIALQ_FORMAT_Q4_K) ? 4 : 8;  // 16-row groups per workgroup
+  static constexpr int MS = (FMT == DIALQ_FORMAT_Q4_K) ? 2 : 8;  // 16-row groups per workgroup
   static constexpr int NS = (FMT == DIALQ_FORMAT_Q4_K) ? 2 : 4;  // 16-col strips per wave
   static constexpr int ROWS = 16 * MS;
   static constexpr int BUF = PARTS * ROWS * STRIDE;   // bf16 elements per LDS buffer
@@ -352,16 +351,23 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][q][v] = 0.0f;
 
+  // Prologue in the steady state's load order (activations of stage st+1,
+  // then weights of stage st+1), so the first stage waits like every other.
   fetch_b(wb[0], 0);
-  fetch_b(wb[1], 1);
   fetch_a(0);
   store_a(0);
   fetch_a(1);
+  __builtin_amdgcn_sched_barrier(0);
+  fetch_b(wb[1], 1);
+  __builtin_amdgcn_sched_barrier(0);
 
   auto stage = [&](u32x2 (&slot)[STEPS][NQ], int st) {
     __syncthreads();  // buffer st&1 written; buffer (st+1)&1 no longer read
     store_a((st + 1) & 1);
     fetch_a(st + 2);
+    // the activation loads of stage st+2 stay ahead of this stage's weight
+    // refills, so the next stage's wait for them leaves the refills in flight
+    __builtin_amdgcn_sched_barrier(0);
     const uint16_t *base = lds + (st & 1) * BUF;
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
@@ -382,6 +388,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
           for (int q = 0; q < NQ; ++q) acc[mt][q] = mfma32(a, b[q], acc[mt][q]);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
   int st = 0;
   for (; st + 1 < nstage; st += 2) {
@@ -453,7 +460,35 @@ hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t 
 }
 
 // ===========================================================================
-// Native low-precision prefill.
+// Native low-precision prefill on v_mfma_scale_f32_32x32x64_f8f6f4.
+//
+// Activations are quantized first (per-token E4M3 with an f32 scale; per-32
+// MXFP4 with E8M0 scales).  Measured issue rates of the scaled MFMAs on
+// gfx950 (independent chains, no memory): 32x32x64 fp8 4.4 PFLOP/s and fp4
+// 8.3 PFLOP/s, against 4.1 and 4.3 for the 16x16x128 form, so the 32x32 form
+// is used for both.  Its operands: lane l holds row (A) / column (B) l % 32
+// and the 32 k values 32*(l/32) .. +31 of a 64-k step, as 32 fp8 bytes or 32
+// fp4 nibbles (low nibble first), with one E8M0 scale per lane for those 32
+// values.  A resident weight tile (16 rows x 128 k) keeps row r, k block g at
+// lane slot 16g + r, so a lane's B operand of step j is the slot
+// 16(2j + l/32) + l%16 of the tile of strip 2q + (l/16)%2: one contiguous
+// 32-byte (fp8) or 16-byte (fp4) buffer load.
+//
+// A 256-thread workgroup computes a (32*MT) x 256 tile of y: wave v owns the
+// 64 columns of strips s0 .. s0+3 (s0 = 16*tn + 4v) as two 32-column MFMA
+// tiles, and all 32*MT rows.  Activations of one 128-k chunk are staged in
+// LDS (double-buffered, one barrier per chunk) and shared by the 4 waves;
+// weights ride a two-chunk register ring, each slot refilled right after use.
+//
+// FP8_BLOCK's f32 128x128 weight scale ws_c is uniform over a wave (its 64
+// columns lie in one 128-column block).  With ws_c = m_c * 2^e_c
+// (m_c in [0.5, 1)) the accumulator R holds y / (xs[m] * mref): before chunk
+// c it is multiplied by mref / m_c (skipped when equal) and mref = m_c, and
+// the chunk's MFMAs carry 2^e_c as the weight's E8M0 scale, so
+// y = xs[m] * mref * R = xs[m] * sum_c ws_c * (xq . wq)_c with no extra
+// accumulator registers.  Chunks with ws_c == 0 contribute nothing and are
+// skipped.  The e_c of a normal f32 scale lies in [-125, 128]; scales at or
+// above 2^127 or below 2^-127 are clamped to the E8M0 range.
 // ===========================================================================
 struct NativeParams {
   WeightView w;
@@ -464,209 +499,289 @@ struct NativeParams {
   int y_dtype;
 };
 
-__device__ __forceinline__ f32x4 mfma_f8f6f4(i32x8 a, i32x8 b, f32x4 c, int sa, int sb, int fmt) {
-  if (fmt == 0)
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 4, 0, sa, 0, sb);
+template <bool FP8>
+__device__ __forceinline__ f32x16 mfma_scaled32(i32x8 a, i32x8 b, f32x16 c, int sa, int sb) {
+  if constexpr (FP8) return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
+  else return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 4, 4, 0, sa, 0, sb);
 }
 
-// FP8_BLOCK: CHUNK 128 = one weight scale block along k.
-template <int MS, int NS>
-__global__ __launch_bounds__(256) void k_gemm_fp8(NativeParams p) {
-  constexpr int ROWS = 16 * MS, STRIDE = 128 + 16;  // bytes per LDS row
-  __shared__ uint8_t lds[ROWS * STRIDE];
+#ifndef NATIVE_MT_FP8
+#define NATIVE_MT_FP8 2  // 32-row MFMA tiles per workgroup, FP8_BLOCK
+#endif
+#ifndef NATIVE_OCC_FP8
+#define NATIVE_OCC_FP8 2  // workgroups per CU the FP8_BLOCK kernel is built for
+#endif
+#ifndef NATIVE_MT_FP4
+#define NATIVE_MT_FP4 2
+#endif
+#ifndef NATIVE_OCC_FP4
+#define NATIVE_OCC_FP4 3
+#endif
+#ifndef NATIVE_DEPTH_FP8
+#define NATIVE_DEPTH_FP8 3  // chunks of weights in flight per wave (register ring slots)
+#endif
+#ifndef NATIVE_DEPTH_FP4
+#define NATIVE_DEPTH_FP4 3
+#endif
+
+template <int FMT, int MT, int OCC, int DEPTH>
+__global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
+  constexpr bool FP8 = FMT == DIALQ_FORMAT_FP8_BLOCK;
+  constexpr int ROWB = FP8 ? 128 : 64;  // activation code bytes per row and chunk
+  constexpr int STRIDE = ROWB + 16;     // padded LDS row: 16-lane b128 reads hit all 64 banks once
+  constexpr int ROWS = 32 * MT, ABUF = ROWS * STRIDE;
+  constexpr int NPIECE = ROWS * ROWB / 16, PIECES = (NPIECE + 255) / 256;
+  static_assert(NPIECE % 256 == 0, "activation pieces must fill the workgroup");
+  constexpr int TILE = FP8 ? 2048 : 1024;  // resident tile bytes
+  constexpr int BW = FP8 ? 2 : 1;          // 16-byte loads per lane and B operand
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * ABUF];
+  __shared__ uint32_t lds_s[2][256];  // MXFP4: the 4 E8M0 scales of a row's chunk (rows < ROWS)
+
   const WeightView &w = p.w;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 4, r = lane & 15;
-  const int64_t m0 = (int64_t)blockIdx.y * ROWS;
-  const int64_t s0 = (int64_t)blockIdx.x * (4 * NS) + wave * NS;
-  const int64_t kc = w.k_chunks;
-  constexpr int PIECES = ROWS * 128 / 16 / 256;  // 16-byte pieces per thread
-
-  f32x4 acc[MS][NS];
-#pragma unroll
-  for (int i = 0; i < MS; ++i)
-#pragma unroll
-    for (int j = 0; j < NS; ++j) acc[i][j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-
-  u32x4 apre[PIECES];
-  RawTile wpre[NS];
-  auto fetch = [&](int64_t c) {
-#pragma unroll
-    for (int q = 0; q < PIECES; ++q) {
-      int piece = tid + q * 256;
-      int row = piece / 8, kb = (piece % 8) * 16;
-      int64_t m = m0 + row;
-      apre[q] = m < p.M ? *(const u32x4 *)(p.xq + m * p.k_pad + c * 128 + kb) : (u32x4){0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      int64_t s = s0 + j;
-      if (s < w.n_strips) wpre[j] = load_tile<DIALQ_FORMAT_FP8_BLOCK>(w.tiles, s * kc + c, lane);
-      else wpre[j].a = wpre[j].b = (u32x4){0, 0, 0, 0};
-    }
-  };
-
-  fetch(0);
-  for (int64_t c = 0; c < kc; ++c) {
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < PIECES; ++q) {
-      int piece = tid + q * 256;
-      int row = piece / 8, kb = (piece % 8) * 16;
-      *(u32x4 *)(lds + row * STRIDE + kb) = apre[q];
-    }
-    __syncthreads();
-    RawTile cur[NS];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) cur[j] = wpre[j];
-    if (c + 1 < kc) fetch(c + 1);
-    float ws[NS];
-    i32x8 bop[NS];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      int64_t s = s0 + j < w.n_strips ? s0 + j : w.n_strips - 1;
-      ws[j] = w.block_scale[((s * 16) / 128) * w.nbk + c];
-      bop[j] = (i32x8){(int)cur[j].a[0], (int)cur[j].a[1], (int)cur[j].a[2], (int)cur[j].a[3],
-                       (int)cur[j].b[0], (int)cur[j].b[1], (int)cur[j].b[2], (int)cur[j].b[3]};
-    }
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms) {
-      const uint8_t *ap = lds + (ms * 16 + r) * STRIDE + 32 * g;
-      u32x4 a0 = *(const u32x4 *)ap, a1 = *(const u32x4 *)(ap + 16);
-      i32x8 aop = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
-                   (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
-#pragma unroll
-      for (int j = 0; j < NS; ++j) {
-        f32x4 t = mfma_f8f6f4(aop, bop[j], (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 127, 127, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[ms][j][i] = __builtin_fmaf(ws[j], t[i], acc[ms][j][i]);
-      }
-    }
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
+  int tm, tn;
+  tile_of(blockIdx.x, gridDim.x, (int)((w.n_strips + 15) / 16), (int)((p.M + ROWS - 1) / ROWS), tm, tn);
+  const int m0 = tm * ROWS;
+  const int s0 = tn * 16 + wave * 4;
+  const int kc = (int)w.k_chunks;
+  const int mrows = (int)((p.M - m0) < ROWS ? (p.M - m0) : ROWS);
+  const uint32_t pitch = (uint32_t)(FP8 ? p.k_pad : p.k_pad / 2);
+  const rsrc_t rt = make_rsrc(w.tiles, (uint32_t)(w.n_strips * w.k_chunks * TILE));
+  const rsrc_t rx = make_rsrc(p.xq + (int64_t)m0 * pitch, (uint32_t)mrows * pitch);
+  rsrc_t rs = rx, rb = rx;
+  if constexpr (!FP8) {
+    rs = make_rsrc((const uint8_t *)p.xs + (int64_t)m0 * (p.k_pad / 32), (uint32_t)(mrows * (p.k_pad / 32)));
+    rb = make_rsrc(w.aux, (uint32_t)(w.n_strips * w.k_chunks * 64));
   }
-
-  const float *xs = (const float *)p.xs;
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int64_t m = m0 + ms * 16 + g * 4 + i;
-      if (m >= p.M) continue;
-      float sx = xs[m];
-#pragma unroll
-      for (int j = 0; j < NS; ++j) {
-        int64_t n = (s0 + j) * 16 + r;
-        if (n < w.N) store_out(p.y, m * w.N + n, p.y_dtype, acc[ms][j][i] * sx);
-      }
-    }
-}
-
-// MXFP4: CHUNK 128 = four 32-blocks; lane group g holds block g.
-template <int MS, int NS>
-__global__ __launch_bounds__(256) void k_gemm_mxfp4(NativeParams p) {
-  constexpr int ROWS = 16 * MS, STRIDE = 64 + 16;  // code bytes per LDS row
-  __shared__ uint8_t lds[ROWS * STRIDE];
-  __shared__ uint32_t lds_s[ROWS];  // 4 E8M0 scales per row
-  const WeightView &w = p.w;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 4, r = lane & 15;
-  const int64_t m0 = (int64_t)blockIdx.y * ROWS;
-  const int64_t s0 = (int64_t)blockIdx.x * (4 * NS) + wave * NS;
-  const int64_t kc = w.k_chunks;
-  constexpr int PIECES = (ROWS * 64 / 16 + 255) / 256;
-  const uint8_t *xsc = (const uint8_t *)p.xs;
-
-  f32x4 acc[MS][NS];
-#pragma unroll
-  for (int i = 0; i < MS; ++i)
-#pragma unroll
-    for (int j = 0; j < NS; ++j) acc[i][j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
   u32x4 apre[PIECES];
   uint32_t spre = 0;
-  RawTile wpre[NS];
-  auto fetch = [&](int64_t c) {
+  auto fetch_a = [&](int c) {
 #pragma unroll
     for (int q = 0; q < PIECES; ++q) {
-      int piece = tid + q * 256;
-      int row = piece / 4, kb = (piece % 4) * 16;
-      int64_t m = m0 + row;
-      apre[q] = (row < ROWS && m < p.M) ? *(const u32x4 *)(p.xq + m * (p.k_pad / 2) + c * 64 + kb)
-                                        : (u32x4){0, 0, 0, 0};
+      const int piece = tid + q * 256, row = piece / (ROWB / 16), kb = (piece % (ROWB / 16)) * 16;
+      apre[q] = bload16(rx, c < kc ? (uint32_t)row * pitch + (uint32_t)(c * ROWB + kb) : kOOB);
     }
-    if (tid < ROWS) {
-      int64_t m = m0 + tid;
-      spre = m < p.M ? *(const uint32_t *)(xsc + m * (p.k_pad / 32) + c * 4) : 0u;
-    }
+    if constexpr (!FP8)
+      spre = bload4(rs, (c < kc && tid < ROWS) ? (uint32_t)(tid * (p.k_pad / 32) + c * 4) : kOOB);
+  };
+  auto store_a = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      int64_t s = s0 + j;
-      if (s < w.n_strips) wpre[j] = load_tile<DIALQ_FORMAT_MXFP4>(w.tiles, s * kc + c, lane);
-      else wpre[j].a = wpre[j].b = (u32x4){0, 0, 0, 0};
+    for (int q = 0; q < PIECES; ++q) {
+      const int piece = tid + q * 256, row = piece / (ROWB / 16), kb = (piece % (ROWB / 16)) * 16;
+      *(u32x4 *)(lds + buf * ABUF + row * STRIDE + kb) = apre[q];
     }
+    if constexpr (!FP8) lds_s[buf][tid] = spre;
   };
 
-  fetch(0);
-  for (int64_t c = 0; c < kc; ++c) {
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < PIECES; ++q) {
-      int piece = tid + q * 256;
-      int row = piece / 4, kb = (piece % 4) * 16;
-      if (row < ROWS) *(u32x4 *)(lds + row * STRIDE + kb) = apre[q];
-    }
-    if (tid < ROWS) lds_s[tid] = spre;
-    __syncthreads();
-    RawTile cur[NS];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) cur[j] = wpre[j];
-    if (c + 1 < kc) fetch(c + 1);
-    i32x8 bop[NS];
-    int bsc[NS];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      int64_t s = s0 + j < w.n_strips ? s0 + j : w.n_strips - 1;
-      bsc[j] = w.aux[(s * kc + c) * 64 + r * 4 + g];
-      bop[j] = (i32x8){(int)cur[j].a[0], (int)cur[j].a[1], (int)cur[j].a[2], (int)cur[j].a[3], 0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms) {
-      int row = ms * 16 + r;
-      u32x4 a0 = *(const u32x4 *)(lds + row * STRIDE + 16 * g);
-      i32x8 aop = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], 0, 0, 0, 0};
-      int asc = (lds_s[row] >> (8 * g)) & 0xff;
-#pragma unroll
-      for (int j = 0; j < NS; ++j) acc[ms][j] = mfma_f8f6f4(aop, bop[j], acc[ms][j], asc, bsc[j], 4);
-    }
+  // Weights: wb[slot][j][q] is the B operand of step j, column tile q (fp4
+  // uses its low 4 dwords).  A slot is refilled in place, after the MFMAs
+  // that read it, so the ring keeps its registers across the loop.
+  auto bload = [&](int c, int j, int q, int i) -> u32x4 {
+    const int strip = s0 + 2 * q + sub;
+    const bool valid = c < kc && strip < w.n_strips;
+    const uint32_t off = valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * TILE +
+                                     (uint32_t)(((2 * j + h) * 16 + r) * (16 * BW) + 16 * i)
+                               : kOOB;
+    return bload16(rt, off);
+  };
+  auto sbload = [&](int c, int q) -> uint32_t {  // MXFP4 weight scales of row r, k blocks 0..3
+    const int strip = s0 + 2 * q + sub;
+    const bool valid = c < kc && strip < w.n_strips;
+    return bload4(rb, valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * 64u + (uint32_t)(r * 4) : kOOB);
+  };
+  i32x8 wb[DEPTH][2][2];
+  uint32_t wsb[DEPTH][2];
+  // FP8_BLOCK: the wave's 128x128 block scale of chunk c rides the ring with
+  // the chunk's weights (one uniform dword load per chunk)
+  uint32_t wsv[DEPTH];
+  rsrc_t rw = rx;
+  if constexpr (FP8) {
+    const int sb = s0 < w.n_strips ? s0 : (int)w.n_strips - 1;
+    rw = make_rsrc(w.block_scale + (int64_t)(sb / 8) * w.nbk, (uint32_t)(kc * 4));
   }
+  auto wsload = [&](int c) -> uint32_t { return bload4(rw, c < kc ? (uint32_t)(c * 4) : kOOB); };
+  auto refill = [&](int slot, int c, int j, int q) {
+    const u32x4 lo = bload(c, j, q, 0);
+    wb[slot][j][q][0] = (int)lo[0];
+    wb[slot][j][q][1] = (int)lo[1];
+    wb[slot][j][q][2] = (int)lo[2];
+    wb[slot][j][q][3] = (int)lo[3];
+    if constexpr (FP8) {
+      const u32x4 hi = bload(c, j, q, 1);
+      wb[slot][j][q][4] = (int)hi[0];
+      wb[slot][j][q][5] = (int)hi[1];
+      wb[slot][j][q][6] = (int)hi[2];
+      wb[slot][j][q][7] = (int)hi[3];
+    }
+  };
+  auto fill_slot = [&](int slot) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        wb[slot][j][q] = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
+        refill(slot, slot, j, q);
+      }
+    if constexpr (!FP8)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) wsb[slot][q] = sbload(slot, q);
+    if constexpr (FP8) wsv[slot] = wsload(slot);
+  };
+  float mref = 1.0f;
 
+  f32x16 acc[MT][2];
 #pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    int64_t n = (s0 + j) * 16 + r;
-    if (n >= w.N) continue;
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int ms = 0; ms < MS; ++ms)
+    for (int q = 0; q < 2; ++q)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        int64_t m = m0 + ms * 16 + g * 4 + i;
-        if (m < p.M) store_out(p.y, m * w.N + n, p.y_dtype, acc[ms][j][i]);
+      for (int v = 0; v < 16; ++v) acc[i][q][v] = 0.0f;
+
+  // Prologue in the steady state's load order (activations of chunk c+1,
+  // then weights of chunk c+1), so the first chunk waits like every other.
+#pragma unroll
+  for (int slot = 0; slot + 1 < DEPTH; ++slot) fill_slot(slot);
+  fetch_a(0);
+  store_a(0);
+  fetch_a(1);
+  __builtin_amdgcn_sched_barrier(0);
+  fill_slot(DEPTH - 1);
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto chunk = [&](int slot, int c) {
+    __syncthreads();  // buffer c&1 written; buffer (c+1)&1 no longer read
+    store_a((c + 1) & 1);
+    fetch_a(c + 2);
+    // the activation loads of chunk c+2 stay ahead of this chunk's weight
+    // refills, so the next chunk's wait for them leaves the refills in flight
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t *base = lds + (c & 1) * ABUF;
+    // every activation operand (and MXFP4 scale word) of the chunk, read at once
+    i32x8 a[2][MT];
+    uint32_t asw[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int row = mt * 32 + (lane & 31);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint8_t *ap = base + row * STRIDE + (FP8 ? 64 * j + 32 * h : 32 * j + 16 * h);
+        const u32x4 a0 = *(const u32x4 *)ap;
+        if constexpr (FP8) {
+          const u32x4 a1 = *(const u32x4 *)(ap + 16);
+          a[j][mt] = (i32x8){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
+                             (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+        } else {
+          a[j][mt] = (i32x8){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], 0, 0, 0, 0};
+        }
+      }
+      if constexpr (!FP8) asw[mt] = lds_s[c & 1][row];
+    }
+    int bsc = 127;
+    bool live = true;
+    float ratio = 1.0f;  // FP8: applied to each tile just before its first MFMA of the chunk
+    if constexpr (FP8) {
+      const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(wsv[slot]));
+      live = ws != 0.0f;
+      if (live) {
+        int e;
+        const float m = __builtin_frexpf(ws, &e);
+        ratio = mref / m;  // exactly 1 when the mantissa repeats
+        mref = m;
+        bsc = 127 + e;
+        bsc = bsc < 0 ? 0 : (bsc > 254 ? 254 : bsc);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      int sbq[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) sbq[q] = FP8 ? bsc : (int)((wsb[slot][q] >> (8 * (2 * j + h))) & 0xff);
+      if (live) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int asc = FP8 ? 127 : (int)((asw[mt] >> (8 * (2 * j + h))) & 0xff);
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            if constexpr (FP8)
+              if (j == 0) acc[mt][q] *= ratio;
+            acc[mt][q] = mfma_scaled32<FP8>(a[j][mt], wb[slot][j][q], acc[mt][q], asc, sbq[q]);
+          }
+        }
+        if constexpr (FP8)
+          if (j == 0) {
+            // each tile's 16 rescale multiplies run under the previous tile's MFMA
+#pragma unroll
+            for (int t = 0; t < 2 * MT; ++t) {
+              __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // VALU
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            }
+          }
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) refill(slot, c + DEPTH, j, q);
+    }
+    if constexpr (!FP8)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) wsb[slot][q] = sbload(c + DEPTH, q);
+    if constexpr (FP8) wsv[slot] = wsload(c + DEPTH);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int c = 0;
+  for (; c + DEPTH - 1 < kc; c += DEPTH) {
+#pragma unroll
+    for (int slot = 0; slot < DEPTH; ++slot) chunk(slot, c + slot);
+  }
+#pragma unroll
+  for (int slot = 0; slot + 1 < DEPTH; ++slot)
+    if (c + slot < kc) chunk(slot, c + slot);
+
+  const float *xs = (const float *)p.xs;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);
+    if (col >= w.N) continue;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = m0 + mt * 32 + 8 * (v / 4) + 4 * h + (v % 4);
+        if (m >= p.M) continue;
+        float out = acc[mt][q][v];
+        if constexpr (FP8) out *= xs[m] * mref;
+        store_out(p.y, m * w.N + col, p.y_dtype, out);
       }
   }
+}
+
+template <int FMT, int MT, int OCC, int DEPTH>
+static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M, int64_t k_pad,
+                                void *y, int y_dtype, hipStream_t st) {
+  constexpr int ROWS = 32 * MT;
+  constexpr int64_t TILE = FMT == DIALQ_FORMAT_FP8_BLOCK ? 2048 : 1024;
+  const int64_t pitch = FMT == DIALQ_FORMAT_FP8_BLOCK ? k_pad : k_pad / 2;
+  // 32-bit buffer offsets, with 0x80000000 reserved as the out-of-range offset
+  if (w.n_strips * w.k_chunks * TILE >= ((int64_t)1 << 31) || ROWS * pitch >= ((int64_t)1 << 31))
+    return hipErrorInvalidValue;
+  const int64_t tiles = ((w.n_strips + 15) / 16) * ((M + ROWS - 1) / ROWS);
+  if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+  NativeParams p{w, xq, xs, M, k_pad, y, y_dtype};
+  k_gemm_native<FMT, MT, OCC, DEPTH><<<dim3((unsigned)tiles), 256, 0, st>>>(p);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm_native(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M,
                               int64_t k_pad, void *y, int y_dtype, hipStream_t st) {
-  constexpr int MS = 8, NS = 4;
-  dim3 grid((unsigned)((w.n_strips + 4 * NS - 1) / (4 * NS)), (unsigned)((M + 16 * MS - 1) / (16 * MS)));
-  NativeParams p{w, xq, xs, M, k_pad, y, y_dtype};
-  if (w.fmt == DIALQ_FORMAT_FP8_BLOCK) {
-    k_gemm_fp8<MS, NS><<<grid, 256, 0, st>>>(p);
-  } else if (w.fmt == DIALQ_FORMAT_MXFP4) {
-    k_gemm_mxfp4<MS, NS><<<grid, 256, 0, st>>>(p);
-  } else {
-    return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  if (k_pad != w.k_chunks * 128) return hipErrorInvalidValue;
+  if (w.fmt == DIALQ_FORMAT_FP8_BLOCK)
+    return native_launch<DIALQ_FORMAT_FP8_BLOCK, NATIVE_MT_FP8, NATIVE_OCC_FP8, NATIVE_DEPTH_FP8>(w, xq, xs, M, k_pad, y,
+                                                                                                y_dtype, st);
+  if (w.fmt == DIALQ_FORMAT_MXFP4)
+    return native_launch<DIALQ_FORMAT_MXFP4, NATIVE_MT_FP4, NATIVE_OCC_FP4, NATIVE_DEPTH_FP4>(w, xq, xs, M, k_pad, y,
+                                                                                             y_dtype, st);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace dialq

@@ -592,48 +592,118 @@ hipError_t launch_dequant(const DequantArgs &a, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Per-token FP8 activation quantizer: s = amax>0 ? amax/448 : 1,
-// q = e4m3_rne(x * (1/s)).  One 256-thread block per row.
-__global__ __launch_bounds__(256) void k_act_fp8(const void *x, int dtype, int64_t K, uint8_t *q,
-                                                 float *scale, int64_t k_pad) {
+// Activation quantizers of the native prefill.
+//   FP8 (per token): s = amax > 0 ? amax / 448 : 1, q = e4m3_rne(x * (1/s)).
+//   MXFP4 (per 32-block): the E8M0 scale and E2M1 codes of mx_quant32.
+// Both write [M, k_pad] (FP8 bytes / MXFP4 nibbles) with a zero tail past K.
+// The weight formats make K a multiple of 8 (FP8_BLOCK) or 32 (MXFP4) and the
+// C ABI makes x 16-byte aligned, so 8 activations come with one 16-byte (f16 /
+// bf16) or 32-byte (f32) load and the codes leave 8 or 32 at a time.
+template <int ACT>
+__device__ __forceinline__ void load8(const void *x, int64_t e, float (&v)[8]) {
+  if constexpr (ACT == DIALQ_F32) {
+    const float4 a = *(const float4 *)((const float *)x + e), b = *(const float4 *)((const float *)x + e + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 u = *(const uint4 *)((const uint16_t *)x + e);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (ACT == DIALQ_BF16) {
+        v[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
+        v[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+      } else {
+        v[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+        v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+      }
+    }
+  }
+}
+
+template <int ACT>
+__global__ __launch_bounds__(256) void k_act_fp8_v8(const void *x, int64_t K, uint8_t *q, float *scale,
+                                                    int64_t k_pad) {
   __shared__ float sh[8];
-  int64_t row = blockIdx.x;
+  const int64_t row = blockIdx.x, g8 = K / 8;
   float amax = 0.0f;
-  for (int64_t i = threadIdx.x; i < K; i += 256) amax = fmaxf(amax, fabsf(load_in(x, row * K + i, dtype)));
+  for (int64_t g = threadIdx.x; g < g8; g += 256) {
+    float v[8];
+    load8<ACT>(x, row * K + 8 * g, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  }
   amax = block_reduce_max<256>(amax, sh);
-  float s = amax > 0.0f ? amax / 448.0f : 1.0f;
-  float inv = 1.0f / s;
-  for (int64_t i = threadIdx.x; i < k_pad; i += 256)
-    q[row * k_pad + i] = i < K ? (uint8_t)f32_to_e4m3(load_in(x, row * K + i, dtype) * inv) : (uint8_t)0;
+  const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+  const float inv = 1.0f / s;
+  for (int64_t g = threadIdx.x; g < k_pad / 8; g += 256) {
+    uint2 out = {0u, 0u};
+    if (g < g8) {
+      float v[8];
+      load8<ACT>(x, row * K + 8 * g, v);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out.x |= (uint32_t)f32_to_e4m3(v[i] * inv) << (8 * i);
+        out.y |= (uint32_t)f32_to_e4m3(v[4 + i] * inv) << (8 * i);
+      }
+    }
+    *(uint2 *)(q + row * k_pad + 8 * g) = out;
+  }
   if (threadIdx.x == 0) scale[row] = s;
 }
 
-// Per-32 MXFP4 activation quantizer into [M, k_pad/2] codes + [M, k_pad/32]
-// E8M0 scales (k_pad: K rounded up to the GEMM chunk; the tail is zero).
-__global__ void k_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad,
-                            uint8_t *packed, uint8_t *scales) {
-  int64_t nb = k_pad / 32;
-  int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+template <int ACT>
+__global__ __launch_bounds__(256) void k_act_mxfp4_v32(const void *x, int64_t M, int64_t K, int64_t k_pad,
+                                                       uint8_t *packed, uint8_t *scales) {
+  const int64_t nb = k_pad / 32;
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= M * nb) return;
-  int64_t row = b / nb, blk = b % nb;
-  if (blk * 32 >= K) {
-    for (int i = 0; i < 16; ++i) packed[row * (k_pad / 2) + blk * 16 + i] = 0;
-    scales[b] = 0;
-    return;
+  const int64_t row = b / nb, blk = b % nb;
+  uint4 codes = {0u, 0u, 0u, 0u};
+  uint8_t sc = 0;
+  if (blk * 32 < K) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float t[8];
+      load8<ACT>(x, row * K + blk * 32 + 8 * i, t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[8 * i + e] = t[e];
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    int shared = amax > 0.0f ? floor_log2_pos(amax) - 2 : -127;
+    shared = shared < -127 ? -127 : (shared > 127 ? 127 : shared);
+    sc = (uint8_t)(shared + 127);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 32; ++i) w[i / 8] |= f32_to_e2m1(ldexpf(v[i], -shared)) << (4 * (i % 8));
+    codes = {w[0], w[1], w[2], w[3]};
   }
-  mx_quant32(x, dtype, row * K + blk * 32, packed + row * (k_pad / 2) + blk * 16, scales + b);
+  *(uint4 *)(packed + row * (k_pad / 2) + blk * 16) = codes;
+  scales[b] = sc;
 }
 
 hipError_t launch_act_fp8(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad, uint8_t *q,
                           float *scale, hipStream_t st) {
-  k_act_fp8<<<(unsigned)M, 256, 0, st>>>(x, dtype, K, q, scale, k_pad);
+  if (K % 8 != 0 || k_pad % 8 != 0 || ((uintptr_t)x & 15u) != 0 || ((uintptr_t)q & 7u) != 0)
+    return hipErrorInvalidValue;
+  if (dtype == DIALQ_BF16) k_act_fp8_v8<DIALQ_BF16><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
+  else if (dtype == DIALQ_F16) k_act_fp8_v8<DIALQ_F16><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
+  else k_act_fp8_v8<DIALQ_F32><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
   return hipGetLastError();
 }
 
 hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad,
                             uint8_t *packed, uint8_t *scales, hipStream_t st) {
   int64_t nb = M * (k_pad / 32);
-  k_act_mxfp4<<<grid_for(nb, 256, 1 << 30), 256, 0, st>>>(x, dtype, M, K, k_pad, packed, scales);
+  if (K % 32 != 0 || k_pad % 32 != 0 || ((uintptr_t)x & 15u) != 0 || ((uintptr_t)packed & 15u) != 0)
+    return hipErrorInvalidValue;
+  const dim3 grid = grid_for(nb, 256, 1 << 30);
+  if (dtype == DIALQ_BF16) k_act_mxfp4_v32<DIALQ_BF16><<<grid, 256, 0, st>>>(x, M, K, k_pad, packed, scales);
+  else if (dtype == DIALQ_F16) k_act_mxfp4_v32<DIALQ_F16><<<grid, 256, 0, st>>>(x, M, K, k_pad, packed, scales);
+  else k_act_mxfp4_v32<DIALQ_F32><<<grid, 256, 0, st>>>(x, M, K, k_pad, packed, scales);
   return hipGetLastError();
 }
 

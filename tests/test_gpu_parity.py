@@ -191,6 +191,86 @@ def test_native_prefill_parity(fmt, torch_dev):
         assert rel <= TOL_LOWP, (dq.FORMAT_NAMES[fmt], m, rel)
 
 
+def _assert_bits_equal(got, want, x):
+    # a code of -0 reaches the product as +0 (-0 + 0 = +0), so zeros compare by value
+    bad = np.argwhere((got.view(np.uint32) != want.view(np.uint32)) & ~((got == 0) & (want == 0)))
+    if len(bad):
+        i, j = bad[0]
+        raise AssertionError(f"{len(bad)} mismatches; first at {(i, j)}: got {got[i, j]!r} want {want[i, j]!r} "
+                             f"x {x[i, j]!r}")
+
+
+@pytest.mark.parametrize("x_dtype", [dq.BF16, dq.F16, dq.F32], ids=["bf16", "f16", "f32"])
+@pytest.mark.parametrize("k", [384, 200], ids=["k384", "k200"])
+def test_native_activation_quantizer_exact(k, x_dtype, torch_dev):
+    """The activation quantizers, bit-exact, seen through an identity weight:
+    y[m, n] = dequant(xq)[m, n] is one exactly rounded f32 product (FP8:
+    e4m3(q) * s) or an exact value (MXFP4: e2m1 * 2^e), so the product
+    equals the oracle's dequantized activations bit for bit."""
+    import torch
+    rng = np.random.default_rng(k + x_dtype)
+    m = 70
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    x[3] = 0.0                       # all-zero token: scale 1 / E8M0 floor
+    x[5, : k // 2] *= 1e-3           # blocks of very different magnitude
+    xe = exact_inputs(x, x_dtype)
+    # FP8_BLOCK identity: code 0x38 (1.0) on the diagonal, unit block scales
+    q = np.zeros((k, k), np.uint8)
+    np.fill_diagonal(q, 0x38)
+    s = np.ones(((k + 127) // 128, (k + 127) // 128), np.float32)
+    lin = dq.Linear.create(dq.FP8_BLOCK, k, k, q, s)
+    y = empty_out(m, k, dq.F32, torch_dev)
+    lin.forward(to_torch(x, x_dtype, torch_dev), y, path=dq.PATH_GEMM_NATIVE)
+    torch.cuda.synchronize()
+    qx, sx = O.act_fp8_quantize(xe)
+    want = (O.e4m3_to_f32(qx) * sx[:, None]).astype(np.float32)
+    _assert_bits_equal(y.cpu().numpy(), want, xe)
+    if k % 32:
+        return
+    # MXFP4 identity: E2M1 code 2 (1.0) on the diagonal, E8M0 scale 127 (1.0)
+    p = np.zeros((k, k // 2), np.uint8)
+    for i in range(k):
+        p[i, i // 2] |= 2 << (4 * (i % 2))
+    lin = dq.Linear.create(dq.MXFP4, k, k, p, np.full((k, k // 32), 127, np.uint8))
+    y = empty_out(m, k, dq.F32, torch_dev)
+    lin.forward(to_torch(x, x_dtype, torch_dev), y, path=dq.PATH_GEMM_NATIVE)
+    torch.cuda.synchronize()
+    px, sxm = O.act_mxfp4_quantize(xe)
+    want = O.mxfp4_dequant(px, sxm).astype(np.float32)
+    _assert_bits_equal(y.cpu().numpy(), want, xe)
+
+
+def test_native_fp8_block_scale_extremes(torch_dev):
+    """FP8 block scales that are zero or span 2^-40 .. 2^40 along k: the
+    native kernel folds each 128x128 block scale into the running sum per
+    chunk, and a zero-scale block must contribute exactly nothing."""
+    import torch
+    n, k, m = 384, 1152, 160
+    rng = np.random.default_rng(77)
+    q = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    q = np.where((q & 0x7F) == 0x7F, q & 0x80, q).astype(np.uint8)  # no NaN codes
+    nb, kb = (n + 127) // 128, (k + 127) // 128
+    s = (2.0 ** rng.integers(-40, 41, (nb, kb))).astype(np.float32)
+    s *= rng.uniform(0.5, 1.0, (nb, kb)).astype(np.float32)
+    s[0, 0] = 0.0
+    s[1, 3:6] = 0.0
+    s[2, :] = s[2, 0]  # equal scales along k: the rescale is skipped
+    lin = dq.Linear.create(dq.FP8_BLOCK, n, k, q, s)
+    deq = O.fp8_block_dequant(q, s)
+    x = O.round_bf16(rng.normal(0, 1, (m, k)).astype(np.float32))
+    yt = empty_out(m, n, dq.F32, torch_dev)
+    lin.forward(to_torch(x, dq.BF16, torch_dev), yt, path=dq.PATH_GEMM_NATIVE)
+    torch.cuda.synchronize()
+    qx, sx = O.act_fp8_quantize(x)
+    ref = O.matmul_f64(O.e4m3_to_f32(qx) * sx[:, None], deq)
+    got = yt.cpu().numpy()
+    # per 128-column block: the blocks' magnitudes differ by up to 2^40
+    for b in range(nb):
+        cols = slice(128 * b, min(n, 128 * b + 128))
+        rel = O.rel_l2(got[:, cols], ref[:, cols])
+        assert rel <= TOL_LOWP, (b, rel)
+
+
 # ---- local q8 (W8A8 decode): bit-exact ---------------------------------------
 @pytest.mark.parametrize("k", [96, 512])
 def test_local_q8_bit_exact(k, torch_dev):
