@@ -248,19 +248,25 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   }
   if (st < nstage) stage(wb[0], st);
 
+  // lane (g, r) holds rows 16ms + 4g + i of column 16(s0 + n) + r
+  const bool full = m0 + S::ROWS <= p.M;
+  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+    typedef decltype(yd) Y;
 #pragma unroll
-  for (int n = 0; n < NS; ++n) {
-    const int64_t col = (int64_t)(s0 + n) * 16 + r;
-    if (col >= w.N) continue;
-    const float scale = epilogue_scale<FMT>(w, col);
+    for (int n = 0; n < NS; ++n) {
+      const int64_t col = (int64_t)(s0 + n) * 16 + r;
+      if (col >= w.N) continue;
+      const float scale = epilogue_scale<FMT>(w, col);
 #pragma unroll
-    for (int ms = 0; ms < MS; ++ms)
+      for (int ms = 0; ms < MS; ++ms) {
+        const int64_t rb = m0 + ms * 16 + g * 4;
+        typename Y::T *py = (typename Y::T *)p.y + rb * w.N + col;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t m = m0 + ms * 16 + g * 4 + i;
-        if (m < p.M) store_out(p.y, m * w.N + col, p.y_dtype, acc[ms][n][i] * scale);
+        for (int i = 0; i < 4; ++i)
+          if (full || rb + i < p.M) py[i * w.N] = Y::conv(acc[ms][n][i] * scale);
       }
-  }
+    }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -397,19 +403,26 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   }
   if (st < nstage) stage(wb[0], st);
 
+  const bool full = m0 + ROWS <= p.M;
+  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+    typedef decltype(yd) Y;
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-    const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);
-    if (col >= w.N) continue;
-    const float scale = w.row_scale[col];
+    for (int q = 0; q < NQ; ++q) {
+      const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);
+      if (col >= w.N) continue;
+      const float scale = w.row_scale[col];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt) {
+        const int64_t rb = m0 + mt * 32 + 4 * h;
+        typename Y::T *py = (typename Y::T *)p.y + rb * w.N + col;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t m = m0 + mt * 32 + 8 * (v / 4) + 4 * h + (v % 4);
-        if (m < p.M) store_out(p.y, m * w.N + col, p.y_dtype, acc[mt][q][v] * scale);
+        for (int v = 0; v < 16; ++v) {
+          const int rr = 8 * (v / 4) + (v % 4);
+          if (full || rb + rr < p.M) py[rr * w.N] = Y::conv(acc[mt][q][v] * scale);
+        }
       }
-  }
+    }
+  });
 }
 
 template <int FMT, int ACT>
@@ -518,10 +531,10 @@ __device__ __forceinline__ f32x16 mfma_scaled32(i32x8 a, i32x8 b, f32x16 c, int 
 #define NATIVE_OCC_FP4 3
 #endif
 #ifndef NATIVE_DEPTH_FP8
-#define NATIVE_DEPTH_FP8 3  // chunks of weights in flight per wave (register ring slots)
+#define NATIVE_DEPTH_FP8 2  // chunks of weights and activations in flight per wave (register ring slots)
 #endif
 #ifndef NATIVE_DEPTH_FP4
-#define NATIVE_DEPTH_FP4 3
+#define NATIVE_DEPTH_FP4 2
 #endif
 
 template <int FMT, int MT, int OCC, int DEPTH>
@@ -556,24 +569,26 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
     rb = make_rsrc(w.aux, (uint32_t)(w.n_strips * w.k_chunks * 64));
   }
 
-  u32x4 apre[PIECES];
-  uint32_t spre = 0;
-  auto fetch_a = [&](int c) {
+  // Activations ride a register ring of DEPTH chunks (slot = chunk % DEPTH)
+  // into the double-buffered LDS stage (buffer = chunk & 1).
+  u32x4 apre[DEPTH][PIECES];
+  uint32_t spre[DEPTH];
+  auto fetch_a = [&](int aslot, int c) {
 #pragma unroll
     for (int q = 0; q < PIECES; ++q) {
       const int piece = tid + q * 256, row = piece / (ROWB / 16), kb = (piece % (ROWB / 16)) * 16;
-      apre[q] = bload16(rx, c < kc ? (uint32_t)row * pitch + (uint32_t)(c * ROWB + kb) : kOOB);
+      apre[aslot][q] = bload16(rx, c < kc ? (uint32_t)row * pitch + (uint32_t)(c * ROWB + kb) : kOOB);
     }
     if constexpr (!FP8)
-      spre = bload4(rs, (c < kc && tid < ROWS) ? (uint32_t)(tid * (p.k_pad / 32) + c * 4) : kOOB);
+      spre[aslot] = bload4(rs, (c < kc && tid < ROWS) ? (uint32_t)(tid * (p.k_pad / 32) + c * 4) : kOOB);
   };
-  auto store_a = [&](int buf) {
+  auto store_a = [&](int aslot, int buf) {
 #pragma unroll
     for (int q = 0; q < PIECES; ++q) {
       const int piece = tid + q * 256, row = piece / (ROWB / 16), kb = (piece % (ROWB / 16)) * 16;
-      *(u32x4 *)(lds + buf * ABUF + row * STRIDE + kb) = apre[q];
+      *(u32x4 *)(lds + buf * ABUF + row * STRIDE + kb) = apre[aslot][q];
     }
-    if constexpr (!FP8) lds_s[buf][tid] = spre;
+    if constexpr (!FP8) lds_s[buf][tid] = spre[aslot];
   };
 
   // Weights: wb[slot][j][q] is the B operand of step j, column tile q (fp4
@@ -640,23 +655,28 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][q][v] = 0.0f;
 
-  // Prologue in the steady state's load order (activations of chunk c+1,
-  // then weights of chunk c+1), so the first chunk waits like every other.
+  // Prologue in the steady state's load order -- activations of chunk j,
+  // then weights of chunk j-1 -- so the first chunks wait like every other:
+  // chunk c waits for the activations of chunk c+1, issued DEPTH chunks
+  // earlier, and leaves everything issued after them in flight.
+  fetch_a(0, 0);
+  store_a(0, 0);
 #pragma unroll
-  for (int slot = 0; slot + 1 < DEPTH; ++slot) fill_slot(slot);
-  fetch_a(0);
-  store_a(0);
-  fetch_a(1);
-  __builtin_amdgcn_sched_barrier(0);
-  fill_slot(DEPTH - 1);
+  for (int j = 1; j <= DEPTH; ++j) {
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_a(j % DEPTH, j);
+    __builtin_amdgcn_sched_barrier(0);
+    fill_slot(j - 1);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   auto chunk = [&](int slot, int c) {
+    const int aslot = (slot + 1) % DEPTH;  // holds the activations of chunk c+1
     __syncthreads();  // buffer c&1 written; buffer (c+1)&1 no longer read
-    store_a((c + 1) & 1);
-    fetch_a(c + 2);
-    // the activation loads of chunk c+2 stay ahead of this chunk's weight
-    // refills, so the next chunk's wait for them leaves the refills in flight
+    store_a(aslot, (c + 1) & 1);
+    fetch_a(aslot, c + 1 + DEPTH);
+    // the activation loads stay ahead of this chunk's weight refills, so the
+    // wait for them leaves the refills in flight
     __builtin_amdgcn_sched_barrier(0);
     const uint8_t *base = lds + (c & 1) * ABUF;
     // every activation operand (and MXFP4 scale word) of the chunk, read at once
@@ -738,22 +758,39 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
   for (int slot = 0; slot + 1 < DEPTH; ++slot)
     if (c + slot < kc) chunk(slot, c + slot);
 
-  const float *xs = (const float *)p.xs;
+  // FP8: per-row factor xs[m] * mref (rows past M read as 0 and are not stored)
+  float rowf[MT][16];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);
-    if (col >= w.N) continue;
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) rowf[mt][v] = 1.0f;
+  if constexpr (FP8) {
+    const rsrc_t rxs = make_rsrc((const float *)p.xs + m0, (uint32_t)mrows * 4u);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t m = m0 + mt * 32 + 8 * (v / 4) + 4 * h + (v % 4);
-        if (m >= p.M) continue;
-        float out = acc[mt][q][v];
-        if constexpr (FP8) out *= xs[m] * mref;
-        store_out(p.y, m * w.N + col, p.y_dtype, out);
-      }
+      for (int v = 0; v < 16; ++v)
+        rowf[mt][v] = __builtin_bit_cast(float, bload4(rxs, (uint32_t)(mt * 32 + 8 * (v / 4) + 4 * h + (v % 4)) * 4u)) * mref;
   }
+  const bool full = m0 + ROWS <= p.M;
+  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+    typedef decltype(yd) Y;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);
+      if (col >= w.N) continue;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int64_t rb = m0 + mt * 32 + 4 * h;
+        typename Y::T *py = (typename Y::T *)p.y + rb * w.N + col;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int rr = 8 * (v / 4) + (v % 4);
+          if (full || rb + rr < p.M) py[rr * w.N] = Y::conv(FP8 ? acc[mt][q][v] * rowf[mt][v] : acc[mt][q][v]);
+        }
+      }
+    }
+  });
 }
 
 template <int FMT, int MT, int OCC, int DEPTH>

@@ -16,6 +16,8 @@
 // applied to the f32 partial product of their own k block.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -460,6 +462,27 @@ __device__ __forceinline__ void bops_mac(const BOps<FMT> &o, const XOp<ACT> *xo,
         acc[i] = __builtin_fmaf(o.s1[j], pq[i], __builtin_fmaf(-o.s2[j], px[i], acc[i]));
     }
   }
+}
+
+// ---- output stores -------------------------------------------------------------
+// The y dtype is dispatched once per workgroup: body(YDtype<DIALQ_BF16>{}) and
+// its siblings each carry a compile-time dtype, so the per-element stores are
+// plain conversions and stores without branches.
+template <int YT>
+struct YDtype {
+  static constexpr int value = YT;
+  typedef typename std::conditional<YT == DIALQ_F32, float, uint16_t>::type T;
+  __device__ static __forceinline__ T conv(float v) {
+    if constexpr (YT == DIALQ_BF16) return f32_to_bf16_bits(v);
+    else if constexpr (YT == DIALQ_F16) return f32_to_f16_bits(v);
+    else return v;
+  }
+};
+template <typename F>
+__device__ __forceinline__ void with_y_dtype(int y_dtype, F &&body) {
+  if (y_dtype == DIALQ_BF16) body(YDtype<DIALQ_BF16>{});
+  else if (y_dtype == DIALQ_F16) body(YDtype<DIALQ_F16>{});
+  else body(YDtype<DIALQ_F32>{});
 }
 
 template <int FMT>
