@@ -621,89 +621,121 @@ __device__ __forceinline__ void load8(const void *x, int64_t e, float (&v)[8]) {
   }
 }
 
-template <int ACT>
+// FP8: one 256-thread block per token.  G > 0 keeps the row's 8-value
+// groups in registers (K <= 2048 * G), so the row is read once; G == 0 reads
+// it twice (amax pass, then conversion).
+template <int ACT, int G>
 __global__ __launch_bounds__(256) void k_act_fp8_v8(const void *x, int64_t K, uint8_t *q, float *scale,
                                                     int64_t k_pad) {
   __shared__ float sh[8];
   const int64_t row = blockIdx.x, g8 = K / 8;
+  float v[G > 0 ? G : 1][8];
   float amax = 0.0f;
-  for (int64_t g = threadIdx.x; g < g8; g += 256) {
-    float v[8];
-    load8<ACT>(x, row * K + 8 * g, v);
+  if constexpr (G > 0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    for (int i = 0; i < G; ++i) {
+      const int64_t g = threadIdx.x + 256 * i;
+      if (g < g8) load8<ACT>(x, row * K + 8 * g, v[i]);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[i][e] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
+    }
+  } else {
+    for (int64_t g = threadIdx.x; g < g8; g += 256) {
+      load8<ACT>(x, row * K + 8 * g, v[0]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[0][e]));
+    }
   }
   amax = block_reduce_max<256>(amax, sh);
   const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
   const float inv = 1.0f / s;
-  for (int64_t g = threadIdx.x; g < k_pad / 8; g += 256) {
+  auto put = [&](int64_t g, const float (&u)[8]) {
     uint2 out = {0u, 0u};
-    if (g < g8) {
-      float v[8];
-      load8<ACT>(x, row * K + 8 * g, v);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        out.x |= (uint32_t)f32_to_e4m3(v[i] * inv) << (8 * i);
-        out.y |= (uint32_t)f32_to_e4m3(v[4 + i] * inv) << (8 * i);
-      }
+    for (int e = 0; e < 4; ++e) {
+      out.x |= (uint32_t)f32_to_e4m3(u[e] * inv) << (8 * e);
+      out.y |= (uint32_t)f32_to_e4m3(u[4 + e] * inv) << (8 * e);
     }
     *(uint2 *)(q + row * k_pad + 8 * g) = out;
+  };
+  if constexpr (G > 0) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int64_t g = threadIdx.x + 256 * i;
+      if (g < g8) put(g, v[i]);
+    }
+  } else {
+    for (int64_t g = threadIdx.x; g < g8; g += 256) {
+      load8<ACT>(x, row * K + 8 * g, v[0]);
+      put(g, v[0]);
+    }
   }
+  for (int64_t g = g8 + threadIdx.x; g < k_pad / 8; g += 256) *(uint2 *)(q + row * k_pad + 8 * g) = uint2{0u, 0u};
   if (threadIdx.x == 0) scale[row] = s;
 }
 
+// MXFP4: four lanes per 32-block, 8 activations each; the block's amax is
+// combined across the four lanes with two butterfly shuffles.
 template <int ACT>
-__global__ __launch_bounds__(256) void k_act_mxfp4_v32(const void *x, int64_t M, int64_t K, int64_t k_pad,
-                                                       uint8_t *packed, uint8_t *scales) {
-  const int64_t nb = k_pad / 32;
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= M * nb) return;
-  const int64_t row = b / nb, blk = b % nb;
-  uint4 codes = {0u, 0u, 0u, 0u};
-  uint8_t sc = 0;
-  if (blk * 32 < K) {
-    float v[32];
+__global__ __launch_bounds__(256) void k_act_mxfp4_v8(const void *x, int64_t M, int64_t K, int64_t k_pad,
+                                                      uint8_t *packed, uint8_t *scales) {
+  const int64_t per_row = k_pad / 8;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= M * per_row) return;  // M * per_row is a multiple of 4: whole blocks leave together
+  const int64_t row = t / per_row, g = t % per_row;
+  float v[8];
+  if (8 * g < K) load8<ACT>(x, row * K + 8 * g, v);
+  else
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float t[8];
-      load8<ACT>(x, row * K + blk * 32 + 8 * i, t);
+    for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+  float amax = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[8 * i + e] = t[e];
-    }
-    float amax = 0.0f;
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  int shared = amax > 0.0f ? floor_log2_pos(amax) - 2 : -127;
+  shared = shared < -127 ? -127 : (shared > 127 ? 127 : shared);
+  uint32_t codes = 0;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    int shared = amax > 0.0f ? floor_log2_pos(amax) - 2 : -127;
-    shared = shared < -127 ? -127 : (shared > 127 ? 127 : shared);
-    sc = (uint8_t)(shared + 127);
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 32; ++i) w[i / 8] |= f32_to_e2m1(ldexpf(v[i], -shared)) << (4 * (i % 8));
-    codes = {w[0], w[1], w[2], w[3]};
-  }
-  *(uint4 *)(packed + row * (k_pad / 2) + blk * 16) = codes;
-  scales[b] = sc;
+  for (int e = 0; e < 8; ++e) codes |= f32_to_e2m1(ldexpf(v[e], -shared)) << (4 * e);
+  *(uint32_t *)(packed + row * (k_pad / 2) + 4 * g) = codes;
+  if ((g & 3) == 0) scales[row * (k_pad / 32) + g / 4] = (uint8_t)(shared + 127);
+}
+
+template <int ACT>
+static void act_fp8_dispatch(const void *x, int64_t M, int64_t K, int64_t k_pad, uint8_t *q, float *scale,
+                             hipStream_t st) {
+  const int64_t g = (K + 2047) / 2048;
+  if (g <= 1) k_act_fp8_v8<ACT, 1><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
+  else if (g <= 2) k_act_fp8_v8<ACT, 2><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
+  else if (g <= 3) k_act_fp8_v8<ACT, 3><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
+  else if (g <= 4) k_act_fp8_v8<ACT, 4><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
+  else if (g <= 6) k_act_fp8_v8<ACT, 6><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
+  else if (g <= 9) k_act_fp8_v8<ACT, 9><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
+  else k_act_fp8_v8<ACT, 0><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
 }
 
 hipError_t launch_act_fp8(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad, uint8_t *q,
                           float *scale, hipStream_t st) {
   if (K % 8 != 0 || k_pad % 8 != 0 || ((uintptr_t)x & 15u) != 0 || ((uintptr_t)q & 7u) != 0)
     return hipErrorInvalidValue;
-  if (dtype == DIALQ_BF16) k_act_fp8_v8<DIALQ_BF16><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
-  else if (dtype == DIALQ_F16) k_act_fp8_v8<DIALQ_F16><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
-  else k_act_fp8_v8<DIALQ_F32><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
+  if (dtype == DIALQ_BF16) act_fp8_dispatch<DIALQ_BF16>(x, M, K, k_pad, q, scale, st);
+  else if (dtype == DIALQ_F16) act_fp8_dispatch<DIALQ_F16>(x, M, K, k_pad, q, scale, st);
+  else act_fp8_dispatch<DIALQ_F32>(x, M, K, k_pad, q, scale, st);
   return hipGetLastError();
 }
 
 hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad,
                             uint8_t *packed, uint8_t *scales, hipStream_t st) {
-  int64_t nb = M * (k_pad / 32);
-  if (K % 32 != 0 || k_pad % 32 != 0 || ((uintptr_t)x & 15u) != 0 || ((uintptr_t)packed & 15u) != 0)
+  if (K % 32 != 0 || k_pad % 32 != 0 || ((uintptr_t)x & 15u) != 0 || ((uintptr_t)packed & 3u) != 0)
     return hipErrorInvalidValue;
-  const dim3 grid = grid_for(nb, 256, 1 << 30);
-  if (dtype == DIALQ_BF16) k_act_mxfp4_v32<DIALQ_BF16><<<grid, 256, 0, st>>>(x, M, K, k_pad, packed, scales);
-  else if (dtype == DIALQ_F16) k_act_mxfp4_v32<DIALQ_F16><<<grid, 256, 0, st>>>(x, M, K, k_pad, packed, scales);
-  else k_act_mxfp4_v32<DIALQ_F32><<<grid, 256, 0, st>>>(x, M, K, k_pad, packed, scales);
+  const dim3 grid = grid_for(M * (k_pad / 8), 256, 1 << 30);
+  if (dtype == DIALQ_BF16) k_act_mxfp4_v8<DIALQ_BF16><<<grid, 256, 0, st>>>(x, M, K, k_pad, packed, scales);
+  else if (dtype == DIALQ_F16) k_act_mxfp4_v8<DIALQ_F16><<<grid, 256, 0, st>>>(x, M, K, k_pad, packed, scales);
+  else k_act_mxfp4_v8<DIALQ_F32><<<grid, 256, 0, st>>>(x, M, K, k_pad, packed, scales);
   return hipGetLastError();
 }
 

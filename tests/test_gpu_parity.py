@@ -191,6 +191,22 @@ def test_native_prefill_parity(fmt, torch_dev):
         assert rel <= TOL_LOWP, (dq.FORMAT_NAMES[fmt], m, rel)
 
 
+@pytest.mark.parametrize("fmt", [dq.FP8_BLOCK, dq.MXFP4], ids=["fp8_block", "mxfp4"])
+def test_native_prefill_long_k(fmt, torch_dev):
+    """K = 20480: past the register-held rows of the FP8 token quantizer (its
+    two-pass form) and 160 chunks of the GEMM."""
+    import torch
+    n, k, m = 96, 20480, 70
+    lin, _, _, deq = _linear(fmt, n, k, seed=90 + fmt)
+    rng = np.random.default_rng(91)
+    x = O.round_bf16(rng.normal(0, 1, (m, k)).astype(np.float32))
+    yt = empty_out(m, n, dq.BF16, torch_dev)
+    lin.forward(to_torch(x, dq.BF16, torch_dev), yt, path=dq.PATH_GEMM_NATIVE)
+    torch.cuda.synchronize()
+    rel = O.rel_l2(yt.float().cpu().numpy(), _native_ref(fmt, x, deq))
+    assert rel <= TOL_LOWP, (dq.FORMAT_NAMES[fmt], rel)
+
+
 def _assert_bits_equal(got, want, x):
     # a code of -0 reaches the product as +0 (-0 + 0 = +0), so zeros compare by value
     bad = np.argwhere((got.view(np.uint32) != want.view(np.uint32)) & ~((got == 0) & (want == 0)))
