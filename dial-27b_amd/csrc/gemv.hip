@@ -809,6 +809,7 @@ constexpr int ring_depth(int slot_vgprs) {
 }
 
 constexpr int kGemvWgPerCu = 2;          // target ranges per CU
+constexpr int kRangeRing = 4;            // ring depth cap of the whole-strip kernel
 constexpr int kGemvParkBytes = 16384;    // parking LDS per workgroup
 constexpr int kGemvStageBytes = 65536;   // staged-activation LDS per workgroup
 
@@ -832,17 +833,17 @@ static int stage_pitch(const WeightView &w, int by, int chunk) {
   return (int)(((kpad_bytes + 1023) / 1024) * 1024 + 64);
 }
 
-// Whole strips per range when there are enough strips to give every CU
-// about kGemvWgPerCu ranges of equal size (no strip is shared, so no
-// cross-workgroup fix-up); 0 selects equal tile ranges (stream-K).
+// Whole strips per range when there is at least one strip per CU: one strip
+// per workgroup (no strip is shared, so no cross-workgroup fix-up).  Measured
+// on the 27B gate shape: one strip per workgroup and four loads in flight per
+// wave stream 17% faster than two strips and eight loads -- several resident
+// workgroups per CU, each with a shallow ring, keep more of HBM busy than a
+// few deep ones (a plain read kernel shows the same).  0 selects equal tile
+// ranges (stream-K).
 static int gemv_spw(const WeightView &w, int64_t mrows) {
-  const int64_t target = (int64_t)kGemvWgPerCu * device_cus();
+  (void)mrows;
   if (w.n_strips < device_cus()) return 0;
-  int64_t spw = (w.n_strips + target / 2) / target;
-  if (spw < 1) spw = 1;
-  const int64_t seg_cap = kGemvParkBytes / (kGemvWaves * mrows * 16 * 4);
-  if (spw > seg_cap) spw = seg_cap;
-  return (int)spw;
+  return 1;
 }
 
 template <int FMT, typename Pol, int U, bool XL>
@@ -887,8 +888,8 @@ static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
   if (d.w.n_strips >= device_cus()) {
     GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
     p.x_pitch = xl ? stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) : 0;
-    if (xl) return launch_ranges<FMT, PolT<A, ACT, true>, U_XL, true>(p, st);
-    return launch_ranges<FMT, PolT<A, ACT, false>, U_X, false>(p, st);
+    if (xl) return launch_ranges<FMT, PolT<A, ACT, true>, (U_XL < kRangeRing ? U_XL : kRangeRing), true>(p, st);
+    return launch_ranges<FMT, PolT<A, ACT, false>, (U_X < kRangeRing ? U_X : kRangeRing), false>(p, st);
   }
   d.x_pitch = xl ? stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) : 0;
   if (xl) return launch_dyn<FMT, PolT<A, ACT, true>, U_XL, true>(d, mrows, st);
