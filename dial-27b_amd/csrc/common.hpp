@@ -82,11 +82,13 @@ __host__ __device__ inline FormatGeom format_geom(int fmt) {
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }
+// RNE; a NaN keeps its upper bits and is made quiet.  Written as a select so
+// that it compiles to straight-line code.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t x = __float_as_uint(f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
-  uint32_t lsb = (x >> 16) & 1u;
-  return (uint16_t)((x + 0x7fffu + lsb) >> 16);
+  const uint32_t x = __float_as_uint(f);
+  const uint32_t rne = (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
+  const uint32_t nan = (x >> 16) | 0x40u;
+  return (uint16_t)(((x & 0x7fffffffu) > 0x7f800000u) ? nan : rne);
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);

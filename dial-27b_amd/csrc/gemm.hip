@@ -250,8 +250,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 
   // lane (g, r) holds rows 16ms + 4g + i of column 16(s0 + n) + r
   const bool full = m0 + S::ROWS <= p.M;
-  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+  auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
     typedef decltype(yd) Y;
+    constexpr bool CHK = decltype(chk)::value;  // row checks only for the ragged last row tile
 #pragma unroll
     for (int n = 0; n < NS; ++n) {
       const int64_t col = (int64_t)(s0 + n) * 16 + r;
@@ -263,9 +264,13 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
         typename Y::T *py = (typename Y::T *)p.y + rb * w.N + col;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (full || rb + i < p.M) py[i * w.N] = Y::conv(acc[ms][n][i] * scale);
+          if (!CHK || rb + i < p.M) py[i * w.N] = Y::conv(acc[ms][n][i] * scale);
       }
     }
+  };
+  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+    if (full) body(yd, std::false_type{});
+    else body(yd, std::true_type{});
   });
 }
 
@@ -404,8 +409,9 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   if (st < nstage) stage(wb[0], st);
 
   const bool full = m0 + ROWS <= p.M;
-  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+  auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
     typedef decltype(yd) Y;
+    constexpr bool CHK = decltype(chk)::value;  // row checks only for the ragged last row tile
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);
@@ -418,10 +424,14 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int rr = 8 * (v / 4) + (v % 4);
-          if (full || rb + rr < p.M) py[rr * w.N] = Y::conv(acc[mt][q][v] * scale);
+          if (!CHK || rb + rr < p.M) py[rr * w.N] = Y::conv(acc[mt][q][v] * scale);
         }
       }
     }
+  };
+  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+    if (full) body(yd, std::false_type{});
+    else body(yd, std::true_type{});
   });
 }
 
@@ -773,8 +783,9 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
         rowf[mt][v] = __builtin_bit_cast(float, bload4(rxs, (uint32_t)(mt * 32 + 8 * (v / 4) + 4 * h + (v % 4)) * 4u)) * mref;
   }
   const bool full = m0 + ROWS <= p.M;
-  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+  auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
     typedef decltype(yd) Y;
+    constexpr bool CHK = decltype(chk)::value;  // row checks only for the ragged last row tile
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);
@@ -786,10 +797,14 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int rr = 8 * (v / 4) + (v % 4);
-          if (full || rb + rr < p.M) py[rr * w.N] = Y::conv(FP8 ? acc[mt][q][v] * rowf[mt][v] : acc[mt][q][v]);
+          if (!CHK || rb + rr < p.M) py[rr * w.N] = Y::conv(FP8 ? acc[mt][q][v] * rowf[mt][v] : acc[mt][q][v]);
         }
       }
     }
+  };
+  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+    if (full) body(yd, std::false_type{});
+    else body(yd, std::true_type{});
   });
 }
 
