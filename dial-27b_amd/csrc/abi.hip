@@ -86,6 +86,8 @@ struct Linear {
   DevBuf scratch;  // activation codes for native prefill / local q8
   DevBuf gemv_ws;  // stream-K partials of the decode GEMV
   DevBuf gemv_cnt; // per-strip piece counters + work-queue head/exit count (zero between calls)
+  DevBuf native_part;  // stream-K partial tiles of the native prefill
+  DevBuf native_cnt;   // its per-tile arrival counters (zero between calls)
   std::mutex scratch_mu;
   float global = 1.0f;
 
@@ -240,6 +242,26 @@ void ensure_scratch(Linear *L, size_t bytes) {
   if (L->scratch.n < bytes) L->scratch.alloc(bytes);
 }
 
+// Stream-K partials and tile counters of the native prefill, owned by the
+// handle like the GEMV workspace (calls on one handle are stream-ordered).
+// They grow on demand, after the stream has drained, never during graph
+// capture: a capture must follow an eager call of at least the same shape.
+void ensure_native_scratch(Linear *L, size_t part_bytes, size_t cnt_count, hipStream_t st) {
+  const size_t cnt_bytes = cnt_count * sizeof(int);
+  if (L->native_part.n >= part_bytes && L->native_cnt.n >= cnt_bytes) return;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hip_check(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
+  if (cs != hipStreamCaptureStatusNone)
+    fail("native prefill scratch must grow (%zu partial bytes, %zu tile counters) during stream capture; run "
+         "one eager call of this shape before capturing", part_bytes, cnt_count);
+  hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");  // earlier launches may use the old buffers
+  if (L->native_part.n < part_bytes) L->native_part.alloc(part_bytes);
+  if (L->native_cnt.n < cnt_bytes) {
+    L->native_cnt.alloc(cnt_bytes);
+    hip_check(hipMemsetAsync(L->native_cnt.p, 0, cnt_bytes, st), "hipMemsetAsync");
+  }
+}
+
 void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, int y_dtype, int path,
                  hipStream_t st) {
   WeightView w = L->view();
@@ -266,6 +288,8 @@ void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, i
     if (fmt != DIALQ_FORMAT_FP8_BLOCK && fmt != DIALQ_FORMAT_MXFP4)
       fail("native fp8/fp4 prefill needs an FP8 block or MXFP4 weight, got %s", format_name(fmt));
     const int64_t k_pad = w.k_chunks * 128;
+    size_t part_bytes = 0, cnt_count = 0;
+    native_workspace(rows, w, part_bytes, cnt_count);
     std::lock_guard<std::mutex> lock(L->scratch_mu);
     if (fmt == DIALQ_FORMAT_FP8_BLOCK) {
       size_t codes = (size_t)(rows * k_pad), off = (codes + 255) / 256 * 256;
@@ -273,14 +297,20 @@ void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, i
       uint8_t *xq = (uint8_t *)L->scratch.p;
       float *xs = (float *)((uint8_t *)L->scratch.p + off);
       hip_check(launch_act_fp8(x, x_dtype, rows, w.K, k_pad, xq, xs, st), "activation quantizer");
-      hip_check(launch_gemm_native(w, xq, xs, rows, k_pad, y, y_dtype, st), "native GEMM launch");
+      ensure_native_scratch(L, part_bytes, cnt_count, st);
+      hip_check(launch_gemm_native(w, xq, xs, rows, k_pad, y, y_dtype, (float *)L->native_part.p,
+                                   L->native_part.n, (int *)L->native_cnt.p, L->native_cnt.n / sizeof(int), st),
+                "native GEMM launch");
     } else {
       size_t codes = (size_t)(rows * k_pad / 2), off = (codes + 255) / 256 * 256;
       ensure_scratch(L, off + (size_t)(rows * k_pad / 32));
       uint8_t *xq = (uint8_t *)L->scratch.p;
       uint8_t *xs = (uint8_t *)L->scratch.p + off;
       hip_check(launch_act_mxfp4(x, x_dtype, rows, w.K, k_pad, xq, xs, st), "activation quantizer");
-      hip_check(launch_gemm_native(w, xq, xs, rows, k_pad, y, y_dtype, st), "native GEMM launch");
+      ensure_native_scratch(L, part_bytes, cnt_count, st);
+      hip_check(launch_gemm_native(w, xq, xs, rows, k_pad, y, y_dtype, (float *)L->native_part.p,
+                                   L->native_part.n, (int *)L->native_cnt.p, L->native_cnt.n / sizeof(int), st),
+                "native GEMM launch");
     }
   } else {
     fail("unknown path %d", path);
@@ -476,7 +506,7 @@ uint64_t dialq_linear_device_bytes(const void *linear) {
   const Linear *L = (const Linear *)linear;
   if (!L) return 0;
   return L->tiles.n + L->aux.n + L->row_scale.n + L->block_scale.n + L->scratch.n + L->gemv_ws.n +
-         L->gemv_cnt.n;
+         L->gemv_cnt.n + L->native_part.n + L->native_cnt.n;
 }
 
 int dialq_linear_describe(const void *linear, dialq_linear_desc *desc) {

@@ -87,13 +87,22 @@ constexpr int kXcds = 8, kPanel = 4;
 #ifndef GEMM32_OCC
 #define GEMM32_OCC 3  // workgroups per CU the 32x32 kernel is built for
 #endif
-__device__ __forceinline__ void tile_of(int b, int G, int nt, int mt, int &tm, int &tn) {
+// Rank of workgroup b among G such that each XCD (b % kXcds) holds a
+// contiguous run of ranks: a bijection onto [0, G).
+__device__ __forceinline__ int xcd_rank(int b, int G) {
   const int q = G / kXcds, rem = G % kXcds, xcd = b % kXcds, local = b / kXcds;
-  const int L = xcd * q + (xcd < rem ? xcd : rem) + local;  // bijection onto [0, G)
+  return xcd * q + (xcd < rem ? xcd : rem) + local;
+}
+// Logical tile L -> (row block, column tile): panels of kPanel row blocks,
+// column-major inside a panel.
+__device__ __forceinline__ void tile_coords(int L, int nt, int mt, int &tm, int &tn) {
   const int panel = L / (kPanel * nt), i = L - panel * (kPanel * nt);
   const int pm = (mt - panel * kPanel) < kPanel ? (mt - panel * kPanel) : kPanel;  // rows in this panel
   tm = panel * kPanel + i % pm;
   tn = i / pm;
+}
+__device__ __forceinline__ void tile_of(int b, int G, int nt, int mt, int &tm, int &tn) {
+  tile_coords(xcd_rank(b, G), nt, mt, tm, tn);
 }
 
 // Weight-only prefill GEMM.  A 256-thread workgroup computes a
@@ -520,6 +529,10 @@ struct NativeParams {
   int64_t M, k_pad;
   void *y;
   int y_dtype;
+  // Split-K: P pieces per tile (1: whole tiles, no partials).
+  int P;
+  float *part;  // [tiles][P][kNativeAcc][256] partial tiles
+  int *cnt;     // [tiles] arrivals per split tile; zero between launches
 };
 
 template <bool FP8>
@@ -547,6 +560,9 @@ __device__ __forceinline__ f32x16 mfma_scaled32(i32x8 a, i32x8 b, f32x16 c, int 
 #define NATIVE_DEPTH_FP4 2
 #endif
 
+constexpr int kNativeAcc = 64;       // f32 accumulators per thread (MT = 2: 2 x 2 tiles x 16)
+constexpr int kNativeMinChunks = 8;  // fewest k chunks per workgroup in the stream-K split
+
 template <int FMT, int MT, int OCC, int DEPTH>
 __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
   constexpr bool FP8 = FMT == DIALQ_FORMAT_FP8_BLOCK;
@@ -555,262 +571,348 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
   constexpr int ROWS = 32 * MT, ABUF = ROWS * STRIDE;
   constexpr int NPIECE = ROWS * ROWB / 16, PIECES = (NPIECE + 255) / 256;
   static_assert(NPIECE % 256 == 0, "activation pieces must fill the workgroup");
+  static_assert(MT * 2 * 16 == kNativeAcc, "partial slots hold MT x 2 tiles of 16 values per thread");
   constexpr int TILE = FP8 ? 2048 : 1024;  // resident tile bytes
   constexpr int BW = FP8 ? 2 : 1;          // 16-byte loads per lane and B operand
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * ABUF];
   __shared__ uint32_t lds_s[2][256];  // MXFP4: the 4 E8M0 scales of a row's chunk (rows < ROWS)
+  __shared__ int lds_last;
 
   const WeightView &w = p.w;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
-  int tm, tn;
-  tile_of(blockIdx.x, gridDim.x, (int)((w.n_strips + 15) / 16), (int)((p.M + ROWS - 1) / ROWS), tm, tn);
-  const int m0 = tm * ROWS;
-  const int s0 = tn * 16 + wave * 4;
   const int kc = (int)w.k_chunks;
-  const int mrows = (int)((p.M - m0) < ROWS ? (p.M - m0) : ROWS);
+  const int nt = (int)((w.n_strips + 15) / 16), mtiles = (int)((p.M + ROWS - 1) / ROWS);
+  // One workgroup per (tile, k piece).  P == 1: whole tiles in the
+  // XCD-aware order of tile_of.  P > 1: each tile's chunks split evenly into
+  // P pieces; units go (column tile, piece, row block) over XCD-contiguous
+  // ranks, so the row blocks that stream the same weight chunks run on one
+  // XCD at once and share them in its L2.
+  const int P = p.P;
+  int tm, tn, piece = 0;
+  if (P == 1) {
+    tile_of(blockIdx.x, gridDim.x, nt, mtiles, tm, tn);
+  } else {
+    const int u = xcd_rank(blockIdx.x, gridDim.x);
+    tm = u % mtiles;
+    piece = (u / mtiles) % P;
+    tn = u / (mtiles * P);
+  }
+  const int c0 = (int)((int64_t)piece * kc / P), c1 = (int)((int64_t)(piece + 1) * kc / P);
+  const int t = tn * mtiles + tm;  // counter index of a split tile
   const uint32_t pitch = (uint32_t)(FP8 ? p.k_pad : p.k_pad / 2);
   const rsrc_t rt = make_rsrc(w.tiles, (uint32_t)(w.n_strips * w.k_chunks * TILE));
-  const rsrc_t rx = make_rsrc(p.xq + (int64_t)m0 * pitch, (uint32_t)mrows * pitch);
-  rsrc_t rs = rx, rb = rx;
-  if constexpr (!FP8) {
-    rs = make_rsrc((const uint8_t *)p.xs + (int64_t)m0 * (p.k_pad / 32), (uint32_t)(mrows * (p.k_pad / 32)));
-    rb = make_rsrc(w.aux, (uint32_t)(w.n_strips * w.k_chunks * 64));
-  }
-
-  // Activations ride a register ring of DEPTH chunks (slot = chunk % DEPTH)
-  // into the double-buffered LDS stage (buffer = chunk & 1).
-  u32x4 apre[DEPTH][PIECES];
-  uint32_t spre[DEPTH];
-  auto fetch_a = [&](int aslot, int c) {
-#pragma unroll
-    for (int q = 0; q < PIECES; ++q) {
-      const int piece = tid + q * 256, row = piece / (ROWB / 16), kb = (piece % (ROWB / 16)) * 16;
-      apre[aslot][q] = bload16(rx, c < kc ? (uint32_t)row * pitch + (uint32_t)(c * ROWB + kb) : kOOB);
-    }
+  rsrc_t rb = rt;
+  if constexpr (!FP8) rb = make_rsrc(w.aux, (uint32_t)(w.n_strips * w.k_chunks * 64));
+  {
+    const int m0 = tm * ROWS;
+    const int s0 = tn * 16 + wave * 4;
+    const int mrows = (int)((p.M - m0) < ROWS ? (p.M - m0) : ROWS);
+    const rsrc_t rx = make_rsrc(p.xq + (int64_t)m0 * pitch, (uint32_t)mrows * pitch);
+    rsrc_t rs = rx;
     if constexpr (!FP8)
-      spre[aslot] = bload4(rs, (c < kc && tid < ROWS) ? (uint32_t)(tid * (p.k_pad / 32) + c * 4) : kOOB);
-  };
-  auto store_a = [&](int aslot, int buf) {
-#pragma unroll
-    for (int q = 0; q < PIECES; ++q) {
-      const int piece = tid + q * 256, row = piece / (ROWB / 16), kb = (piece % (ROWB / 16)) * 16;
-      *(u32x4 *)(lds + buf * ABUF + row * STRIDE + kb) = apre[aslot][q];
-    }
-    if constexpr (!FP8) lds_s[buf][tid] = spre[aslot];
-  };
+      rs = make_rsrc((const uint8_t *)p.xs + (int64_t)m0 * (p.k_pad / 32), (uint32_t)(mrows * (p.k_pad / 32)));
 
-  // Weights: wb[slot][j][q] is the B operand of step j, column tile q (fp4
-  // uses its low 4 dwords).  A slot is refilled in place, after the MFMAs
-  // that read it, so the ring keeps its registers across the loop.
-  auto bload = [&](int c, int j, int q, int i) -> u32x4 {
-    const int strip = s0 + 2 * q + sub;
-    const bool valid = c < kc && strip < w.n_strips;
-    const uint32_t off = valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * TILE +
-                                     (uint32_t)(((2 * j + h) * 16 + r) * (16 * BW) + 16 * i)
-                               : kOOB;
-    return bload16(rt, off);
-  };
-  auto sbload = [&](int c, int q) -> uint32_t {  // MXFP4 weight scales of row r, k blocks 0..3
-    const int strip = s0 + 2 * q + sub;
-    const bool valid = c < kc && strip < w.n_strips;
-    return bload4(rb, valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * 64u + (uint32_t)(r * 4) : kOOB);
-  };
-  i32x8 wb[DEPTH][2][2];
-  uint32_t wsb[DEPTH][2];
-  // FP8_BLOCK: the wave's 128x128 block scale of chunk c rides the ring with
-  // the chunk's weights (one uniform dword load per chunk)
-  uint32_t wsv[DEPTH];
-  rsrc_t rw = rx;
-  if constexpr (FP8) {
-    const int sb = s0 < w.n_strips ? s0 : (int)w.n_strips - 1;
-    rw = make_rsrc(w.block_scale + (int64_t)(sb / 8) * w.nbk, (uint32_t)(kc * 4));
-  }
-  auto wsload = [&](int c) -> uint32_t { return bload4(rw, c < kc ? (uint32_t)(c * 4) : kOOB); };
-  auto refill = [&](int slot, int c, int j, int q) {
-    const u32x4 lo = bload(c, j, q, 0);
-    wb[slot][j][q][0] = (int)lo[0];
-    wb[slot][j][q][1] = (int)lo[1];
-    wb[slot][j][q][2] = (int)lo[2];
-    wb[slot][j][q][3] = (int)lo[3];
-    if constexpr (FP8) {
-      const u32x4 hi = bload(c, j, q, 1);
-      wb[slot][j][q][4] = (int)hi[0];
-      wb[slot][j][q][5] = (int)hi[1];
-      wb[slot][j][q][6] = (int)hi[2];
-      wb[slot][j][q][7] = (int)hi[3];
-    }
-  };
-  auto fill_slot = [&](int slot) {
+    // Activations ride a register ring of DEPTH chunks (slot = (c - c0) %
+    // DEPTH) into the double-buffered LDS stage (buffer = (c - c0) & 1).
+    u32x4 apre[DEPTH][PIECES];
+    uint32_t spre[DEPTH];
+    auto fetch_a = [&](int aslot, int c) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        wb[slot][j][q] = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
-        refill(slot, slot, j, q);
+      for (int q = 0; q < PIECES; ++q) {
+        const int pc = tid + q * 256, row = pc / (ROWB / 16), kb = (pc % (ROWB / 16)) * 16;
+        apre[aslot][q] = bload16(rx, c < c1 ? (uint32_t)row * pitch + (uint32_t)(c * ROWB + kb) : kOOB);
       }
-    if constexpr (!FP8)
+      if constexpr (!FP8)
+        spre[aslot] = bload4(rs, (c < c1 && tid < ROWS) ? (uint32_t)(tid * (p.k_pad / 32) + c * 4) : kOOB);
+    };
+    auto store_a = [&](int aslot, int buf) {
 #pragma unroll
-      for (int q = 0; q < 2; ++q) wsb[slot][q] = sbload(slot, q);
-    if constexpr (FP8) wsv[slot] = wsload(slot);
-  };
-  float mref = 1.0f;
+      for (int q = 0; q < PIECES; ++q) {
+        const int pc = tid + q * 256, row = pc / (ROWB / 16), kb = (pc % (ROWB / 16)) * 16;
+        *(u32x4 *)(lds + buf * ABUF + row * STRIDE + kb) = apre[aslot][q];
+      }
+      if constexpr (!FP8) lds_s[buf][tid] = spre[aslot];
+    };
 
-  f32x16 acc[MT][2];
+    // Weights: wb[slot][j][q] is the B operand of step j, column tile q (fp4
+    // uses its low 4 dwords).  A slot is refilled in place, after the MFMAs
+    // that read it, so the ring keeps its registers across the loop.
+    auto bload = [&](int c, int j, int q, int i) -> u32x4 {
+      const int strip = s0 + 2 * q + sub;
+      const bool valid = c < c1 && strip < w.n_strips;
+      const uint32_t off = valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * TILE +
+                                       (uint32_t)(((2 * j + h) * 16 + r) * (16 * BW) + 16 * i)
+                                 : kOOB;
+      return bload16(rt, off);
+    };
+    auto sbload = [&](int c, int q) -> uint32_t {  // MXFP4 weight scales of row r, k blocks 0..3
+      const int strip = s0 + 2 * q + sub;
+      const bool valid = c < c1 && strip < w.n_strips;
+      return bload4(rb, valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * 64u + (uint32_t)(r * 4) : kOOB);
+    };
+    i32x8 wb[DEPTH][2][2];
+    uint32_t wsb[DEPTH][2];
+    // FP8_BLOCK: the wave's 128x128 block scale of chunk c rides the ring with
+    // the chunk's weights (one uniform dword load per chunk)
+    uint32_t wsv[DEPTH];
+    rsrc_t rw = rx;
+    if constexpr (FP8) {
+      const int sb = s0 < w.n_strips ? s0 : (int)w.n_strips - 1;
+      rw = make_rsrc(w.block_scale + (int64_t)(sb / 8) * w.nbk, (uint32_t)(kc * 4));
+    }
+    auto wsload = [&](int c) -> uint32_t { return bload4(rw, c < c1 ? (uint32_t)(c * 4) : kOOB); };
+    auto refill = [&](int slot, int c, int j, int q) {
+      const u32x4 lo = bload(c, j, q, 0);
+      wb[slot][j][q][0] = (int)lo[0];
+      wb[slot][j][q][1] = (int)lo[1];
+      wb[slot][j][q][2] = (int)lo[2];
+      wb[slot][j][q][3] = (int)lo[3];
+      if constexpr (FP8) {
+        const u32x4 hi = bload(c, j, q, 1);
+        wb[slot][j][q][4] = (int)hi[0];
+        wb[slot][j][q][5] = (int)hi[1];
+        wb[slot][j][q][6] = (int)hi[2];
+        wb[slot][j][q][7] = (int)hi[3];
+      }
+    };
+    auto fill_slot = [&](int slot, int c) {
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+        for (int q = 0; q < 2; ++q) {
+          wb[slot][j][q] = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
+          refill(slot, c, j, q);
+        }
+      if constexpr (!FP8)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][q][v] = 0.0f;
+        for (int q = 0; q < 2; ++q) wsb[slot][q] = sbload(c, q);
+      if constexpr (FP8) wsv[slot] = wsload(c);
+    };
+    float mref = 1.0f;
 
-  // Prologue in the steady state's load order -- activations of chunk j,
-  // then weights of chunk j-1 -- so the first chunks wait like every other:
-  // chunk c waits for the activations of chunk c+1, issued DEPTH chunks
-  // earlier, and leaves everything issued after them in flight.
-  fetch_a(0, 0);
-  store_a(0, 0);
+    f32x16 acc[MT][2];
 #pragma unroll
-  for (int j = 1; j <= DEPTH; ++j) {
-    __builtin_amdgcn_sched_barrier(0);
-    fetch_a(j % DEPTH, j);
-    __builtin_amdgcn_sched_barrier(0);
-    fill_slot(j - 1);
-  }
-  __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][q][e] = 0.0f;
 
-  auto chunk = [&](int slot, int c) {
-    const int aslot = (slot + 1) % DEPTH;  // holds the activations of chunk c+1
-    __syncthreads();  // buffer c&1 written; buffer (c+1)&1 no longer read
-    store_a(aslot, (c + 1) & 1);
-    fetch_a(aslot, c + 1 + DEPTH);
-    // the activation loads stay ahead of this chunk's weight refills, so the
-    // wait for them leaves the refills in flight
-    __builtin_amdgcn_sched_barrier(0);
-    const uint8_t *base = lds + (c & 1) * ABUF;
-    // every activation operand (and MXFP4 scale word) of the chunk, read at once
-    i32x8 a[2][MT];
-    uint32_t asw[MT];
+    // Chunk c: barrier; read its activations from its LDS buffer; MFMAs, each
+    // weight slot refilled with chunk c+DEPTH after use; then store the
+    // activations of chunk c+1 (issued DEPTH chunks earlier) into the other
+    // buffer, free since the barrier, and fetch those of chunk c+1+DEPTH.
+    // The store's wait for its data thus comes after the chunk's MFMAs are
+    // issued.  Loads go out as weights of chunk j-1, then activations of
+    // chunk j, in the prologue as in the loop, so every wait is the same.
+    __syncthreads();  // the previous segment's reads of buffer 0 are done
+    fetch_a(0, c0);
+    store_a(0, 0);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int row = mt * 32 + (lane & 31);
+    for (int j = 1; j <= DEPTH; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      fill_slot(j - 1, c0 + j - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      fetch_a(j % DEPTH, c0 + j);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    auto chunk = [&](int slot, int c) {
+      const int aslot = (slot + 1) % DEPTH;  // holds the activations of chunk c+1
+      const int buf = (c - c0) & 1;
+      __syncthreads();  // this chunk's buffer written; the other one no longer read
+      const uint8_t *base = lds + buf * ABUF;
+      // every activation operand (and MXFP4 scale word) of the chunk, read at once
+      i32x8 a[2][MT];
+      uint32_t asw[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int row = mt * 32 + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint8_t *ap = base + row * STRIDE + (FP8 ? 64 * j + 32 * h : 32 * j + 16 * h);
+          const u32x4 a0 = *(const u32x4 *)ap;
+          if constexpr (FP8) {
+            const u32x4 a1 = *(const u32x4 *)(ap + 16);
+            a[j][mt] = (i32x8){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
+                               (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+          } else {
+            a[j][mt] = (i32x8){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], 0, 0, 0, 0};
+          }
+        }
+        if constexpr (!FP8) asw[mt] = lds_s[buf][row];
+      }
+      int bsc = 127;
+      bool live = true;
+      float ratio = 1.0f;  // FP8: applied to each tile just before its first MFMA of the chunk
+      if constexpr (FP8) {
+        const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(wsv[slot]));
+        live = ws != 0.0f;
+        if (live) {
+          int e;
+          const float m = __builtin_frexpf(ws, &e);
+          ratio = mref / m;  // exactly 1 when the mantissa repeats
+          mref = m;
+          bsc = 127 + e;
+          bsc = bsc < 0 ? 0 : (bsc > 254 ? 254 : bsc);
+        }
+      }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const uint8_t *ap = base + row * STRIDE + (FP8 ? 64 * j + 32 * h : 32 * j + 16 * h);
-        const u32x4 a0 = *(const u32x4 *)ap;
-        if constexpr (FP8) {
-          const u32x4 a1 = *(const u32x4 *)(ap + 16);
-          a[j][mt] = (i32x8){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
-                             (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
-        } else {
-          a[j][mt] = (i32x8){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], 0, 0, 0, 0};
-        }
-      }
-      if constexpr (!FP8) asw[mt] = lds_s[c & 1][row];
-    }
-    int bsc = 127;
-    bool live = true;
-    float ratio = 1.0f;  // FP8: applied to each tile just before its first MFMA of the chunk
-    if constexpr (FP8) {
-      const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(wsv[slot]));
-      live = ws != 0.0f;
-      if (live) {
-        int e;
-        const float m = __builtin_frexpf(ws, &e);
-        ratio = mref / m;  // exactly 1 when the mantissa repeats
-        mref = m;
-        bsc = 127 + e;
-        bsc = bsc < 0 ? 0 : (bsc > 254 ? 254 : bsc);
-      }
-    }
+        int sbq[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      int sbq[2];
+        for (int q = 0; q < 2; ++q) sbq[q] = FP8 ? bsc : (int)((wsb[slot][q] >> (8 * (2 * j + h))) & 0xff);
+        if (live) {
 #pragma unroll
-      for (int q = 0; q < 2; ++q) sbq[q] = FP8 ? bsc : (int)((wsb[slot][q] >> (8 * (2 * j + h))) & 0xff);
-      if (live) {
+          for (int mt = 0; mt < MT; ++mt) {
+            const int asc = FP8 ? 127 : (int)((asw[mt] >> (8 * (2 * j + h))) & 0xff);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int asc = FP8 ? 127 : (int)((asw[mt] >> (8 * (2 * j + h))) & 0xff);
-#pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            if constexpr (FP8)
-              if (j == 0) acc[mt][q] *= ratio;
-            acc[mt][q] = mfma_scaled32<FP8>(a[j][mt], wb[slot][j][q], acc[mt][q], asc, sbq[q]);
-          }
-        }
-        if constexpr (FP8)
-          if (j == 0) {
-            // each tile's 16 rescale multiplies run under the previous tile's MFMA
-#pragma unroll
-            for (int t = 0; t < 2 * MT; ++t) {
-              __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // VALU
-              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            for (int q = 0; q < 2; ++q) {
+              if constexpr (FP8)
+                if (j == 0) acc[mt][q] *= ratio;
+              acc[mt][q] = mfma_scaled32<FP8>(a[j][mt], wb[slot][j][q], acc[mt][q], asc, sbq[q]);
             }
           }
+          if constexpr (FP8)
+            if (j == 0) {
+              // each tile's 16 rescale multiplies run under the previous tile's MFMA
+#pragma unroll
+              for (int tt = 0; tt < 2 * MT; ++tt) {
+                __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // VALU
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+              }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) refill(slot, c + DEPTH, j, q);
       }
+      if constexpr (!FP8)
 #pragma unroll
-      for (int q = 0; q < 2; ++q) refill(slot, c + DEPTH, j, q);
+        for (int q = 0; q < 2; ++q) wsb[slot][q] = sbload(c + DEPTH, q);
+      if constexpr (FP8) wsv[slot] = wsload(c + DEPTH);
+      __builtin_amdgcn_sched_barrier(0);
+      store_a(aslot, buf ^ 1);
+      fetch_a(aslot, c + 1 + DEPTH);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    int c = c0;
+    for (; c + DEPTH - 1 < c1; c += DEPTH) {
+#pragma unroll
+      for (int slot = 0; slot < DEPTH; ++slot) chunk(slot, c + slot);
     }
-    if constexpr (!FP8)
 #pragma unroll
-      for (int q = 0; q < 2; ++q) wsb[slot][q] = sbload(c + DEPTH, q);
-    if constexpr (FP8) wsv[slot] = wsload(c + DEPTH);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  int c = 0;
-  for (; c + DEPTH - 1 < kc; c += DEPTH) {
-#pragma unroll
-    for (int slot = 0; slot < DEPTH; ++slot) chunk(slot, c + slot);
-  }
-#pragma unroll
-  for (int slot = 0; slot + 1 < DEPTH; ++slot)
-    if (c + slot < kc) chunk(slot, c + slot);
+    for (int slot = 0; slot + 1 < DEPTH; ++slot)
+      if (c + slot < c1) chunk(slot, c + slot);
 
-  // FP8: per-row factor xs[m] * mref (rows past M read as 0 and are not stored)
-  float rowf[MT][16];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) rowf[mt][v] = 1.0f;
-  if constexpr (FP8) {
-    const rsrc_t rxs = make_rsrc((const float *)p.xs + m0, (uint32_t)mrows * 4u);
+    // The segment's sum over its chunks, without the per-token factor.
+    float sum[kNativeAcc];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v)
-        rowf[mt][v] = __builtin_bit_cast(float, bload4(rxs, (uint32_t)(mt * 32 + 8 * (v / 4) + 4 * h + (v % 4)) * 4u)) * mref;
-  }
-  const bool full = m0 + ROWS <= p.M;
-  auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
-    typedef decltype(yd) Y;
-    constexpr bool CHK = decltype(chk)::value;  // row checks only for the ragged last row tile
+      for (int q = 0; q < 2; ++q)
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);
-      if (col >= w.N) continue;
+        for (int e = 0; e < 16; ++e) sum[(mt * 2 + q) * 16 + e] = FP8 ? acc[mt][q][e] * mref : acc[mt][q][e];
+
+    if (P > 1) {
+      // Split tile.  Each piece publishes its partial with agent-scope
+      // relaxed atomic stores, waits for them (vmcnt 0), then counts itself
+      // in; the last to arrive adds the P partials in piece order -- the
+      // same order whichever piece is last, so the result does not depend
+      // on timing -- writes the tile and re-arms the counter.
+      float *mine = p.part + ((size_t)t * P + piece) * (kNativeAcc * 256);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int64_t rb = m0 + mt * 32 + 4 * h;
-        typename Y::T *py = (typename Y::T *)p.y + rb * w.N + col;
+      for (int e = 0; e < kNativeAcc; ++e)
+        __hip_atomic_store(&mine[e * 256 + tid], sum[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();  // every wave's partial stores are complete
+      if (tid == 0) lds_last = __hip_atomic_fetch_add(&p.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1;
+      __syncthreads();
+      if (!lds_last) return;
+      const rsrc_t rp = make_rsrc(p.part, (uint32_t)((size_t)nt * mtiles * P * kNativeAcc * 256 * 4));
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int rr = 8 * (v / 4) + (v % 4);
-          if (!CHK || rb + rr < p.M) py[rr * w.N] = Y::conv(FP8 ? acc[mt][q][v] * rowf[mt][v] : acc[mt][q][v]);
+      for (int eb = 0; eb < kNativeAcc; eb += 16) {  // 16 values at a time keeps registers in check
+        float tot[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tot[e] = 0.0f;
+        for (int u = 0; u < P; ++u) {
+          if (u == piece) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) tot[e] += sum[eb + e];
+            continue;
+          }
+          const uint32_t base_off = (uint32_t)(((size_t)t * P + u) * (kNativeAcc * 256) + tid) * 4u;
+          float pv[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            pv[e] = __uint_as_float(
+                (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, (int)(base_off + (eb + e) * 1024u), 0, kSC1));
+#pragma unroll
+          for (int e = 0; e < 16; ++e) tot[e] += pv[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sum[eb + e] = tot[e];
+      }
+      if (tid == 0) __hip_atomic_store(&p.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // Epilogue: y = sum (x the FP8 per-token scale), rows past M not stored.
+    float rowf[MT][16];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) rowf[mt][e] = 1.0f;
+    if constexpr (FP8) {
+      const rsrc_t rxs = make_rsrc((const float *)p.xs + m0, (uint32_t)mrows * 4u);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          rowf[mt][e] = __builtin_bit_cast(float, bload4(rxs, (uint32_t)(mt * 32 + 8 * (e / 4) + 4 * h + (e % 4)) * 4u));
+    }
+    const bool full = m0 + ROWS <= p.M;
+    auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
+      typedef decltype(yd) Y;
+      constexpr bool CHK = decltype(chk)::value;  // row checks only for the ragged last row tile
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);
+        if (col >= w.N) continue;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int64_t rbase = m0 + mt * 32 + 4 * h;
+          typename Y::T *py = (typename Y::T *)p.y + rbase * w.N + col;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int rr = 8 * (e / 4) + (e % 4);
+            if (!CHK || rbase + rr < p.M) py[rr * w.N] = Y::conv(sum[(mt * 2 + q) * 16 + e] * rowf[mt][e]);
+          }
         }
       }
-    }
-  };
-  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
-    if (full) body(yd, std::false_type{});
-    else body(yd, std::true_type{});
-  });
+    };
+    with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+      if (full) body(yd, std::false_type{});
+      else body(yd, std::true_type{});
+    });
+  }
+}
+
+// k pieces per tile: 1 (whole tiles) when the tiles fill every resident
+// workgroup slot, else as many as fit in one round of slots, each at least
+// kNativeMinChunks chunks long.
+static int native_pieces(int occ, int64_t tiles, int64_t kc) {
+  const int64_t slots = (int64_t)occ * device_cus();
+  int64_t P = tiles >= slots ? 1 : slots / tiles;
+  const int64_t cap = kc / kNativeMinChunks;
+  if (P > cap) P = cap;
+  return (int)(P < 1 ? 1 : P);
 }
 
 template <int FMT, int MT, int OCC, int DEPTH>
 static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M, int64_t k_pad,
-                                void *y, int y_dtype, hipStream_t st) {
+                                void *y, int y_dtype, float *part, size_t part_bytes, int *cnt, size_t cnt_count,
+                                hipStream_t st) {
   constexpr int ROWS = 32 * MT;
   constexpr int64_t TILE = FMT == DIALQ_FORMAT_FP8_BLOCK ? 2048 : 1024;
   const int64_t pitch = FMT == DIALQ_FORMAT_FP8_BLOCK ? k_pad : k_pad / 2;
@@ -818,21 +920,34 @@ static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const vo
   if (w.n_strips * w.k_chunks * TILE >= ((int64_t)1 << 31) || ROWS * pitch >= ((int64_t)1 << 31))
     return hipErrorInvalidValue;
   const int64_t tiles = ((w.n_strips + 15) / 16) * ((M + ROWS - 1) / ROWS);
-  if (tiles > 0x7fffffff) return hipErrorInvalidValue;
-  NativeParams p{w, xq, xs, M, k_pad, y, y_dtype};
-  k_gemm_native<FMT, MT, OCC, DEPTH><<<dim3((unsigned)tiles), 256, 0, st>>>(p);
+  const int P = native_pieces(OCC, tiles, w.k_chunks);
+  if (tiles * P > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (P > 1 && ((size_t)tiles > cnt_count || (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) > part_bytes))
+    return hipErrorInvalidValue;
+  NativeParams p{w, xq, xs, M, k_pad, y, y_dtype, P, part, cnt};
+  k_gemm_native<FMT, MT, OCC, DEPTH><<<dim3((unsigned)(tiles * P)), 256, 0, st>>>(p);
   return hipGetLastError();
 }
 
+void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count) {
+  const int occ = w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4;
+  const int rows = 32 * (w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
+  const int64_t tiles = ((w.n_strips + 15) / 16) * ((M + rows - 1) / rows);
+  const int P = native_pieces(occ, tiles, w.k_chunks);
+  part_bytes = P > 1 ? (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) : 0;
+  cnt_count = P > 1 ? (size_t)tiles : 0;
+}
+
 hipError_t launch_gemm_native(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M,
-                              int64_t k_pad, void *y, int y_dtype, hipStream_t st) {
+                              int64_t k_pad, void *y, int y_dtype, float *part, size_t part_bytes, int *cnt,
+                              size_t cnt_count, hipStream_t st) {
   if (k_pad != w.k_chunks * 128) return hipErrorInvalidValue;
   if (w.fmt == DIALQ_FORMAT_FP8_BLOCK)
-    return native_launch<DIALQ_FORMAT_FP8_BLOCK, NATIVE_MT_FP8, NATIVE_OCC_FP8, NATIVE_DEPTH_FP8>(w, xq, xs, M, k_pad, y,
-                                                                                                y_dtype, st);
+    return native_launch<DIALQ_FORMAT_FP8_BLOCK, NATIVE_MT_FP8, NATIVE_OCC_FP8, NATIVE_DEPTH_FP8>(
+        w, xq, xs, M, k_pad, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
   if (w.fmt == DIALQ_FORMAT_MXFP4)
-    return native_launch<DIALQ_FORMAT_MXFP4, NATIVE_MT_FP4, NATIVE_OCC_FP4, NATIVE_DEPTH_FP4>(w, xq, xs, M, k_pad, y,
-                                                                                             y_dtype, st);
+    return native_launch<DIALQ_FORMAT_MXFP4, NATIVE_MT_FP4, NATIVE_OCC_FP4, NATIVE_DEPTH_FP4>(
+        w, xq, xs, M, k_pad, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
   return hipErrorInvalidValue;
 }
 

@@ -789,7 +789,7 @@ __global__ __launch_bounds__(64 * (kDynWaves + 1)) void k_gemv_dyn(DynParams p) 
 // ---------------------------------------------------------------------------
 // host dispatch
 // ---------------------------------------------------------------------------
-static int device_cus() {
+int device_cus() {
   static int cus = 0;
   if (cus == 0) {
     int dev = 0, n = 0;

@@ -57,9 +57,15 @@ hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t 
                        int y_dtype, hipStream_t st);
 // Native low-precision prefill: FP8_BLOCK with per-token fp8 activations,
 // MXFP4 with per-32 MXFP4 activations.  `xq` / `xs` are the quantized
-// activations (codes and scales) produced by launch_act_*.
+// activations (codes and scales) produced by launch_act_*.  The stream-K
+// schedule needs native_workspace(M, w) of scratch: `part` (partial tiles)
+// and `cnt` (per-tile counters, zero before the call and left zero after it).
+void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count);
 hipError_t launch_gemm_native(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M,
-                              int64_t k_pad, void *y, int y_dtype, hipStream_t st);
+                              int64_t k_pad, void *y, int y_dtype, float *part, size_t part_bytes, int *cnt,
+                              size_t cnt_count, hipStream_t st);
+// Compute units of the current device (cached at first use).
+int device_cus();
 // Local q8 W8A8 decode (one row).
 hipError_t launch_local_q8(const WeightView &w, const void *x, int x_dtype, void *y, int y_dtype,
                            void *scratch, hipStream_t st);

@@ -624,6 +624,16 @@ __device__ __forceinline__ void load8(const void *x, int64_t e, float (&v)[8]) {
 // FP8: one 256-thread block per token.  G > 0 keeps the row's 8-value
 // groups in registers (K <= 2048 * G), so the row is read once; G == 0 reads
 // it twice (amax pass, then conversion).
+// Four E4M3 codes, RNE, by the hardware converter.  For finite inputs of
+// magnitude below 464 it agrees with f32_to_e4m3 (x / s never exceeds 448 by
+// more than rounding); NaN takes f32_to_e4m3's code 0x7f.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  if (a != a || b != b || c != c || d != d)
+    return f32_to_e4m3(a) | (f32_to_e4m3(b) << 8) | (f32_to_e4m3(c) << 16) | (f32_to_e4m3(d) << 24);
+  uint32_t r = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)r, true);
+}
+
 template <int ACT, int G>
 __global__ __launch_bounds__(256) void k_act_fp8_v8(const void *x, int64_t K, uint8_t *q, float *scale,
                                                     int64_t k_pad) {
@@ -653,12 +663,10 @@ __global__ __launch_bounds__(256) void k_act_fp8_v8(const void *x, int64_t K, ui
   const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
   const float inv = 1.0f / s;
   auto put = [&](int64_t g, const float (&u)[8]) {
-    uint2 out = {0u, 0u};
+    float t[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      out.x |= (uint32_t)f32_to_e4m3(u[e] * inv) << (8 * e);
-      out.y |= (uint32_t)f32_to_e4m3(u[4 + e] * inv) << (8 * e);
-    }
+    for (int e = 0; e < 8; ++e) t[e] = u[e] * inv;
+    const uint2 out = {e4m3x4(t[0], t[1], t[2], t[3]), e4m3x4(t[4], t[5], t[6], t[7])};
     *(uint2 *)(q + row * k_pad + 8 * g) = out;
   };
   if constexpr (G > 0) {
@@ -698,9 +706,22 @@ __global__ __launch_bounds__(256) void k_act_mxfp4_v8(const void *x, int64_t M, 
   amax = fmaxf(amax, __shfl_xor(amax, 2));
   int shared = amax > 0.0f ? floor_log2_pos(amax) - 2 : -127;
   shared = shared < -127 ? -127 : (shared > 127 ? 127 : shared);
-  uint32_t codes = 0;
+  bool nan = false;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) codes |= f32_to_e2m1(ldexpf(v[e], -shared)) << (4 * e);
+  for (int e = 0; e < 8; ++e) nan |= v[e] != v[e];
+  uint32_t codes = 0;
+  if (shared >= -126 && !nan) {
+    // hardware E2M1 conversion of v / 2^shared (RNE, saturating at 6); the
+    // scale is a normal f32 here, and NaN inputs take the path below
+    const float sc = __builtin_bit_cast(float, (uint32_t)(shared + 127) << 23);
+    codes = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(codes, v[0], v[1], sc, 0);
+    codes = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(codes, v[2], v[3], sc, 1);
+    codes = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(codes, v[4], v[5], sc, 2);
+    codes = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(codes, v[6], v[7], sc, 3);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) codes |= f32_to_e2m1(ldexpf(v[e], -shared)) << (4 * e);
+  }
   *(uint32_t *)(packed + row * (k_pad / 2) + 4 * g) = codes;
   if ((g & 3) == 0) scales[row * (k_pad / 32) + g / 4] = (uint8_t)(shared + 127);
 }

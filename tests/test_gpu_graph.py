@@ -44,3 +44,31 @@ def test_graph_replay_matches_eager(fmt, n, torch_dev):
             other.forward(x, y_other, path=dq.PATH_GEMV, stream=stream)
             torch.cuda.synchronize()
             assert np.isfinite(y_other.float().cpu().numpy()).all()
+
+
+@pytest.mark.parametrize("fmt", [dq.FP8_BLOCK, dq.MXFP4], ids=lambda f: dq.FORMAT_NAMES[f])
+def test_graph_replay_native_prefill(fmt, torch_dev):
+    """The native prefill's stream-K schedule splits tiles between
+    workgroups; their per-tile arrival counters are reset by the last
+    arriver, so graph replays reproduce the eager result bit for bit."""
+    import torch
+    n, k, m = 300, 2560, 300
+    raw, scales, ckw, _ = make_weight(fmt, n, k, 70 + fmt)
+    lin = dq.Linear.create(fmt, n, k, raw, scales, **ckw)
+    x = torch.randn(m, k, device=torch_dev).to(torch.bfloat16)
+    y_eager = torch.empty(m, n, device=torch_dev, dtype=torch.bfloat16)
+    y_graph = torch.empty_like(y_eager)
+    stream = torch.cuda.current_stream()
+    lin.forward(x, y_eager, path=dq.PATH_GEMM_NATIVE, stream=stream)  # sizes the scratch
+    torch.cuda.synchronize()
+    ref = y_eager.cpu()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        lin.forward(x, y_graph, path=dq.PATH_GEMM_NATIVE, stream=torch.cuda.current_stream())
+    for rep in range(4):
+        y_graph.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph.cpu(), ref), (dq.FORMAT_NAMES[fmt], rep)
+        lin.forward(x * 2, y_eager, path=dq.PATH_GEMM_NATIVE, stream=stream)
+        torch.cuda.synchronize()

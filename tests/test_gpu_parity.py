@@ -207,6 +207,29 @@ def test_native_prefill_long_k(fmt, torch_dev):
     assert rel <= TOL_LOWP, (dq.FORMAT_NAMES[fmt], rel)
 
 
+@pytest.mark.parametrize("fmt", [dq.FP8_BLOCK, dq.MXFP4], ids=["fp8_block", "mxfp4"])
+def test_native_prefill_stream_k_split_tiles(fmt, torch_dev):
+    """Tiles shared by several workgroups (stream-K): the result matches the
+    oracle and is bit-identical from call to call, whichever workgroup
+    finishes a shared tile last."""
+    import torch
+    n, k = 300, 2560
+    lin, _, _, deq = _linear(fmt, n, k, seed=95 + fmt)
+    for m in (300, 45):
+        rng = np.random.default_rng(m)
+        x = O.round_bf16(rng.normal(0, 1, (m, k)).astype(np.float32))
+        xt = to_torch(x, dq.BF16, torch_dev)
+        outs = []
+        for _ in range(3):
+            yt = empty_out(m, n, dq.F32, torch_dev)
+            lin.forward(xt, yt, path=dq.PATH_GEMM_NATIVE)
+            torch.cuda.synchronize()
+            outs.append(yt.cpu().numpy())
+        assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs[1:])
+        rel = O.rel_l2(O.round_bf16(outs[0]), _native_ref(fmt, x, deq))
+        assert rel <= TOL_LOWP, (dq.FORMAT_NAMES[fmt], m, rel)
+
+
 def _assert_bits_equal(got, want, x):
     # a code of -0 reaches the product as +0 (-0 + 0 = +0), so zeros compare by value
     bad = np.argwhere((got.view(np.uint32) != want.view(np.uint32)) & ~((got == 0) & (want == 0)))
@@ -214,6 +237,47 @@ def _assert_bits_equal(got, want, x):
         i, j = bad[0]
         raise AssertionError(f"{len(bad)} mismatches; first at {(i, j)}: got {got[i, j]!r} want {want[i, j]!r} "
                              f"x {x[i, j]!r}")
+
+
+def _tie_rows(k):
+    """Activation rows whose scaled values sit on the E4M3 / E2M1 rounding
+    ties and saturation edges: row 0 has amax 448 (FP8 scale 1), every
+    32-block of row 1 has amax 6 (MXFP4 shared exponent 0)."""
+    e4m3_ties = [1.0625, -1.1875, 2.5625, 0.0029296875, -0.0048828125, 0.0009765625, 447.9, 464.0 - 1e-3,
+                 240.0 + 8.0, 3.0 * 2 ** -10, 13.0, 0.001953125, 1e-30]
+    e2m1_ties = [0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.25, -0.75, -5.0, 0.1, 5.99, 1e-30, -2.5, 2.0, 0.5]
+    x = np.zeros((2, k), np.float32)
+    x[0, 0] = 448.0
+    x[0, 1:1 + len(e4m3_ties)] = e4m3_ties
+    for b in range(k // 32):
+        x[1, 32 * b] = 6.0
+        x[1, 32 * b + 1:32 * b + 1 + len(e2m1_ties)] = e2m1_ties
+    return x
+
+
+def test_native_activation_quantizer_ties(torch_dev):
+    """Rounding ties, subnormal codes and saturation of both activation
+    quantizers, bit-exact against the oracle through an identity weight."""
+    import torch
+    k = 384
+    x = np.concatenate([_tie_rows(k), np.random.default_rng(5).normal(0, 1, (6, k)).astype(np.float32)])
+    q = np.zeros((k, k), np.uint8)
+    np.fill_diagonal(q, 0x38)
+    lin = dq.Linear.create(dq.FP8_BLOCK, k, k, q, np.ones((3, 3), np.float32))
+    y = empty_out(len(x), k, dq.F32, torch_dev)
+    lin.forward(to_torch(x, dq.F32, torch_dev), y, path=dq.PATH_GEMM_NATIVE)
+    torch.cuda.synchronize()
+    qx, sx = O.act_fp8_quantize(x)
+    _assert_bits_equal(y.cpu().numpy(), (O.e4m3_to_f32(qx) * sx[:, None]).astype(np.float32), x)
+    p = np.zeros((k, k // 2), np.uint8)
+    for i in range(k):
+        p[i, i // 2] |= 2 << (4 * (i % 2))
+    lin = dq.Linear.create(dq.MXFP4, k, k, p, np.full((k, k // 32), 127, np.uint8))
+    y = empty_out(len(x), k, dq.F32, torch_dev)
+    lin.forward(to_torch(x, dq.F32, torch_dev), y, path=dq.PATH_GEMM_NATIVE)
+    torch.cuda.synchronize()
+    px, sxm = O.act_mxfp4_quantize(x)
+    _assert_bits_equal(y.cpu().numpy(), O.mxfp4_dequant(px, sxm).astype(np.float32), x)
 
 
 @pytest.mark.parametrize("x_dtype", [dq.BF16, dq.F16, dq.F32], ids=["bf16", "f16", "f32"])
