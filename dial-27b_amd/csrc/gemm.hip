@@ -561,7 +561,11 @@ __device__ __forceinline__ f32x16 mfma_scaled32(i32x8 a, i32x8 b, f32x16 c, int 
 #endif
 
 constexpr int kNativeAcc = 64;       // f32 accumulators per thread (MT = 2: 2 x 2 tiles x 16)
-constexpr int kNativeMinChunks = 8;  // fewest k chunks per workgroup in the stream-K split
+// Fewest k chunks per piece of a split tile: a piece's partial (64 KB out,
+// read back by the last piece) must be worth the extra parallelism; fp4
+// chunks take half the MFMA time of fp8 ones (measured: MXFP4 k/v and q/o
+// at 27B shapes are faster unsplit, the 136-chunk down projection split).
+constexpr int native_min_chunks(int fmt) { return fmt == DIALQ_FORMAT_FP8_BLOCK ? 8 : 32; }
 
 template <int FMT, int MT, int OCC, int DEPTH>
 __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
@@ -900,11 +904,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 
 // k pieces per tile: 1 (whole tiles) when the tiles fill every resident
 // workgroup slot, else as many as fit in one round of slots, each at least
-// kNativeMinChunks chunks long.
-static int native_pieces(int occ, int64_t tiles, int64_t kc) {
+// native_min_chunks chunks long.
+static int native_pieces(int fmt, int occ, int64_t tiles, int64_t kc) {
   const int64_t slots = (int64_t)occ * device_cus();
   int64_t P = tiles >= slots ? 1 : slots / tiles;
-  const int64_t cap = kc / kNativeMinChunks;
+  const int64_t cap = kc / native_min_chunks(fmt);
   if (P > cap) P = cap;
   return (int)(P < 1 ? 1 : P);
 }
@@ -920,7 +924,7 @@ static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const vo
   if (w.n_strips * w.k_chunks * TILE >= ((int64_t)1 << 31) || ROWS * pitch >= ((int64_t)1 << 31))
     return hipErrorInvalidValue;
   const int64_t tiles = ((w.n_strips + 15) / 16) * ((M + ROWS - 1) / ROWS);
-  const int P = native_pieces(OCC, tiles, w.k_chunks);
+  const int P = native_pieces(FMT, OCC, tiles, w.k_chunks);
   if (tiles * P > 0x7fffffffLL) return hipErrorInvalidValue;
   if (P > 1 && ((size_t)tiles > cnt_count || (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) > part_bytes))
     return hipErrorInvalidValue;
@@ -933,7 +937,7 @@ void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t
   const int occ = w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4;
   const int rows = 32 * (w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
   const int64_t tiles = ((w.n_strips + 15) / 16) * ((M + rows - 1) / rows);
-  const int P = native_pieces(occ, tiles, w.k_chunks);
+  const int P = native_pieces(w.fmt, occ, tiles, w.k_chunks);
   part_bytes = P > 1 ? (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) : 0;
   cnt_count = P > 1 ? (size_t)tiles : 0;
 }

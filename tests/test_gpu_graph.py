@@ -52,7 +52,7 @@ def test_graph_replay_native_prefill(fmt, torch_dev):
     workgroups; their per-tile arrival counters are reset by the last
     arriver, so graph replays reproduce the eager result bit for bit."""
     import torch
-    n, k, m = 300, 2560, 300
+    n, k, m = 300, 8192, 300  # 64 chunks: FP8 tiles split in 8 pieces, MXFP4 in 2
     raw, scales, ckw, _ = make_weight(fmt, n, k, 70 + fmt)
     lin = dq.Linear.create(fmt, n, k, raw, scales, **ckw)
     x = torch.randn(m, k, device=torch_dev).to(torch.bfloat16)

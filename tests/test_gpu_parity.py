@@ -213,7 +213,7 @@ def test_native_prefill_stream_k_split_tiles(fmt, torch_dev):
     oracle and is bit-identical from call to call, whichever workgroup
     finishes a shared tile last."""
     import torch
-    n, k = 300, 2560
+    n, k = 300, 8192  # 64 chunks: FP8 tiles split in 8 pieces, MXFP4 in 2
     lin, _, _, deq = _linear(fmt, n, k, seed=95 + fmt)
     for m in (300, 45):
         rng = np.random.default_rng(m)
