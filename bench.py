@@ -18,7 +18,9 @@ roofline of the dominant kernel and the CPU baseline.
 
 `--profile` runs only the dominant kernel (W8A16 gate GEMV, eager launches
 over rotating copies) plus a 256 MiB device-to-device copy used to scale the
-HBM byte counters; it is the program the committed rocprofv3 summaries run.
+HBM byte counters; `--profile-prefill` runs only the prefill GEMMs of one
+layer per format.  They are the programs the committed rocprofv3 summaries
+run.
 """
 from __future__ import annotations
 
@@ -35,6 +37,9 @@ HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "fp4": 10100.0}
 LAYER_27B = [("q", 6144, 5120), ("k", 1024, 5120), ("v", 1024, 5120), ("o", 5120, 6144),
              ("gate", 17408, 5120), ("up", 17408, 5120), ("down", 5120, 17408)]
+# The same weights as the fused projections DIAL's Qwen3-VL layers run
+# (cat(q, k, v) rows and cat(gate, up) rows, qwen3_vl/text.rs): four linears.
+LAYER_27B_FUSED = [("qkv", 8192, 5120), ("o", 5120, 6144), ("gate_up", 34816, 5120), ("down", 5120, 17408)]
 METRIC = "quant GEMV weight GB/s (% HBM peak) + prefill GEMM TFLOP/s, 27B shapes, 1 GPU"
 
 
@@ -44,7 +49,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--copies", type=int, default=3, help="layer copies rotated per step")
-    ap.add_argument("--prefill-iters", type=int, default=5)
+    ap.add_argument("--prefill-iters", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--sweep", default="w8a16,q4_k,fp8_block,mxfp4",
@@ -52,6 +57,8 @@ def parse():
     ap.add_argument("--profile", action="store_true",
                     help="only the dominant kernel's launches and the calibration copy (for rocprofv3)")
     ap.add_argument("--profile-launches", type=int, default=50)
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="only the prefill GEMMs of one layer per format (for rocprofv3)")
     return ap.parse_args()
 
 
@@ -83,12 +90,12 @@ def read_traffic():
         return None
 
 
-def build_layers(dq, torch, fmt, copies, dev, seed=0):
+def build_layers(dq, torch, fmt, copies, dev, seed=0, shapes=LAYER_27B):
     g = torch.Generator(device=dev).manual_seed(seed)
     layers = []
     for _ in range(copies):
         lins = []
-        for name, n, k in LAYER_27B:
+        for name, n, k in shapes:
             w = torch.randn(n, k, device=dev, generator=g, dtype=torch.float32) * 0.02
             lins.append(dq.Linear.quantize(fmt, w, scale_dtype=dq.BF16))
             del w
@@ -97,8 +104,8 @@ def build_layers(dq, torch, fmt, copies, dev, seed=0):
     return layers
 
 
-def layer_bytes(dq, fmt):
-    return sum(dq.raw_weight_bytes(fmt, n, k) for _, n, k in LAYER_27B)
+def layer_bytes(dq, fmt, shapes=LAYER_27B):
+    return sum(dq.raw_weight_bytes(fmt, n, k) for _, n, k in shapes)
 
 
 def decode_pass(dq, lins, xs, ys, stream):
@@ -106,11 +113,11 @@ def decode_pass(dq, lins, xs, ys, stream):
         lin.forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
 
 
-def time_decode(dq, torch, layers, steps, warmup, dev):
+def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B):
     """Wall time of `steps` decode passes, one HIP-graph replay per pass,
     rotating layer copies."""
-    xs = [torch.randn(1, k, device=dev).to(torch.bfloat16) for _, n, k in LAYER_27B]
-    ys = [torch.empty(1, n, device=dev, dtype=torch.bfloat16) for _, n, k in LAYER_27B]
+    xs = [torch.randn(1, k, device=dev).to(torch.bfloat16) for _, n, k in shapes]
+    ys = [torch.empty(1, n, device=dev, dtype=torch.bfloat16) for _, n, k in shapes]
     stream = torch.cuda.current_stream()
     for lins in layers:  # eager first: sizes the GEMV workspaces outside capture
         decode_pass(dq, lins, xs, ys, stream)
@@ -182,18 +189,40 @@ def profile_run(dq, torch, dev, launches):
           "(calibration: 268435456 bytes read and written per copy)", flush=True)
 
 
+def profile_prefill_run(dq, torch, dev, iters=5):
+    """Prefill GEMMs of one 27B layer, eager: FP8-128 and MXFP4 native at
+    M = 1024, W8A16 and Q4_K weight-only at M = 2048."""
+    for fmt, m, path in ((dq.FP8_BLOCK, 1024, dq.PATH_GEMM_NATIVE), (dq.MXFP4, 1024, dq.PATH_GEMM_NATIVE),
+                         (dq.W8A16, 2048, dq.PATH_GEMM), (dq.Q4_K, 2048, dq.PATH_GEMM)):
+        lins = build_layers(dq, torch, fmt, 1, dev)[0]
+        tf, secs = time_prefill(dq, torch, lins, m, iters, dev, path)
+        print(f"# profile prefill {dq.FORMAT_NAMES[fmt]} M={m}: {tf:.1f} TFLOP/s ({secs * 1e3:.3f} ms/layer)",
+              flush=True)
+        del lins
+        torch.cuda.empty_cache()
+
+
 def time_prefill(dq, torch, lins, m, iters, dev, path):
+    """Device time of one prefill pass over the layer's seven linears
+    (activation quantization included for the native paths), captured in a
+    HIP graph like the decode step and replayed `iters` times between HIP
+    events on the replay stream."""
     stream = torch.cuda.current_stream()
     xs = [torch.randn(m, k, device=dev).to(torch.bfloat16) for _, n, k in LAYER_27B]
     ys = [torch.empty(m, n, device=dev, dtype=torch.bfloat16) for _, n, k in LAYER_27B]
-    for lin, x, y in zip(lins, xs, ys):
-        lin.forward(x, y, path=path, stream=stream)
+
+    def body(st):
+        for lin, x, y in zip(lins, xs, ys):
+            lin.forward(x, y, path=path, stream=st)
+    body(stream)  # eager first: sizes the handles' scratch outside capture
+    torch.cuda.synchronize()
+    g = capture(torch, body)
+    g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(iters):
-        for lin, x, y in zip(lins, xs, ys):
-            lin.forward(x, y, path=path, stream=stream)
+        g.replay()
     e1.record(stream)
     e1.synchronize()
     secs = e0.elapsed_time(e1) * 1e-3 / iters
@@ -239,6 +268,9 @@ def main():
     if a.profile:
         profile_run(dq, torch, dev, a.profile_launches)
         return
+    if a.profile_prefill:
+        profile_prefill_run(dq, torch, dev)
+        return
     fmt_of = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}
 
     # ---- headline: W8A16 decode over the 27B layer -----------------------
@@ -266,13 +298,23 @@ def main():
           + ", ".join(f"{k}={v * 1e6:.1f}" for k, v in per.items()), file=sys.stderr, flush=True)
 
     extra = {"decode_gbs": {"w8a16": round(value, 1)}, "decode_us_per_launch_w8a16":
-             {k: round(v * 1e6, 2) for k, v in per.items()}, "prefill_tflops": {}}
+             {k: round(v * 1e6, 2) for k, v in per.items()}, "prefill_tflops": {}, "prefill_pct_mfma_peak": {}}
     sweep = [s for s in a.sweep.split(",") if s]
     if "w8a16" in sweep:
         tf, s2 = time_prefill(dq, torch, layers[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
         extra["prefill_tflops"]["w8a16_m2048"] = round(tf, 1)
+        extra["prefill_pct_mfma_peak"]["w8a16_m2048"] = round(100.0 * tf / MFMA_PEAK_TFLOPS["bf16"], 1)
         print(f"# w8a16 prefill M=2048: {tf:.1f} TFLOP/s ({s2 * 1e3:.2f} ms/layer)", file=sys.stderr, flush=True)
     del layers
+    torch.cuda.empty_cache()
+    # the same layer with fused qkv / gate_up projections (four linears)
+    fl = build_layers(dq, torch, dq.W8A16, a.copies, dev, seed=3, shapes=LAYER_27B_FUSED)
+    fsteps = max(a.steps // 3, 10)
+    fs = time_decode(dq, torch, fl, fsteps, 10, dev, shapes=LAYER_27B_FUSED)
+    extra["decode_gbs_fused_qkv_gate_up"] = {"w8a16": round(layer_bytes(dq, dq.W8A16, LAYER_27B_FUSED) * fsteps / fs / 1e9, 1)}
+    print(f"# w8a16 decode, fused qkv / gate_up: {extra['decode_gbs_fused_qkv_gate_up']['w8a16']} GB/s",
+          file=sys.stderr, flush=True)
+    del fl
     torch.cuda.empty_cache()
     for name in sweep:
         if name == "w8a16":
@@ -285,9 +327,12 @@ def main():
         if fmt in (dq.FP8_BLOCK, dq.MXFP4):
             tf, s2 = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE)
             extra["prefill_tflops"][name + "_native_m1024"] = round(tf, 1)
+            peak = MFMA_PEAK_TFLOPS["fp8" if fmt == dq.FP8_BLOCK else "fp4"]
+            extra["prefill_pct_mfma_peak"][name + "_native_m1024"] = round(100.0 * tf / peak, 1)
         else:
             tf, s2 = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
             extra["prefill_tflops"][name + "_m2048"] = round(tf, 1)
+            extra["prefill_pct_mfma_peak"][name + "_m2048"] = round(100.0 * tf / MFMA_PEAK_TFLOPS["bf16"], 1)
         print(f"# {name}: decode {gbs:.1f} GB/s, prefill {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)
         del ls
         torch.cuda.empty_cache()
