@@ -3,7 +3,10 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include <fstream>
+
 #include "dial_host.hpp"
+#include "gguf.hpp"
 
 namespace py = pybind11;
 using namespace dial;
@@ -37,6 +40,62 @@ py::array tensor_to_numpy(const Tensor &t) {
   py::array out(d, shape);
   if (!b.empty()) std::memcpy(out.mutable_data(), b.data(), b.size());
   return out;
+}
+
+py::object gguf_value_to_py(const gguf::Value &v) {
+  switch (v.type) {
+    case gguf::ValueType::U8:
+    case gguf::ValueType::U16:
+    case gguf::ValueType::U32:
+    case gguf::ValueType::U64:
+      return py::int_(v.u);
+    case gguf::ValueType::I8:
+    case gguf::ValueType::I16:
+    case gguf::ValueType::I32:
+    case gguf::ValueType::I64:
+      return py::int_(v.i);
+    case gguf::ValueType::F32:
+    case gguf::ValueType::F64:
+      return py::float_(v.f);
+    case gguf::ValueType::Bool:
+      return py::bool_(v.u != 0);
+    case gguf::ValueType::String:
+      return py::str(v.s);
+    case gguf::ValueType::Array: {
+      py::list l;
+      for (const gguf::Value &e : v.arr) l.append(gguf_value_to_py(e));
+      return l;
+    }
+  }
+  return py::none();
+}
+
+// The parsed header of a GGUF file: version, tensor_data_offset, metadata
+// {key: (type id, value)} and tensors {name: (ggml dtype name, dims, offset)}.
+py::dict gguf_read(const std::string &path) {
+  const gguf::Content c = gguf::read_file(path);
+  py::dict meta, tensors, out;
+  for (const auto &kv : c.metadata)
+    meta[py::str(kv.first)] = py::make_tuple((uint32_t)kv.second.type, gguf_value_to_py(kv.second));
+  for (const auto &kv : c.tensor_infos)
+    tensors[py::str(kv.first)] =
+        py::make_tuple(gguf::ggml_dtype_name(kv.second.ggml_dtype), kv.second.dims, kv.second.offset);
+  out["version"] = c.version;
+  out["tensor_data_offset"] = c.tensor_data_offset;
+  out["metadata"] = meta;
+  out["tensors"] = tensors;
+  return out;
+}
+
+py::bytes gguf_tensor_bytes(const std::string &path, const std::string &name) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) throw Error("cannot open " + path);
+  f.seekg(0, std::ios::end);
+  const uint64_t size = (uint64_t)f.tellg();
+  f.seekg(0);
+  const gguf::Content c = gguf::Content::read(f, size);
+  const std::vector<uint8_t> b = c.tensor_bytes(f, name);
+  return py::bytes((const char *)b.data(), b.size());
 }
 
 }  // namespace
@@ -104,7 +163,10 @@ PYBIND11_MODULE(dialq_host, m) {
       .def("resident_bytes", &W8A16Linear::resident_bytes);
 
   py::class_<GgufMatMul, std::shared_ptr<GgufMatMul>> gg(m, "GgufMatMul");
-  py::enum_<GgufMatMul::Kind>(gg, "Kind").value("Q8_0", GgufMatMul::Q8_0).value("Q4_K", GgufMatMul::Q4_K);
+  py::enum_<GgufMatMul::Kind>(gg, "Kind")
+      .value("Q8_0", GgufMatMul::Q8_0)
+      .value("Q4_K", GgufMatMul::Q4_K)
+      .value("Q6_K", GgufMatMul::Q6_K);
   gg.def_static("from_blocks", &GgufMatMul::from_blocks)
       .def_static("quantize", &GgufMatMul::quantize)
       .def("forward", &GgufMatMul::forward)
@@ -123,8 +185,17 @@ PYBIND11_MODULE(dialq_host, m) {
   m.def("configure_worker_w8a16_from_args", &configure_worker_w8a16_from_args);
   m.def("worker_w8a16_enabled", &worker_w8a16_enabled);
   m.def("worker_w8a16_summary", &worker_w8a16_summary);
-  m.def("set_worker_gguf_enabled", &set_worker_gguf_enabled);
+  m.def("configure_worker_gguf_from_args", &configure_worker_gguf_from_args, py::arg("path"),
+        py::arg("fp16_prefill"), py::arg("output_head"), py::arg("sample_token"), py::arg("worker_mode"),
+        py::arg("device"), py::arg("dtype"), py::arg("num_hidden_layers"));
   m.def("worker_gguf_enabled", &worker_gguf_enabled);
+  m.def("worker_gguf_fp16_prefill_enabled", &worker_gguf_fp16_prefill_enabled);
+  m.def("worker_gguf_output_head_requested", &worker_gguf_output_head_requested);
+  m.def("worker_gguf_sample_token_requested", &worker_gguf_sample_token_requested);
+  m.def("worker_gguf_summary", &worker_gguf_summary);
+  m.def("load_worker_gguf_linear", &load_worker_gguf_linear);
+  m.def("gguf_read", &gguf_read);
+  m.def("gguf_tensor_bytes", &gguf_tensor_bytes);
   m.def("worker_gguf_prefill_for_dims", &worker_gguf_prefill_for_dims);
   m.def("forward_worker_gguf", &forward_worker_gguf);
   m.def("build_worker_gguf_fp16_prefill_linear", &build_worker_gguf_fp16_prefill_linear);

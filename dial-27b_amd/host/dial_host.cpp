@@ -9,10 +9,13 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <fstream>
 #include <mutex>
+#include <shared_mutex>
 #include <sstream>
 
 #include "dialq.h"
+#include "gguf.hpp"
 
 namespace dial {
 
@@ -614,7 +617,7 @@ QuantLinear linear_no_bias(int64_t input_size, int64_t output_size, const VarSto
 namespace {
 std::atomic<bool> g_w8a16_enabled{false};
 std::atomic<size_t> g_w8a16_count{0}, g_w8a16_bytes{0};
-std::atomic<bool> g_gguf_enabled{false}, g_gguf_fp16_prefill{false};
+std::atomic<bool> g_gguf_fp16_prefill{false};
 }  // namespace
 
 void configure_worker_w8a16_from_args(bool requested, bool worker_mode, Device device, DType dtype) {
@@ -703,12 +706,179 @@ Tensor GgufMatMul::dequantize_f16() const {
   return dq_dequantize(*h_, DType::F16, out_dim_, in_dim_, Device::rocm(h_->device));
 }
 
-void set_worker_gguf_enabled(bool enabled, bool fp16_prefill) {
-  g_gguf_enabled.store(enabled);
-  g_gguf_fp16_prefill.store(enabled && fp16_prefill);
+// ---- GGUF worker source (worker_gguf.rs:19-25,65-197,388-397,462-572) -------
+namespace {
+struct WorkerGgufSource {
+  std::string path;
+  gguf::Content content;
+  std::mutex file_mu;  // the file position is shared: reads are serialized
+  std::ifstream file;
+  Device device;
+};
+std::shared_mutex g_gguf_mu;
+std::shared_ptr<WorkerGgufSource> g_gguf_source;
+std::atomic<bool> g_gguf_output_head{false}, g_gguf_sample_token{false};
+std::atomic<size_t> g_gguf_count{0}, g_gguf_bytes{0}, g_gguf_prefill_count{0}, g_gguf_prefill_bytes{0};
+std::atomic<unsigned> g_gguf_warmed{0};
+
+std::shared_ptr<WorkerGgufSource> gguf_source() {
+  std::shared_lock<std::shared_mutex> lk(g_gguf_mu);
+  return g_gguf_source;
 }
-bool worker_gguf_enabled() { return g_gguf_enabled.load(); }
+
+// warmup_worker_gguf (worker_gguf.rs:524-572): the first linear of each GGUF
+// dtype runs one F16 decode row and one 9-row F32 prefill, so the kernels'
+// first-launch cost is paid at load time.  DIAL_WORKER_GGUF_WARMUP=0 (or
+// false / FALSE / no / NO) skips it.
+void warmup_worker_gguf(const GgufMatMul &mm, gguf::GgmlDType dtype, int64_t in_dim, Device device) {
+  if (const char *e = getenv("DIAL_WORKER_GGUF_WARMUP")) {
+    const std::string v = e;
+    if (v == "0" || v == "false" || v == "FALSE" || v == "no" || v == "NO") return;
+  }
+  const unsigned bit = dtype == gguf::GgmlDType::Q4K ? 1u : dtype == gguf::GgmlDType::Q6K ? 2u : 4u;
+  if (g_gguf_warmed.fetch_or(bit) & bit) return;
+  try {
+    std::vector<uint16_t> z16((size_t)in_dim, 0);
+    Tensor decode = Tensor::from_host(z16.data(), DType::F16, {1, 1, in_dim}).to_device(device);
+    Tensor out = forward_worker_gguf(mm, decode);
+    if (out.dtype() != DType::F16)
+      bail("GGUF F16 decode warmup returned %s, expected F16", dtype_name(out.dtype()));
+    std::vector<float> z32((size_t)(9 * in_dim), 0.0f);
+    Tensor prefill = Tensor::from_host(z32.data(), DType::F32, {1, 9, in_dim}).to_device(device);
+    (void)mm.forward(prefill);
+    DeviceScope ds(device);
+    hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  } catch (...) {
+    g_gguf_warmed.fetch_and(~bit);
+    throw;
+  }
+  log_info(std::string("worker GGUF ROCm warmup complete: dtype=") + gguf::ggml_dtype_name(dtype) +
+           " decode=F16/direct seq=1 fallback=F32 seq=9");
+}
+}  // namespace
+
+void configure_worker_gguf_from_args(const std::optional<std::string> &path, bool fp16_prefill, bool output_head,
+                                     bool sample_token, bool worker_mode, Device device, DType dtype,
+                                     int64_t num_hidden_layers) {
+  g_gguf_fp16_prefill.store(false);
+  g_gguf_output_head.store(false);
+  g_gguf_sample_token.store(false);
+  {
+    std::unique_lock<std::shared_mutex> lk(g_gguf_mu);
+    g_gguf_source.reset();
+  }
+  if (!worker_mode) {
+    if (path || fp16_prefill || output_head || sample_token)
+      log_info("worker GGUF options ignored in master mode; master weights remain unchanged");
+    return;
+  }
+  if (!path) {
+    if (fp16_prefill || output_head || sample_token)
+      bail("--worker-gguf-fp16-prefill/--worker-gguf-output-head requires --worker-quantized-gguf");
+    return;
+  }
+  if (!device.is_rocm()) bail("--worker-quantized-gguf currently requires a ROCm worker");
+  if (dtype != DType::F16 && dtype != DType::BF16)
+    bail("--worker-quantized-gguf requires --dtype f16 or bf16 so DIAL activation and KV-cache contracts remain "
+         "unchanged");
+  if (sample_token && !output_head)
+    bail("--worker-gguf-sample-token true requires --worker-gguf-output-head true");
+
+  auto src = std::make_shared<WorkerGgufSource>();
+  src->path = *path;
+  src->device = device;
+  src->file.open(*path, std::ios::binary);
+  if (!src->file) bail("cannot open worker GGUF %s: %s", path->c_str(), std::strerror(errno));
+  try {
+    src->file.seekg(0, std::ios::end);
+    const uint64_t size = (uint64_t)src->file.tellg();
+    src->file.seekg(0);
+    src->content = gguf::Content::read(src->file, size);
+  } catch (const Error &e) {
+    bail("cannot parse worker GGUF %s: %s", path->c_str(), e.what());
+  }
+  const gguf::Value *arch = src->content.get("general.architecture");
+  if (!arch) bail("worker GGUF %s is missing general.architecture", path->c_str());
+  if (arch->type != gguf::ValueType::String || arch->s != "qwen3vl")
+    bail("worker GGUF %s has unsupported architecture metadata %s; expected qwen3vl", path->c_str(),
+         arch->debug().c_str());
+  if (const gguf::Value *bc = src->content.get("qwen3vl.block_count")) {
+    uint64_t block_count;
+    try {
+      block_count = bc->to_u64();
+    } catch (const Error &e) {
+      bail("invalid qwen3vl.block_count: %s", e.what());
+    }
+    if ((int64_t)block_count != num_hidden_layers)
+      bail("worker GGUF block count %llu does not match Hugging Face config %lld", (unsigned long long)block_count,
+           (long long)num_hidden_layers);
+  }
+  g_gguf_count.store(0);
+  g_gguf_bytes.store(0);
+  g_gguf_warmed.store(0);
+  g_gguf_prefill_count.store(0);
+  g_gguf_prefill_bytes.store(0);
+  {
+    std::unique_lock<std::shared_mutex> lk(g_gguf_mu);
+    g_gguf_source = src;
+  }
+  g_gguf_fp16_prefill.store(fp16_prefill);
+  g_gguf_output_head.store(output_head);
+  g_gguf_sample_token.store(sample_token);
+  log_info("worker GGUF enabled: file=" + *path + " format=Ollama/llama.cpp activations=" + dtype_name(dtype) +
+           " kv_cache=" + dtype_name(dtype));
+  if (fp16_prefill)
+    log_info("worker GGUF hybrid enabled: prefill=fused-FP16 decode=GGUF (both resident; routing by sequence length)");
+}
+
+bool worker_gguf_enabled() { return (bool)gguf_source(); }
 bool worker_gguf_fp16_prefill_enabled() { return g_gguf_fp16_prefill.load(); }
+bool worker_gguf_output_head_requested() { return g_gguf_output_head.load(); }
+bool worker_gguf_sample_token_requested() { return g_gguf_sample_token.load(); }
+
+std::optional<std::tuple<size_t, size_t, size_t, size_t>> worker_gguf_summary() {
+  if (!worker_gguf_enabled()) return std::nullopt;
+  return std::make_tuple(g_gguf_count.load(), g_gguf_bytes.load(), g_gguf_prefill_count.load(),
+                         g_gguf_prefill_bytes.load());
+}
+
+std::optional<TextLinear> load_worker_gguf_linear(std::optional<int64_t> layer_idx, const std::string &tensor_suffix,
+                                                  int64_t in_dim, int64_t out_dim) {
+  std::shared_ptr<WorkerGgufSource> src = gguf_source();
+  if (!src) return std::nullopt;
+  if (!layer_idx) bail("worker GGUF requires a numeric transformer layer name");
+  const std::string name = "blk." + std::to_string(*layer_idx) + "." + tensor_suffix + ".weight";
+  auto it = src->content.tensor_infos.find(name);
+  if (it == src->content.tensor_infos.end())
+    bail("worker GGUF %s has no tensor %s", src->path.c_str(), name.c_str());
+  const gguf::TensorInfo &info = it->second;
+  if (info.dims != std::vector<int64_t>{out_dim, in_dim}) {
+    std::string d = "[";
+    for (size_t i = 0; i < info.dims.size(); ++i) d += (i ? ", " : "") + std::to_string(info.dims[i]);
+    bail("worker GGUF tensor %s shape %s], expected [%lld, %lld]", name.c_str(), d.c_str(), (long long)out_dim,
+         (long long)in_dim);
+  }
+  GgufMatMul::Kind kind;
+  switch (info.ggml_dtype) {
+    case gguf::GgmlDType::Q8_0: kind = GgufMatMul::Q8_0; break;
+    case gguf::GgmlDType::Q4K: kind = GgufMatMul::Q4_K; break;
+    case gguf::GgmlDType::Q6K: kind = GgufMatMul::Q6_K; break;
+    default:
+      bail("worker GGUF tensor %s has dtype %s; the ROCm GGUF path takes Q8_0, Q4K and Q6K", name.c_str(),
+           gguf::ggml_dtype_name(info.ggml_dtype));
+  }
+  std::vector<uint8_t> raw;
+  {
+    std::lock_guard<std::mutex> lk(src->file_mu);
+    raw = src->content.tensor_bytes(src->file, name);
+  }
+  std::shared_ptr<GgufMatMul> mm = GgufMatMul::from_blocks(kind, raw, out_dim, in_dim, src->device);
+  warmup_worker_gguf(*mm, info.ggml_dtype, in_dim, src->device);
+  g_gguf_count.fetch_add(1);
+  g_gguf_bytes.fetch_add(raw.size());
+  log_info("loaded worker GGUF tensor " + name + " dtype=" + gguf::ggml_dtype_name(info.ggml_dtype));
+  return TextLinear::gguf(name, mm);
+}
 
 // worker_gguf_prefill_for_dims (worker_gguf.rs:399-406): dims [.., seq, hidden]
 bool worker_gguf_prefill_for_dims(const std::vector<int64_t> &dims) {
@@ -724,7 +894,7 @@ bool worker_gguf_prefill_for_dims(const std::vector<int64_t> &dims) {
 Tensor forward_worker_gguf(const GgufMatMul &matmul, const Tensor &x) { return matmul.forward(x); }
 
 Linear build_worker_gguf_fp16_prefill_linear(const std::string &name, const std::vector<TextLinear> &sources) {
-  if (sources.empty()) bail("%s: no source linears", name.c_str());
+  if (sources.empty()) bail("cannot build empty FP16 GGUF prefill projection");
   std::vector<Tensor> parts;
   int64_t rows = 0, in_dim = -1;
   for (const TextLinear &src : sources) {
@@ -744,6 +914,9 @@ Linear build_worker_gguf_fp16_prefill_linear(const std::string &name, const std:
            "hipMemcpy D2D");
     off += w.nbytes();
   }
+  g_gguf_prefill_count.fetch_add(1);
+  g_gguf_prefill_bytes.fetch_add(fused.nbytes());
+  log_info("built worker GGUF FP16 prefill projection " + name + " shape=" + fused.dims_debug());
   return Linear(fused);
 }
 

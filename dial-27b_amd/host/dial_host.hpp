@@ -9,7 +9,9 @@
 //   TextLinear, W8A16Linear (CudaW8A16Linear),
 //   configure_worker_w8a16_from_args              qwen3_vl/worker_w8a16.rs:15-140,302-386
 //   GgufMatMul (candle QMatMul), forward_worker_gguf,
-//   worker_gguf_prefill_for_dims                  qwen3_vl/worker_gguf.rs:399-406,574-611
+//   configure_worker_gguf_from_args,
+//   load_worker_gguf_linear,
+//   worker_gguf_prefill_for_dims                  qwen3_vl/worker_gguf.rs:65-197,388-522,574-611
 // (paths relative to dial-core/src/models).
 //
 // Differences, all MI355X-side:
@@ -30,6 +32,7 @@
 #include <optional>
 #include <stdexcept>
 #include <string>
+#include <tuple>
 #include <utility>
 #include <vector>
 
@@ -183,8 +186,9 @@ class W8A16Linear {
 // candle QMatMul stand-in for GGUF Q8_0 / Q4_K weights.
 class GgufMatMul {
  public:
-  enum Kind { Q8_0 = 2, Q4_K = 3 };
-  // Raw GGUF blocks (34 B per 32 / 144 B per 256 along each row), shape [out, in].
+  enum Kind { Q8_0 = 2, Q4_K = 3, Q6_K = 8 };  // dialq format ids
+  // Raw GGUF blocks (34 B per 32 / 144 B per 256 / 210 B per 256 along each
+  // row), shape [out, in].
   static std::shared_ptr<GgufMatMul> from_blocks(Kind kind, const std::vector<uint8_t> &blocks, int64_t out_dim,
                                                  int64_t in_dim, Device device);
   // QTensor::quantize of a dense [out, in] tensor (host or device).
@@ -220,11 +224,26 @@ class TextLinear {
 void configure_worker_w8a16_from_args(bool requested, bool worker_mode, Device device, DType dtype);
 bool worker_w8a16_enabled();
 std::optional<std::pair<size_t, size_t>> worker_w8a16_summary();
-// GGUF worker state: the GGUF file reader is not part of this build, so the
-// switch that configure_worker_gguf_from_args sets is exposed directly.
-void set_worker_gguf_enabled(bool enabled, bool fp16_prefill);
+// configure_worker_gguf_from_args (worker_gguf.rs:65-180): opens and parses
+// the GGUF file (host/gguf.hpp), checks general.architecture == "qwen3vl"
+// and qwen3vl.block_count against the model config, and keeps the source
+// for load_worker_gguf_linear.  Worker mode only; ROCm device, F16 or BF16
+// runtime.
+void configure_worker_gguf_from_args(const std::optional<std::string> &path, bool fp16_prefill, bool output_head,
+                                     bool sample_token, bool worker_mode, Device device, DType dtype,
+                                     int64_t num_hidden_layers);
 bool worker_gguf_enabled();
 bool worker_gguf_fp16_prefill_enabled();
+bool worker_gguf_output_head_requested();
+bool worker_gguf_sample_token_requested();
+// (GGUF linears, their raw bytes, FP16 prefill linears, their bytes)
+std::optional<std::tuple<size_t, size_t, size_t, size_t>> worker_gguf_summary();
+// load_worker_gguf_linear (worker_gguf.rs:462-522): tensor
+// blk.{layer}.{suffix}.weight, shape [out_dim, in_dim], uploaded and
+// repacked (Q8_0, Q4_K, Q6_K), warmed once per GGUF dtype.  nullopt when no
+// GGUF source is configured.
+std::optional<TextLinear> load_worker_gguf_linear(std::optional<int64_t> layer_idx, const std::string &tensor_suffix,
+                                                  int64_t in_dim, int64_t out_dim);
 bool worker_gguf_prefill_for_dims(const std::vector<int64_t> &dims);
 Tensor forward_worker_gguf(const GgufMatMul &matmul, const Tensor &x);
 // build_worker_gguf_fp16_prefill_linear (worker_gguf.rs:425-452): the F16

@@ -134,7 +134,7 @@ def test_w8a16_text_linear_matches_dense_for_decode_and_prefill(torch_dev):
     idx = np.arange(out_dim * in_dim, dtype=np.float32)
     w = (np.sin(idx * 0.037) * 0.25 + ((idx % 11) - 5.0) * 0.002).astype(np.float16).reshape(out_dim, in_dim)
     dense = H.Linear(_t(w).to_device(ROCM))
-    H.set_worker_gguf_enabled(False, False)
+    H.configure_worker_gguf_from_args(None, False, False, False, True, ROCM, H.DType.F16, 1)
     H.configure_worker_w8a16_from_args(True, True, ROCM, H.DType.F16)
     lin = H.TextLinear.from_dense("test.linear", dense)
     assert lin.is_w8a16()

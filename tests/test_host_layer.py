@@ -24,13 +24,9 @@ def test_quant_linear_mode_gate():
 
 
 def test_worker_w8a16_gate():
-    # worker_w8a16.rs:15-44: GGUF takes precedence; master mode, non-GPU
-    # devices and unsupported dtypes keep dense weights
-    H.set_worker_gguf_enabled(True, False)
-    H.configure_worker_w8a16_from_args(True, True, H.Device.rocm(0), H.DType.F16)
-    assert not H.worker_w8a16_enabled()
-    assert "GGUF takes precedence" in H.last_warning()
-    H.set_worker_gguf_enabled(False, False)
+    # worker_w8a16.rs:15-44: master mode, non-GPU devices and unsupported
+    # dtypes keep dense weights (GGUF precedence: test_gguf_reader.py)
+    H.configure_worker_gguf_from_args(None, False, False, False, True, H.Device.rocm(0), H.DType.F16, 1)
     H.configure_worker_w8a16_from_args(True, False, H.Device.rocm(0), H.DType.F16)
     assert not H.worker_w8a16_enabled()
     H.configure_worker_w8a16_from_args(True, True, H.Device.cpu(), H.DType.F16)
