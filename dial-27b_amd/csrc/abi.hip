@@ -113,6 +113,7 @@ const char *format_name(int fmt) {
     case DIALQ_FORMAT_W8A16: return "W8A16";
     case DIALQ_FORMAT_Q8_0: return "Q8_0";
     case DIALQ_FORMAT_Q4_K: return "Q4_K";
+    case DIALQ_FORMAT_Q6_K: return "Q6_K";
     case DIALQ_FORMAT_FP8_ROW: return "FP8";
     case DIALQ_FORMAT_FP8_BLOCK: return "FP8 block";
     case DIALQ_FORMAT_NVFP4: return "NVFP4";
@@ -145,6 +146,10 @@ void raw_sizes(const dialq_linear_desc &d, size_t &wbytes, size_t &sbytes, size_
       return;
     case DIALQ_FORMAT_Q4_K:
       wbytes = (size_t)(N * (K / 256) * 144);
+      sbytes = scount = 0;
+      return;
+    case DIALQ_FORMAT_Q6_K:
+      wbytes = (size_t)(N * (K / 256) * 210);
       sbytes = scount = 0;
       return;
     case DIALQ_FORMAT_FP8_ROW:
@@ -418,7 +423,7 @@ void *dialq_linear_quantize(const dialq_linear_desc *desc, const void *dense, in
   guarded(error, error_size, [&] {
     validate_desc(desc);
     const dialq_linear_desc &d = *desc;
-    if (d.format == DIALQ_FORMAT_FP8_ROW || d.format == DIALQ_FORMAT_NVFP4)
+    if (d.format == DIALQ_FORMAT_FP8_ROW || d.format == DIALQ_FORMAT_NVFP4 || d.format == DIALQ_FORMAT_Q6_K)
       fail("%s weights come pre-quantized from the checkpoint; use dialq_linear_create", format_name(d.format));
     if (!dense) fail("dense weight must not be NULL");
     size_t es = dtype_size(dense_dtype);
@@ -496,6 +501,7 @@ uint64_t dialq_linear_resident_bytes(const void *linear) {
     case DIALQ_FORMAT_W8A16: return N * K + N * (d.scale_dtype == DIALQ_BF16 ? 2 : 4);
     case DIALQ_FORMAT_Q8_0: return N * (K / 32) * 34;
     case DIALQ_FORMAT_Q4_K: return N * (K / 256) * 144;
+    case DIALQ_FORMAT_Q6_K: return N * (K / 256) * 210;
     case DIALQ_FORMAT_FP8_BLOCK: return N * K + 4 * ((N + 127) / 128) * ((K + 127) / 128);
     case DIALQ_FORMAT_MXFP4: return N * K / 2 + N * K / 32;
   }

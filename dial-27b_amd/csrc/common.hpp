@@ -23,10 +23,19 @@
 //     Q4_K            CHUNK 256, 32 B: bytes 8i..8i+7 = qs[32i + 8g + j]
 //                                       (i < 4): low nibbles are sub-block 2i,
 //                                       high nibbles sub-block 2i+1
+//     Q6_K            CHUNK 256, 48 B in three 1 KB planes (plane p holds
+//                                       bytes 16l..16l+15 for lane l):
+//                                       plane h < 2: bytes 8i+j = ql[64h + 32i
+//                                       + 8g + j] (i < 2); plane 2: bytes 8h+j
+//                                       = qh[32h + 8g + j].  Value k = 32t + 8g
+//                                       + j (t = 4h + qd) is the nibble qd >> 1
+//                                       of ql byte i = qd & 1 with bits 2qd of
+//                                       the qh byte on top
 //   Scales that vary along k live in an aux array in the same tile order
 //   (aux[(s * k_chunks + c) * AUX + ...]):
 //     Q8_0   AUX 64 : u32 per row r = {f16 d(block 0), f16 d(block 1)}
 //     Q4_K   AUX 256: 16 B per row = the block header {d, dmin, scales[12]}
+//     Q6_K   AUX 288: 16 B per row = the i8 scales[16]; then 2 B per row = d
 //     NVFP4  AUX 128: 8 E4M3 group scales per row (k/16)
 //     MXFP4  AUX 64 : 4 E8M0 block scales per row (k/32)
 //   Per-row scales (W8A16, FP8_ROW) are an f32 array of n_strips*16 values;
@@ -73,6 +82,8 @@ __host__ __device__ inline FormatGeom format_geom(int fmt) {
       return {128, 16, 1024, 64, 32};
     case DIALQ_FORMAT_Q4_K:
       return {256, 32, 2048, 256, 256};
+    case DIALQ_FORMAT_Q6_K:
+      return {256, 48, 3072, 288, 256};
     default:
       return {0, 0, 0, 0, 0};
   }

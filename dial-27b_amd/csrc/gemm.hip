@@ -39,8 +39,9 @@ struct GemmShape {
   static constexpr int KS = (CHUNK == 64 && FMT != DIALQ_FORMAT_Q8_0) ? 2 : 1;
   static constexpr int SK = KS * CHUNK;                // k per stage
   static constexpr int STRIDE = SK + 8;                // bf16 elements per LDS row
-  static constexpr int MS = (FMT == DIALQ_FORMAT_Q4_K) ? 2 : 8;  // 16-row groups per workgroup
-  static constexpr int NS = (FMT == DIALQ_FORMAT_Q4_K) ? 2 : 4;  // 16-col strips per wave
+  static constexpr bool KQ = FMT == DIALQ_FORMAT_Q4_K || FMT == DIALQ_FORMAT_Q6_K;
+  static constexpr int MS = KQ ? 2 : 8;  // 16-row groups per workgroup
+  static constexpr int NS = KQ ? 2 : 4;  // 16-col strips per wave
   static constexpr int ROWS = 16 * MS;
   static constexpr int BUF = PARTS * ROWS * STRIDE;   // bf16 elements per LDS buffer
   static constexpr int LDS_BYTES = 2 * BUF * 2;
@@ -55,13 +56,22 @@ __device__ __forceinline__ RawTile gemm_tile(const WeightView &w, rsrc_t rt, rsr
   typedef FmtTraits<FMT> T;
   const int r = lane & 15, g = lane >> 4;
   const uint32_t tidx = (uint32_t)s * (uint32_t)w.k_chunks + (uint32_t)c;
-  const uint32_t off = valid ? tidx * (64 * T::LANE) + lane * T::LANE : kOOB;
   RawTile t;
+  t.s0 = 0;
+  t.hdr = (u32x4){0, 0, 0, 0};
+  if constexpr (FMT == DIALQ_FORMAT_Q6_K) {  // three 1 KB planes, 16 B per lane each
+    const uint32_t off = valid ? tidx * 3072 + lane * 16 : kOOB;
+    t.a = bload16(rt, off);
+    t.b = bload16(rt, valid ? off + 1024 : kOOB);
+    t.hdr = bload16(rt, valid ? off + 2048 : kOOB);
+    t.sc = bload16(ra, valid ? tidx * 288 + r * 16 : kOOB);
+    t.s0 = bload2(ra, valid ? tidx * 288 + 256 + r * 2 : kOOB);
+    return t;
+  }
+  const uint32_t off = valid ? tidx * (64 * T::LANE) + lane * T::LANE : kOOB;
   t.a = bload16(rt, off);
   t.b = (u32x4){0, 0, 0, 0};
   if constexpr (T::LANE == 32) t.b = bload16(rt, valid ? off + 16 : kOOB);
-  t.s0 = 0;
-  t.hdr = (u32x4){0, 0, 0, 0};
   if constexpr (FMT == DIALQ_FORMAT_Q8_0) t.s0 = bload4(ra, valid ? tidx * 64 + r * 4 : kOOB);
   else if constexpr (FMT == DIALQ_FORMAT_Q4_K) t.hdr = bload16(ra, valid ? tidx * 256 + r * 16 : kOOB);
   else if constexpr (FMT == DIALQ_FORMAT_NVFP4) t.s0 = bload2(ra, valid ? tidx * 128 + r * 8 + 2 * g : kOOB);
@@ -142,6 +152,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
     ra = make_rsrc(w.aux, (uint32_t)(total * 64));
   else if constexpr (FMT == DIALQ_FORMAT_Q4_K)
     ra = make_rsrc(w.aux, (uint32_t)(total * 256));
+  else if constexpr (FMT == DIALQ_FORMAT_Q6_K)
+    ra = make_rsrc(w.aux, (uint32_t)(total * 288));
   else if constexpr (FMT == DIALQ_FORMAT_NVFP4)
     ra = make_rsrc(w.aux, (uint32_t)(total * 128));
   else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK)
@@ -487,6 +499,7 @@ hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t 
     case DIALQ_FORMAT_NVFP4: return gemm_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, st);
     case DIALQ_FORMAT_MXFP4: return gemm_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, st);
     case DIALQ_FORMAT_Q4_K: return gemm_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, st);
+    case DIALQ_FORMAT_Q6_K: return gemm_act<DIALQ_FORMAT_Q6_K>(w, x, x_dtype, M, y, y_dtype, st);
   }
   return hipErrorInvalidValue;
 }

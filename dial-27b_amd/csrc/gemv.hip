@@ -1,5 +1,5 @@
 // Decode GEMV for quantized weights, gfx950: up to 16 rows of x per pass
-// (8 for the Q4_K row-packed policy); larger M runs several passes.
+// (8 for the Q4_K / Q6_K row-packed policies); larger M runs several passes.
 //
 // Reference kernels replaced: dial_w8a16_decode_f16 (worker_w8a16.rs:146-184),
 // dial_nvfp4_decode_f16 / dial_fp8_decode_f16 (cuda_quant.rs:67-133) and
@@ -88,12 +88,21 @@ __device__ __forceinline__ void tile_fill(RawTile &t, const WeightView &w, const
   typedef FmtTraits<FMT> T;
   const int r = lane & 15, g = lane >> 4;
   const uint32_t tidx = (uint32_t)s * (uint32_t)w.k_chunks + (uint32_t)c;
+  t.s0 = 0;
+  t.hdr = (u32x4){0, 0, 0, 0};
+  if constexpr (FMT == DIALQ_FORMAT_Q6_K) {  // three 1 KB planes, 16 B per lane each
+    const uint32_t off = valid ? tidx * 3072 + lane * 16 : kOOB;
+    t.a = sload16(cx.rt, off);
+    t.b = sload16(cx.rt, valid ? off + 1024 : kOOB);
+    t.hdr = sload16(cx.rt, valid ? off + 2048 : kOOB);
+    t.sc = sload16(cx.ra, valid ? tidx * 288 + r * 16 : kOOB);
+    t.s0 = sload2(cx.ra, valid ? tidx * 288 + 256 + r * 2 : kOOB);
+    return;
+  }
   const uint32_t off = valid ? tidx * (64 * T::LANE) + lane * T::LANE : kOOB;
   t.a = sload16(cx.rt, off);
   t.b = (u32x4){0, 0, 0, 0};
   if constexpr (T::LANE == 32) t.b = sload16(cx.rt, valid ? off + 16 : kOOB);
-  t.s0 = 0;
-  t.hdr = (u32x4){0, 0, 0, 0};
   if constexpr (FMT == DIALQ_FORMAT_Q8_0) t.s0 = sload4(cx.ra, valid ? tidx * 64 + r * 4 : kOOB);
   else if constexpr (FMT == DIALQ_FORMAT_Q4_K) t.hdr = sload16(cx.ra, valid ? tidx * 256 + r * 16 : kOOB);
   else if constexpr (FMT == DIALQ_FORMAT_NVFP4) t.s0 = sload2(cx.ra, valid ? tidx * 128 + r * 8 + 2 * g : kOOB);
@@ -255,6 +264,97 @@ struct Q4kRowsPolicy {
   }
 };
 
+// Q6_K, M <= 4*RP: the row packing of the Q4_K policy with 16-value
+// sub-blocks.  A 32-k slice t spans sub-blocks 2t (lane groups g < 2) and
+// 2t + 1 (g >= 2), so A row rho = 4m' + jj feeds sub-block 4u + jj of
+// group u = t/2 from the lanes with g/2 == jj%2 in the slices with
+// t%2 == jj/2: each lane fetches four activation operands per row pass
+// (t = 2u + jj/2), and MFMAs 2u, 2u+1 leave D_{4u+jj}[m'][n] in rows
+// 4m' + jj of accumulator u.  Weights enter as bf16(128 + q); with X the
+// sub-block's activation sums (ones operand), y += d*sc*(D - 160 X).
+template <int ACT, int RP, bool XL>
+struct Q6kRowsPolicy {
+  static constexpr int XACT = ACT;
+  static constexpr int NV = RP;
+  struct Slot {
+    RawTile t;
+    int c;
+    XRing<ACT, 4 * RP, XL> x;  // [q][u]: slice 2u + jj/2 of row 4q + mq
+  };
+  struct Acc {
+    float v[RP];
+  };
+  static __device__ __forceinline__ void zero(Acc &a) {
+#pragma unroll
+    for (int q = 0; q < RP; ++q) a.v[q] = 0.0f;
+  }
+  static __device__ __forceinline__ int xk(int c, int u, int lane) {
+    return c * 256 + 32 * (2 * u + ((lane & 3) >> 1)) + 8 * (lane >> 4);
+  }
+  static __device__ __forceinline__ void fill(Slot &sl, const WeightView &w, const Ctx &cx, int s, int c, bool valid,
+                                              int lane) {
+    tile_fill<DIALQ_FORMAT_Q6_K>(sl.t, w, cx, s, c, valid, lane);
+    sl.c = c;
+    if constexpr (!XL) {
+      // lanes whose lane group never matches their row's sub-block feed zeros
+      const int mq = (lane & 15) >> 2;
+      const bool used = valid && ((lane >> 5) & 1) == (lane & 1);
+#pragma unroll
+      for (int q = 0; q < RP; ++q)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sl.x.v[4 * q + u] = x_fetch<ACT, false>(cx, 4 * q + mq, xk(c, u, lane), used);
+    }
+  }
+  static __device__ __forceinline__ void compute(const Slot &sl, Acc &acc, const Ctx &cx) {
+    const int lane = threadIdx.x & 63, jj = lane & 3, mq = (lane & 15) >> 2;
+    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const u32x4 z4 = {0, 0, 0, 0};
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool gmatch = ((lane >> 5) & 1) == (jj & 1);  // g/2 == jj%2
+    const float d = f16_bits_to_f32(sl.t.s0 & 0xffffu);
+    u32x4 wb[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) wb[t] = q6x8_to_bf16_off128(t < 4 ? sl.t.a : sl.t.b, sl.t.hdr, t);
+#pragma unroll
+    for (int q = 0; q < RP; ++q) {
+      f32x4 cq[4], cs[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        XOp<ACT> src;
+        if constexpr (XL) src = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, 4 * q + mq, xk(sl.c, u, lane), true));
+        else src = xraw_to_op<ACT>(sl.x.v[4 * q + u]);
+        cq[u] = zero;
+        cs[u] = zero;
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+          const bool on = gmatch && (v == (jj >> 1));
+          XOp<ACT> av;
+          av.hi = on ? src.hi : z4;
+          if constexpr (ActTraits<ACT>::PARTS == 2) av.lo = on ? src.lo : z4;
+          cq[u] = mfma_x<ACT>(av, wb[2 * u + v], cq[u]);
+          cs[u] = mfma_x<ACT>(av, ones, cs[u]);
+        }
+      }
+      // lane (g, r) holds rows 4g+i: m' = g, sub-block 4u + i = byte i of sc[u]
+      float sum = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sum = __builtin_fmaf(sbyte_f32(sl.t.sc[u], i), __builtin_fmaf(-160.0f, cs[u][i], cq[u][i]), sum);
+      acc.v[q] = __builtin_fmaf(d, sum, acc.v[q]);
+    }
+  }
+  static __device__ __forceinline__ void values(const Acc &a, float (&v)[NV], int (&mrow)[NV], int lane) {
+    const int g = lane >> 4;
+#pragma unroll
+    for (int q = 0; q < RP; ++q) {
+      v[q] = a.v[q];
+      mrow[q] = 4 * q + g;
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // The GEMV kernel.  Dynamic LDS: [staged x: mrows * pitch][32 zero bytes]
 // [part[j][wave][m][16]: the accumulator of wave `wave` for the j-th strip
@@ -317,6 +417,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
     cx.ra = make_rsrc(w.aux, (uint32_t)(total * 64));
   else if constexpr (FMT == DIALQ_FORMAT_Q4_K)
     cx.ra = make_rsrc(w.aux, (uint32_t)(total * 256));
+  else if constexpr (FMT == DIALQ_FORMAT_Q6_K)
+    cx.ra = make_rsrc(w.aux, (uint32_t)(total * 288));
   else if constexpr (FMT == DIALQ_FORMAT_NVFP4)
     cx.ra = make_rsrc(w.aux, (uint32_t)(total * 128));
   else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK)
@@ -693,6 +795,8 @@ __global__ __launch_bounds__(64 * (kDynWaves + 1)) void k_gemv_dyn(DynParams p) 
     cx.ra = make_rsrc(w.aux, (uint32_t)(total * 64));
   else if constexpr (FMT == DIALQ_FORMAT_Q4_K)
     cx.ra = make_rsrc(w.aux, (uint32_t)(total * 256));
+  else if constexpr (FMT == DIALQ_FORMAT_Q6_K)
+    cx.ra = make_rsrc(w.aux, (uint32_t)(total * 288));
   else if constexpr (FMT == DIALQ_FORMAT_NVFP4)
     cx.ra = make_rsrc(w.aux, (uint32_t)(total * 128));
   else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK)
@@ -901,14 +1005,17 @@ template <int FMT, int ACT, bool XL>
 using GenericPol = GenericPolicy<FMT, ACT, XL>;
 template <int RP, int ACT, bool XL>
 using Q4kRowsPol = Q4kRowsPolicy<ACT, RP, XL>;
+template <int RP, int ACT, bool XL>
+using Q6kRowsPol = Q6kRowsPolicy<ACT, RP, XL>;
 
 template <int FMT, int ACT>
 static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype,
                                 float *ws, size_t ws_bytes, int *cnt, hipStream_t st) {
   typedef FmtTraits<FMT> T;
   constexpr int XV = (ACT == DIALQ_F32) ? 8 : 4;  // VGPRs per 8-element activation operand
-  constexpr int TV = T::LANE / 4 + ((FMT == DIALQ_FORMAT_Q4_K) ? 4 : 1) + 1;  // tile + scales + chunk
-  const int rows_per_pass = (FMT == DIALQ_FORMAT_Q4_K && M <= 8) ? 8 : 16;
+  constexpr bool KQ = FMT == DIALQ_FORMAT_Q4_K || FMT == DIALQ_FORMAT_Q6_K;
+  constexpr int TV = T::LANE / 4 + (FMT == DIALQ_FORMAT_Q4_K ? 4 : FMT == DIALQ_FORMAT_Q6_K ? 5 : 1) + 1;  // tile + scales + chunk
+  const int rows_per_pass = (KQ && M <= 8) ? 8 : 16;
   for (int64_t mb = 0; mb < M; mb += rows_per_pass) {
     const int64_t rem = M - mb, mrows = rem < 16 ? rem : 16;
     DynParams p{w, x, y, M, mb, y_dtype, 1, 1, 1, 1, 0, ws, ws_bytes, cnt};
@@ -918,6 +1025,13 @@ static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, v
         e = launch_pol<FMT, ACT, Q4kRowsPol, 1, ring_depth(TV), ring_depth(TV + 2 * XV)>(p, mrows, st);
       else if (rem <= 8)
         e = launch_pol<FMT, ACT, Q4kRowsPol, 2, ring_depth(TV), ring_depth(TV + 4 * XV)>(p, mrows, st);
+      else
+        e = launch_pol<FMT, ACT, GenericPol, FMT, ring_depth(TV), ring_depth(TV + T::NX * XV)>(p, mrows, st);
+    } else if constexpr (FMT == DIALQ_FORMAT_Q6_K) {
+      if (rem <= 4)
+        e = launch_pol<FMT, ACT, Q6kRowsPol, 1, ring_depth(TV), ring_depth(TV + 4 * XV)>(p, mrows, st);
+      else if (rem <= 8)
+        e = launch_pol<FMT, ACT, Q6kRowsPol, 2, ring_depth(TV), ring_depth(TV + 8 * XV)>(p, mrows, st);
       else
         e = launch_pol<FMT, ACT, GenericPol, FMT, ring_depth(TV), ring_depth(TV + T::NX * XV)>(p, mrows, st);
     } else {
@@ -957,6 +1071,7 @@ hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t 
     case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
     case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
     case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    case DIALQ_FORMAT_Q6_K: return gemv_act<DIALQ_FORMAT_Q6_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
   }
   return hipErrorInvalidValue;
 }

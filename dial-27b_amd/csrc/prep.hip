@@ -287,10 +287,24 @@ struct RepackGeom {
   int chunk, lane_bytes, tile_bytes, aux_bytes;
 };
 
+// Q6_K tile byte b of (strip s, chunk c): plane b / 1024, lane (b / 16) % 64,
+// byte j = b % 16 -> the ql (planes 0, 1) or qh (plane 2) byte of its
+// super-block (layout in common.hpp).
+__device__ __forceinline__ int64_t raw_index_q6k_tile(const RepackGeom &g, int64_t s, int64_t c, int b) {
+  const int plane = b >> 10, lane = (b >> 4) & 63, j = b & 15;
+  const int r = lane & 15, kg = lane >> 4;
+  const int64_t n = s * 16 + r;
+  if (n >= g.N || c >= g.K / 256) return -1;
+  const int64_t blk = (n * (g.K / 256) + c) * 210;
+  const int within = 32 * (j >> 3) + 8 * kg + (j & 7);
+  return plane < 2 ? blk + 64 * plane + within : blk + 128 + within;
+}
+
 __device__ __forceinline__ int64_t raw_index_tile(const RepackGeom &g, int64_t i) {
   int64_t t = i / g.tile_bytes;
   int b = (int)(i % g.tile_bytes);
   int64_t s = t / g.k_chunks, c = t % g.k_chunks;
+  if (g.fmt == DIALQ_FORMAT_Q6_K) return raw_index_q6k_tile(g, s, c, b);
   int lane = b / g.lane_bytes, j = b % g.lane_bytes;
   int r = lane & 15, kg = lane >> 4;
   int64_t n = s * 16 + r;
@@ -338,6 +352,11 @@ __device__ __forceinline__ int64_t raw_index_aux(const RepackGeom &g, int64_t i)
       int64_t n = s * 16 + b / 16;
       if (n >= g.N || c >= g.K / 256) return -1;
       return (n * (g.K / 256) + c) * 144 + (b % 16);
+    }
+    case DIALQ_FORMAT_Q6_K: {  // scales[16] per row, then d per row
+      int64_t n = s * 16 + (b < 256 ? b / 16 : (b - 256) / 2);
+      if (n >= g.N || c >= g.K / 256) return -1;
+      return (n * (g.K / 256) + c) * 210 + (b < 256 ? 192 + b % 16 : 208 + (b - 256) % 2);
     }
     case DIALQ_FORMAT_NVFP4: {
       int64_t n = s * 16 + b / 8;
@@ -479,6 +498,18 @@ __global__ void k_dequant(DequantArgs a) {
         v = d1 * (float)q - m1;
         break;
       }
+      case DIALQ_FORMAT_Q6_K: {
+        const int t6 = kk / 32, kg = (kk % 32) / 8, j = kk % 8;
+        const int h = t6 >> 2, qd = t6 & 3;
+        const uint8_t lb = tile[h * 1024 + (kg * 16 + r) * 16 + 8 * (qd & 1) + j];
+        const uint8_t hb = tile[2048 + (kg * 16 + r) * 16 + 8 * h + j];
+        const int q = (int)(((lb >> (4 * (qd >> 1))) & 15u) | (((hb >> (2 * qd)) & 3u) << 4));
+        const uint8_t *aux = a.aux + (s * a.k_chunks + c) * 288;
+        const float d = f16_bits_to_f32((uint32_t)aux[256 + 2 * r] | ((uint32_t)aux[257 + 2 * r] << 8));
+        const float sc = (float)(int8_t)aux[r * 16 + kk / 16];
+        v = d * sc * (float)(q - 32);  // exact: 11 + 8 + 6 significant bits
+        break;
+      }
     }
     store_out(a.out, i, a.out_dtype, v);
   }
@@ -553,8 +584,8 @@ hipError_t launch_repack(int fmt, int64_t N, int64_t K, const void *raw_w, const
                                                          sanitize);
   if (g.aux_bytes > 0) {
     int64_t a_total = strips * g.k_chunks * g.aux_bytes;
-    // Q8_0 / Q4_K scales live inside the raw blocks; NVFP4 / MXFP4 in `raw_s`.
-    const uint8_t *src = (fmt == DIALQ_FORMAT_Q8_0 || fmt == DIALQ_FORMAT_Q4_K)
+    // Q8_0 / Q4_K / Q6_K scales live inside the raw blocks; NVFP4 / MXFP4 in `raw_s`.
+    const uint8_t *src = (fmt == DIALQ_FORMAT_Q8_0 || fmt == DIALQ_FORMAT_Q4_K || fmt == DIALQ_FORMAT_Q6_K)
                              ? (const uint8_t *)raw_w
                              : (const uint8_t *)raw_s;
     k_repack_aux<<<grid_for(a_total, 256), 256, 0, st>>>(g, src, aux, a_total,
@@ -580,8 +611,9 @@ hipError_t launch_unpack(int fmt, int64_t N, int64_t K, const uint8_t *tiles, co
   k_unpack_tiles<<<grid_for(t_total, 256), 256, 0, st>>>(g, tiles, (uint8_t *)raw_w, t_total);
   if (g.aux_bytes > 0) {
     int64_t a_total = strips * g.k_chunks * g.aux_bytes;
-    uint8_t *dst = (fmt == DIALQ_FORMAT_Q8_0 || fmt == DIALQ_FORMAT_Q4_K) ? (uint8_t *)raw_w
-                                                                           : (uint8_t *)raw_s;
+    uint8_t *dst = (fmt == DIALQ_FORMAT_Q8_0 || fmt == DIALQ_FORMAT_Q4_K || fmt == DIALQ_FORMAT_Q6_K)
+                       ? (uint8_t *)raw_w
+                       : (uint8_t *)raw_s;
     k_unpack_aux<<<grid_for(a_total, 256), 256, 0, st>>>(g, aux, dst, a_total);
   }
   return hipGetLastError();

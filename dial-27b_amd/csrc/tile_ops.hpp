@@ -9,10 +9,10 @@
 // C[m = 4(l/16)+i][n = l%16].
 //
 // Exactness: every weight code is converted to an exact bf16 value (int8,
-// E4M3, E2M1 times an E4M3 or E8M0 scale, Q4_K nibbles offset by 128), so
+// E4M3, E2M1 times an E4M3 or E8M0 scale, Q4_K / Q6_K codes offset by 128), so
 // the products are exact and only the fp32 accumulation order differs from
 // the oracle.  Scales that cannot be folded exactly into a bf16 operand
-// (Q8_0's f16 d, Q4_K's d*sc and dmin*m, FP8_BLOCK's f32 block scale) are
+// (Q8_0's f16 d, Q4_K's d*sc and dmin*m, Q6_K's d*sc, FP8_BLOCK's f32 block scale) are
 // applied to the f32 partial product of their own k block.
 #pragma once
 
@@ -264,6 +264,31 @@ __device__ __forceinline__ u32x4 nib8_to_bf16_off128(uint32_t d0, uint32_t d1, i
   return r;
 }
 
+// Q6_K slice t of a lane (8 values k = 32t + 8g + j): 6-bit codes q from the
+// ql plane of half t/4 (bytes 8(qd&1).., nibble qd>>1) and the qh plane
+// (bytes 8h.., bits 2qd), qd = t%4, as bf16 (128 + q).
+__device__ __forceinline__ u32x4 q6x8_to_bf16_off128(const u32x4 &ql, const u32x4 &qh, int t) {
+  const int h = t >> 2, qd = t & 3, i = qd & 1;
+  const int ns = 4 * (qd >> 1), hs = 2 * qd;
+  uint32_t q[2];
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const uint32_t hb = hs <= 4 ? (qh[2 * h + w] << (4 - hs)) : (qh[2 * h + w] >> (hs - 4));
+    q[w] = ((ql[2 * i + w] >> ns) & 0x0f0f0f0fu) | (hb & 0x30303030u);
+  }
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(0x43434343u, q[0], 0x04010400u);
+  r[1] = __builtin_amdgcn_perm(0x43434343u, q[0], 0x04030402u);
+  r[2] = __builtin_amdgcn_perm(0x43434343u, q[1], 0x04010400u);
+  r[3] = __builtin_amdgcn_perm(0x43434343u, q[1], 0x04030402u);
+  return r;
+}
+
+// Signed byte i of a dword as f32.
+__device__ __forceinline__ float sbyte_f32(uint32_t d, int i) {
+  return (float)((int32_t)(d << (24 - 8 * i)) >> 24);
+}
+
 // ---- format traits -----------------------------------------------------------
 // CHUNK: k per tile; LANE: bytes per lane; NX: MFMA k-slices per tile;
 // xk(t, g): k offset (within the chunk) of slice t for lane group g.
@@ -304,25 +329,20 @@ struct FmtTraits<DIALQ_FORMAT_Q4_K> {
   static constexpr int CHUNK = 256, LANE = 32, NX = 8;
   __device__ static int xk(int t, int g) { return 32 * t + 8 * g; }
 };
+template <>
+struct FmtTraits<DIALQ_FORMAT_Q6_K> {  // LANE: 16 B in each of three 1 KB planes
+  static constexpr int CHUNK = 256, LANE = 48, NX = 8;
+  __device__ static int xk(int t, int g) { return 32 * t + 8 * g; }
+};
 
 struct RawTile {
   u32x4 a;
   u32x4 b;       // second 16 bytes (LANE == 32 formats)
   uint32_t s0;   // per-lane scale bits: Q8_0 d pair, NVFP4 E4M3 pair,
                  // MXFP4 E8M0, FP8_BLOCK f32 block scale
-  u32x4 hdr;     // Q4_K super-block header {d, dmin, scales[12]}
+  u32x4 hdr;     // Q4_K super-block header {d, dmin, scales[12]}; Q6_K qh plane
+  u32x4 sc;      // Q6_K i8 scales[16] of the lane's row (d in s0)
 };
-
-template <int LANE>
-__device__ __forceinline__ RawTile load_tile_at(const uint8_t *p) {
-  RawTile r;
-  r.a = __builtin_nontemporal_load((const u32x4 *)p);
-  if constexpr (LANE == 32)
-    r.b = __builtin_nontemporal_load((const u32x4 *)(p + 16));
-  else
-    r.b = (u32x4){0, 0, 0, 0};
-  return r;
-}
 
 template <int FMT>
 __device__ __forceinline__ RawTile load_tile(const uint8_t *tiles, int64_t tile_idx, int lane) {
@@ -337,41 +357,16 @@ __device__ __forceinline__ RawTile load_tile(const uint8_t *tiles, int64_t tile_
   return r;
 }
 
-// All global loads of one tile for one lane (weights and the k-varying
-// scales of the lane's row), issued unconditionally so the compiler can
-// count outstanding loads statically; callers pass a valid (clamped) chunk.
-template <int FMT>
-__device__ __forceinline__ RawTile load_tile_full(const WeightView &w, const uint8_t *tbase, int s,
-                                                  int c, int lane) {
-  constexpr int LANE = FmtTraits<FMT>::LANE;
-  const int r = lane & 15, g = lane >> 4;
-  const uint32_t tidx = (uint32_t)s * (uint32_t)w.k_chunks + (uint32_t)c;
-  RawTile t = load_tile_at<LANE>(tbase + (uint32_t)c * (64 * LANE));
-  t.s0 = 0;
-  t.hdr = (u32x4){0, 0, 0, 0};
-  if constexpr (FMT == DIALQ_FORMAT_Q8_0) {
-    t.s0 = *(const uint32_t *)(w.aux + tidx * 64 + r * 4);
-  } else if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
-    t.hdr = *(const u32x4 *)(w.aux + tidx * 256 + r * 16);
-  } else if constexpr (FMT == DIALQ_FORMAT_NVFP4) {
-    t.s0 = *(const uint16_t *)(w.aux + tidx * 128 + r * 8 + 2 * g);
-  } else if constexpr (FMT == DIALQ_FORMAT_MXFP4) {
-    t.s0 = w.aux[tidx * 64 + r * 4 + g];
-  } else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK) {
-    t.s0 = __float_as_uint(w.block_scale[(uint32_t)((s * 16) / 128) * (uint32_t)w.nbk + (uint32_t)c]);
-  }
-  return t;
-}
-
 // B operands of one tile plus the lane row's scale factors.
 template <int FMT>
 struct BOps {
   u32x4 b[FmtTraits<FMT>::NX];
-  float s1[FmtTraits<FMT>::NX];  // Q8_0: d per block; Q4_K: d*sc; FP8_BLOCK: s
-  float s2[FmtTraits<FMT>::NX];  // Q4_K: 128*d*sc + dmin*m
+  float s1[FmtTraits<FMT>::NX];  // Q8_0: d per block; Q4_K: d*sc; FP8_BLOCK: s;
+                                 // Q6_K: d*sc of the slice's upper sub-block
+  float s2[FmtTraits<FMT>::NX];  // Q4_K: 128*d*sc + dmin*m; Q6_K: d*(sc_lo - sc_hi)
 };
 
-// `t` must come from load_tile_full (scales included).
+// `t` must carry the lane row's scales (gemv tile_fill / gemm gemm_tile).
 template <int FMT>
 __device__ __forceinline__ BOps<FMT> make_bops(const RawTile &t) {
   BOps<FMT> o;
@@ -427,6 +422,16 @@ __device__ __forceinline__ BOps<FMT> make_bops(const RawTile &t) {
       const int i4 = j >> 1;
       o.b[j] = nib8_to_bf16_off128(qd[2 * i4], qd[2 * i4 + 1], (j & 1) ? 4 : 0);
     }
+  } else if constexpr (FMT == DIALQ_FORMAT_Q6_K) {
+    const float d = f16_bits_to_f32(t.s0 & 0xffffu);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      o.b[j] = q6x8_to_bf16_off128(j < 4 ? t.a : t.b, t.hdr, j);
+      // sub-blocks 2j (lanes g < 2) and 2j + 1 (g >= 2): bytes 2j, 2j+1
+      const float lo = sbyte_f32(t.sc[j >> 1], 2 * (j & 1)), hi = sbyte_f32(t.sc[j >> 1], 2 * (j & 1) + 1);
+      o.s1[j] = d * hi;
+      o.s2[j] = d * (lo - hi);
+    }
   }
   return o;
 }
@@ -460,6 +465,27 @@ __device__ __forceinline__ void bops_mac(const BOps<FMT> &o, const XOp<ACT> *xo,
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         acc[i] = __builtin_fmaf(o.s1[j], pq[i], __builtin_fmaf(-o.s2[j], px[i], acc[i]));
+    }
+  } else if constexpr (FMT == DIALQ_FORMAT_Q6_K) {
+    // A 32-k slice spans two 16-value sub-blocks with their own scales:
+    // lanes g < 2 hold the lower one.  With P = x.(128 + q) and C = sum(x),
+    // over the whole slice (a) and over the lower sub-block only (l):
+    // y += s_hi*(Pa - 160 Ca) + (s_lo - s_hi)*(Pl - 160 Cl).
+    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const u32x4 z4 = {0, 0, 0, 0};
+    const bool lower = (threadIdx.x & 32) == 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      XOp<ACT> xl;
+      xl.hi = lower ? xo[j].hi : z4;
+      if constexpr (ActTraits<ACT>::PARTS == 2) xl.lo = lower ? xo[j].lo : z4;
+      const f32x4 pa = mfma_x<ACT>(xo[j], o.b[j], zero), ca = mfma_x<ACT>(xo[j], ones, zero);
+      const f32x4 pl = mfma_x<ACT>(xl, o.b[j], zero), cl = mfma_x<ACT>(xl, ones, zero);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ua = __builtin_fmaf(-160.0f, ca[i], pa[i]), ul = __builtin_fmaf(-160.0f, cl[i], pl[i]);
+        acc[i] = __builtin_fmaf(o.s1[j], ua, __builtin_fmaf(o.s2[j], ul, acc[i]));
+      }
     }
   }
 }

@@ -21,9 +21,9 @@ LIB_PATH = os.path.join(PKG_ROOT, "lib", "libdialq.so")
 HEADER_PATH = os.path.join(PKG_ROOT, "..", "include", "dialq.h")
 
 # enum dialq_format
-W8A16, Q8_0, Q4_K, FP8_ROW, FP8_BLOCK, NVFP4, MXFP4 = 1, 2, 3, 4, 5, 6, 7
+W8A16, Q8_0, Q4_K, FP8_ROW, FP8_BLOCK, NVFP4, MXFP4, Q6_K = 1, 2, 3, 4, 5, 6, 7, 8
 FORMAT_NAMES = {W8A16: "w8a16", Q8_0: "q8_0", Q4_K: "q4_k", FP8_ROW: "fp8_row",
-                FP8_BLOCK: "fp8_block", NVFP4: "nvfp4", MXFP4: "mxfp4"}
+                FP8_BLOCK: "fp8_block", NVFP4: "nvfp4", MXFP4: "mxfp4", Q6_K: "q6_k"}
 # enum dialq_dtype
 F32, F16, BF16 = 0, 1, 2
 # flags
@@ -257,6 +257,8 @@ class Linear:
             w, s = np.empty((n, k // 32 * 34), np.uint8), None
         elif fmt == Q4_K:
             w, s = np.empty((n, k // 256 * 144), np.uint8), None
+        elif fmt == Q6_K:
+            w, s = np.empty((n, k // 256 * 210), np.uint8), None
         elif fmt == FP8_ROW:
             w, s = np.empty((n, k), np.uint8), np.empty(n, np.float32)
         elif fmt == FP8_BLOCK:
@@ -280,6 +282,8 @@ def raw_weight_bytes(fmt, n, k) -> int:
         return n * (k // 32) * 34
     if fmt == Q4_K:
         return n * (k // 256) * 144
+    if fmt == Q6_K:
+        return n * (k // 256) * 210
     if fmt == FP8_ROW:
         return n * k + 4 * n
     if fmt == FP8_BLOCK:

@@ -49,7 +49,11 @@ enum dialq_format {
    * global (cuda_quant.rs:43-56, quant.rs:160-208) */
   DIALQ_FORMAT_NVFP4 = 6,
   /* MXFP4 (OCP MX v1.0): E2M1 [N, K/2] + E8M0 scale per 32 along K */
-  DIALQ_FORMAT_MXFP4 = 7
+  DIALQ_FORMAT_MXFP4 = 7,
+  /* GGUF Q6_K: [N, K/256] super-blocks {u8 ql[128]; u8 qh[64]; i8 scales[16];
+   * f16 d} (210 B), w = d * scales[k/16] * (q6 - 32); the second type of a
+   * Q4_K_M file (worker_gguf.rs:536-540, docs/worker_gguf.md:3-5) */
+  DIALQ_FORMAT_Q6_K = 8
 };
 
 enum dialq_dtype { DIALQ_F32 = 0, DIALQ_F16 = 1, DIALQ_BF16 = 2 };
@@ -93,7 +97,7 @@ uint32_t dialq_abi_version(void);
  *   scales / scale_bytes:  W8A16: N f32|bf16; FP8_ROW: N or 1 f32;
  *                          FP8_BLOCK: ceil(N/128)*ceil(K/128) f32;
  *                          NVFP4: N*K/16 E4M3 bytes; MXFP4: N*K/32 E8M0 bytes;
- *                          Q8_0 / Q4_K: NULL, 0 (scales live in the blocks)
+ *                          Q8_0 / Q4_K / Q6_K: NULL, 0 (scales live in the blocks)
  *   host_io: 1 = weight/scales are host pointers, 0 = device pointers
  *   stream:  hipStream_t (NULL = default stream); the call synchronizes it
  * Returns an owned handle, or NULL with a message in `error`. */

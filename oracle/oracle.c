@@ -403,6 +403,35 @@ void or_q4_k_dequant(const uint8_t *blocks, int64_t n, int64_t k, float *out) {
     }
 }
 
+void or_q6_k_dequant(const uint8_t *blocks, int64_t n, int64_t k, float *out) {
+  int64_t nb = k / 256;
+  for (int64_t r = 0; r < n; ++r)
+    for (int64_t b = 0; b < nb; ++b) {
+      const uint8_t *blk = blocks + (r * nb + b) * 210;
+      const uint8_t *ql = blk, *qh = blk + 128;
+      const int8_t *sc = (const int8_t *)(blk + 192);
+      const float d = or_f16_to_f32(get_u16(blk + 208));
+      float *y = out + r * k + b * 256;
+      for (int h = 0; h < 2; ++h) {
+        for (int l = 0; l < 32; ++l) {
+          const int is = l / 16;
+          const int q1 = (int)((ql[l] & 0xf) | (((qh[l] >> 0) & 3) << 4)) - 32;
+          const int q2 = (int)((ql[l + 32] & 0xf) | (((qh[l] >> 2) & 3) << 4)) - 32;
+          const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+          const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+          y[l] = d * (float)sc[is] * (float)q1;
+          y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+          y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+          y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+        }
+        y += 128;
+        ql += 64;
+        qh += 32;
+        sc += 8;
+      }
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* FP8                                                                 */
 /* ------------------------------------------------------------------ */

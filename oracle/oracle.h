@@ -90,6 +90,21 @@ void or_q4_k_quantize(const float *w, int64_t n, int64_t k, uint8_t *blocks);
 void or_q4_k_dequant(const uint8_t *blocks, int64_t n, int64_t k, float *out);
 void or_q4_k_scale_min(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m);
 
+/* ---- GGUF Q6_K: 210-byte super-blocks {u8 ql[128]; u8 qh[64];
+ * i8 scales[16]; f16 d} ------------------------------------------------
+ * The second block type of a Q4_K_M file (qwen3_vl/worker_gguf.rs:536-540,
+ * docs/worker_gguf.md:3-5).  Dequant restates the GGUF Q6_K block format
+ * (ggml's dequantize_row_q6_K, which candle-core 0.11 BlockQ6K::to_float
+ * reproduces; neither is in the reference tree): per 128-value half h and
+ * l < 32, value 32*qd + l of the half is the 4-bit field qd>>1 of
+ * ql[64h + l + 32*(qd&1)] with bits 2qd..2qd+1 of qh[32h + l] on top,
+ * q - 32, times d * scales[8h + 2qd + l/16].  Products are exact in f32
+ * (11 + 8 + 6 significant bits).  Pinned against an element-wise encoder
+ * written from the same layout description (tests/test_oracle_formats.py)
+ * and invariants (zero d, constant codes); parity with candle's own
+ * element order is unpinned (no Q6_K fixture exists in the reference). */
+void or_q6_k_dequant(const uint8_t *blocks, int64_t n, int64_t k, float *out);
+
 /* ---- FP8 E4M3 ---------------------------------------------------------
  * Reference layout (cuda_quant.rs:58-65): u8[n,k] with one f32 scale per
  * row (a per-tensor scale is broadcast, quant.rs:418-425).

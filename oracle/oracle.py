@@ -58,6 +58,7 @@ def _declare(L):
         "or_q8_0_dequant": (None, [_P, _I64, _I64, _P]),
         "or_q4_k_quantize": (None, [_P, _I64, _I64, _P]),
         "or_q4_k_dequant": (None, [_P, _I64, _I64, _P]),
+        "or_q6_k_dequant": (None, [_P, _I64, _I64, _P]),
         "or_fp8_row_dequant": (None, [_P, _P, _I64, _I64, _P]),
         "or_fp8_block_quantize": (None, [_P, _I64, _I64, _P, _P]),
         "or_fp8_block_dequant": (None, [_P, _P, _I64, _I64, _P]),
@@ -182,6 +183,25 @@ def q4_k_dequant(blocks, n, k):
     out = np.empty((n, k), np.float32)
     lib().or_q4_k_dequant(_p(blocks), n, k, _p(out))
     return out
+
+
+def q6_k_dequant(blocks, n, k):
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    out = np.empty((n, k), np.float32)
+    lib().or_q6_k_dequant(_p(blocks), n, k, _p(out))
+    return out
+
+
+def q6_k_random_blocks(n, k, seed=0, d_scale=2e-4):
+    """Seeded Q6_K blocks for tests: uniform 6-bit codes and i8 scales, d =
+    f16(d_scale * u) with u in [0.5, 1.5) (GGUF Q6_K quantization is not part
+    of the path: Q6_K weights come from files)."""
+    rng = np.random.default_rng(seed)
+    nb = n * (k // 256)
+    b = rng.integers(0, 256, (nb, 210), dtype=np.uint8)
+    d = (d_scale * rng.uniform(0.5, 1.5, nb)).astype(np.float16)
+    b[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    return b.reshape(n, (k // 256) * 210)
 
 
 def fp8_row_dequant(q, scale):

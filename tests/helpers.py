@@ -27,6 +27,9 @@ def make_weight(fmt, n, k, seed=0, scale_dtype=dq.BF16):
     if fmt == dq.Q4_K:
         b = O.q4_k_quantize(w)
         return b, None, kw, O.q4_k_dequant(b, n, k)
+    if fmt == dq.Q6_K:
+        b = O.q6_k_random_blocks(n, k, seed)
+        return b, None, kw, O.q6_k_dequant(b, n, k)
     if fmt == dq.FP8_BLOCK:
         q, s = O.fp8_block_quantize(w)
         return q, s, kw, O.fp8_block_dequant(q, s)
@@ -53,7 +56,7 @@ def make_weight(fmt, n, k, seed=0, scale_dtype=dq.BF16):
 
 
 def k_align(fmt):
-    return {dq.Q4_K: 256, dq.Q8_0: 32, dq.MXFP4: 32, dq.NVFP4: 16}.get(fmt, 8)
+    return {dq.Q4_K: 256, dq.Q6_K: 256, dq.Q8_0: 32, dq.MXFP4: 32, dq.NVFP4: 16}.get(fmt, 8)
 
 
 def reference_product(x_f32, deq, y_dtype):

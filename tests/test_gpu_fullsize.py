@@ -96,3 +96,24 @@ def test_27b_layer_sweep(fmt, shape, torch_dev):
 def test_27b_lowp_decode_and_prefill(fmt, shape, torch_dev):
     _check(fmt, shape[0], shape[1], 1, torch_dev)
     _check(fmt, shape[0], shape[1], 1024, torch_dev, tol=2e-3, native=True)
+
+
+@pytest.mark.parametrize("shape", SHAPES_8B_GGUF + [(5120, 17408), (1024, 5120)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_q6_k_full_size(shape, torch_dev):
+    # Q6_K comes from GGUF files only (no quantizer on the path): seeded
+    # random blocks, created through the C ABI's repacker
+    import torch
+    n, k = shape
+    blocks = O.q6_k_random_blocks(n, k, seed=n + k)
+    lin = dq.Linear.create(dq.Q6_K, n, k, blocks, None)
+    rng = np.random.default_rng(n)
+    rows = np.sort(rng.choice(n, SAMPLE, replace=False))
+    deq = O.q6_k_dequant(blocks[rows], SAMPLE, k)
+    for m in (1, 4, 8, 256):
+        x = O.round_bf16(rng.normal(0, 1, (m, k)).astype(np.float32))
+        yt = torch.empty(m, n, dtype=torch.bfloat16, device=torch_dev)
+        lin.forward(to_torch(x, dq.BF16, torch_dev), yt)
+        torch.cuda.synchronize()
+        got = yt[:, torch.from_numpy(rows).to(torch_dev)].float().cpu().numpy()
+        ref = O.round_bf16((x.astype(np.float64) @ deq.astype(np.float64).T).astype(np.float32))
+        assert O.rel_l2(got, ref) <= 1e-3, (n, k, m)

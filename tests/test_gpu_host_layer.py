@@ -189,3 +189,45 @@ def test_hybrid_linear_keeps_q4k_for_single_token_decode(torch_dev):
     # several tokens take the dense FP16 copy
     x3 = _t(((np.arange(768) % 29 - 14.0) / 15.0).astype(np.float16).reshape(1, 3, 256)).to_device(ROCM)
     assert np.array_equal(hybrid.forward(x3).numpy().view(np.uint16), fp16.forward(x3).numpy().view(np.uint16))
+
+
+def test_worker_gguf_file_linears_load_and_match_oracle(tmp_path, torch_dev):
+    # worker_gguf.rs:65-180 (configure), 462-522 (load_worker_gguf_linear),
+    # 524-572 (warm-up per GGUF dtype), 388-397 (summary), 425-452 (FP16
+    # prefill copy): a Q4_K_M-style file mixing Q4K, Q6K and Q8_0 linears
+    import oracle as O
+    from gguf_writer import write_gguf
+    rng = np.random.default_rng(5)
+    h, i = 256, 512
+    gate = O.q4_k_quantize(rng.normal(0, 0.02, (i, h)).astype(np.float32))
+    up = O.q6_k_random_blocks(i, h, seed=7)
+    down = O.q8_0_quantize(rng.normal(0, 0.02, (h, i)).astype(np.float32))
+    deq = {"ffn_gate": O.q4_k_dequant(gate, i, h), "ffn_up": O.q6_k_dequant(up, i, h),
+           "ffn_down": O.q8_0_dequant(down, h, i)}
+    path = tmp_path / "tiny-q4_k_m.gguf"
+    write_gguf(str(path), [("general.architecture", "STRING", "qwen3vl"), ("qwen3vl.block_count", "U32", 1)],
+               [("blk.0.ffn_gate.weight", "Q4K", [i, h], gate.tobytes()),
+                ("blk.0.ffn_up.weight", "Q6K", [i, h], up.tobytes()),
+                ("blk.0.ffn_down.weight", "Q8_0", [h, i], down.tobytes())])
+    try:
+        H.configure_worker_gguf_from_args(str(path), True, False, False, True, ROCM, H.DType.F16, 1)
+        lins = {name: H.load_worker_gguf_linear(0, name, *dims)
+                for name, dims in (("ffn_gate", (h, i)), ("ffn_up", (h, i)), ("ffn_down", (i, h)))}
+        assert all(l.is_gguf() for l in lins.values())
+        assert H.worker_gguf_summary() == (3, gate.nbytes + up.nbytes + down.nbytes, 0, 0)
+        for name, lin in lins.items():
+            k = deq[name].shape[1]
+            for rows in (1, 7):
+                x = O.round_f16(rng.normal(0, 1, (rows, k)).astype(np.float32))
+                out = lin.forward(_t(x.astype(np.float16).reshape(1, rows, k)).to_device(ROCM))
+                assert out.dtype == H.DType.F16 and out.dims == [1, rows, deq[name].shape[0]]
+                ref = O.round_f16(O.matmul_f64(x, deq[name]).astype(np.float32))
+                assert O.rel_l2(out.numpy().astype(np.float32).reshape(rows, -1), ref) <= 1e-3, (name, rows)
+            # the F16 prefill copy is the dequantized weight, rounded once
+            w16 = lin.gguf_dequantize_f16_weight().numpy()
+            assert np.array_equal(w16, O.round_f16(deq[name]).astype(np.float16))
+        fused = H.build_worker_gguf_fp16_prefill_linear("blk.0.gate_up", [lins["ffn_gate"], lins["ffn_up"]])
+        assert fused.weight().dims == [2 * i, h]
+        assert H.worker_gguf_summary()[2:] == (1, 2 * i * h * 2)
+    finally:
+        H.configure_worker_gguf_from_args(None, False, False, False, True, ROCM, H.DType.F16, 1)

@@ -15,7 +15,7 @@ from helpers import (empty_out, exact_inputs, k_align, make_weight, reference_pr
 
 pytestmark = pytest.mark.gpu
 
-ALL_FORMATS = [dq.W8A16, dq.Q8_0, dq.Q4_K, dq.FP8_ROW, dq.FP8_BLOCK, dq.NVFP4, dq.MXFP4]
+ALL_FORMATS = [dq.W8A16, dq.Q8_0, dq.Q4_K, dq.Q6_K, dq.FP8_ROW, dq.FP8_BLOCK, dq.NVFP4, dq.MXFP4]
 TOL_BF16 = 1e-3   # relative L2, weight-only products
 TOL_LOWP = 2e-3   # relative L2, native fp8 / fp4 prefill
 

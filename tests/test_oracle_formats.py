@@ -138,6 +138,46 @@ def test_q4_k_quantizer_round_trip(O):
             assert max(scs) == 63
 
 
+def _q6k_encode(codes, scales, d):
+    """One Q6_K block from 256 6-bit codes, 16 i8 scales and an f16 d, placed
+    element by element from the block layout description: value e of half
+    h = e // 128 (w = e % 128, quarter qd = w // 32, l = w % 32) keeps its
+    low 4 bits in nibble qd // 2 of ql[64h + 32(qd % 2) + l] and its top 2
+    bits at bit 2qd of qh[32h + l]; sub-block e // 16 has scales[e // 16]."""
+    blk = np.zeros(210, np.uint8)
+    for e in range(256):
+        h, w = divmod(e, 128)
+        qd, l = divmod(w, 32)
+        blk[64 * h + 32 * (qd % 2) + l] |= (int(codes[e]) & 15) << (4 * (qd // 2))
+        blk[128 + 32 * h + l] |= (int(codes[e]) >> 4) << (2 * qd)
+    blk[192:208] = np.asarray(scales, np.int8).view(np.uint8)
+    blk[208:210] = np.array([d], np.float16).view(np.uint8)
+    return blk
+
+
+def test_q6_k_dequant_element_layout(O):
+    rng = np.random.default_rng(6)
+    blocks, expect = [], []
+    for trial in range(6):
+        codes = rng.integers(0, 64, 256)
+        scales = rng.integers(-128, 128, 16)
+        d = np.float16(rng.uniform(1e-4, 1e-2) * (-1 if trial == 3 else 1))
+        blocks.append(_q6k_encode(codes, scales, d))
+        # exact in f32: f16 d (11 bits) * i8 scale (8) * (q - 32) (6)
+        expect.append((np.float64(d) * scales[np.arange(256) // 16] * (codes - 32.0)).astype(np.float32))
+    # 3 rows x 2 super-blocks
+    got = O.q6_k_dequant(np.concatenate(blocks).reshape(3, 420), 3, 512)
+    assert np.array_equal(got.ravel().view(np.uint32), np.concatenate(expect).view(np.uint32))
+    # invariants: d = 0 -> zeros; every code 32 -> zeros; unit scales and
+    # codes e % 64 -> (e % 64) - 32 in order
+    z = O.q6_k_dequant(_q6k_encode(rng.integers(0, 64, 256), rng.integers(-128, 128, 16), 0.0)[None], 1, 256)
+    assert not z.any()
+    z = O.q6_k_dequant(_q6k_encode(np.full(256, 32), rng.integers(-128, 128, 16), 0.5)[None], 1, 256)
+    assert not z.any()
+    ramp = O.q6_k_dequant(_q6k_encode(np.arange(256) % 64, np.ones(16), 1.0)[None], 1, 256)
+    assert np.array_equal(ramp.ravel(), (np.arange(256) % 64 - 32).astype(np.float32))
+
+
 def test_fp8_block_quantizer_matches_torch_cast(O):
     rng = np.random.default_rng(4)
     n, k = 200, 300                             # ragged: partial 128-blocks
