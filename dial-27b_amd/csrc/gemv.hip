@@ -57,13 +57,41 @@ constexpr int kGemvWaves = 4;  // waves per workgroup
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
+typedef __attribute__((address_space(3))) float lds_f32;
+
 struct Ctx {
   rsrc_t rt, ra, rx;
   const lds_u8 *xl;    // staged rows (XL)
   const lds_u8 *zero;  // 32 zero bytes (XL)
+  const lds_f32 *xs;   // [mrows][nsub] activation sums per scale sub-block (policies with XS)
+  int nsub;            // sub-blocks per row in xs
   int pitch;           // bytes per staged row
   int mrows, K;
 };
+
+// Activation sums per scale sub-block of `sub` values, from the staged rows:
+// xs[m][b] = sum of x[m][b*sub .. b*sub + sub-1] (the padded tail reads as
+// zeros).  Filled by all threads of the workgroup.
+template <int ACT>
+__device__ __forceinline__ void stage_xsums(const Ctx &cx, lds_f32 *xs, int sub, int threads) {
+  constexpr int BY = ActTraits<ACT>::BYTES;
+  const int total = cx.mrows * cx.nsub;
+  for (int e = threadIdx.x; e < total; e += threads) {
+    const int m = e / cx.nsub, b = e - m * cx.nsub;
+    const lds_u8 *src = cx.xl + m * cx.pitch + b * sub * BY;
+    float a = 0.0f;
+    for (int i = 0; i < sub * BY; i += 16) {
+      const u32x4 v = *(const u32x4 __attribute__((address_space(3))) *)(src + i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (ACT == DIALQ_BF16) a += bf16_bits_to_f32(v[j] & 0xffffu) + bf16_bits_to_f32(v[j] >> 16);
+        else if constexpr (ACT == DIALQ_F16) a += f16_bits_to_f32(v[j] & 0xffffu) + f16_bits_to_f32(v[j] >> 16);
+        else a += __uint_as_float(v[j]);
+      }
+    }
+    xs[e] = a;
+  }
+}
 
 template <int ACT, bool XL>
 __device__ __forceinline__ XRaw<ACT> x_fetch(const Ctx &cx, int row, int k, bool valid) {
@@ -126,6 +154,7 @@ template <int FMT, int ACT, bool XL>
 struct GenericPolicy {
   typedef FmtTraits<FMT> T;
   static constexpr int XACT = ACT;
+  static constexpr int XSUB = 0;  // no activation-sum table
   static constexpr int NV = 4;  // accumulator values per lane
   struct Slot {
     RawTile t;
@@ -176,10 +205,11 @@ struct GenericPolicy {
 // term use the per-sub-block activation sums X_t[m'] from a second MFMA with
 // a ones operand:  y += s1*D - (128*s1 + dmin*m)*X.  RP passes cover rows
 // 4*pass + m'.
-template <int ACT, int RP, bool XL>
+template <int ACT, int RP, bool XL, bool XS>
 struct Q4kRowsPolicy {
   static constexpr int XACT = ACT;
   static constexpr int NV = RP;
+  static constexpr int XSUB = XS ? 32 : 0;  // XS: sums from the staged table, no ones-operand MFMA
   struct Slot {
     RawTile t;
     int c;
@@ -220,38 +250,63 @@ struct Q4kRowsPolicy {
     const uint32_t qd[8] = {sl.t.a[0], sl.t.a[1], sl.t.a[2], sl.t.a[3], sl.t.b[0], sl.t.b[1], sl.t.b[2], sl.t.b[3]};
 #pragma unroll
     for (int q = 0; q < RP; ++q) {
-      XOp<ACT> xa, xb;
-      if constexpr (XL) {
-        xa = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, 4 * q + mq, xk(sl.c, 0, lane), true));
-        xb = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, 4 * q + mq, xk(sl.c, 1, lane), true));
-      } else {
-        xa = xraw_to_op<ACT>(sl.x.v[2 * q]);
-        xb = xraw_to_op<ACT>(sl.x.v[2 * q + 1]);
-      }
       f32x4 cq[2] = {zero, zero}, cs[2] = {zero, zero};
+      if constexpr (XL && ACT == DIALQ_BF16) {
+        // bf16 operands straight from the staged rows: a lane outside MFMA
+        // t's sub-block (or past the last row) reads the zero block
+        const int row = 4 * q + mq;
+        const lds_u8 *rowp = cx.xl + row * cx.pitch + (sl.c * 256 + 8 * (lane >> 4)) * 2;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const u32x4 wb = nib8_to_bf16_off128(qd[2 * (t >> 1)], qd[2 * (t >> 1) + 1], (t & 1) ? 4 : 0);
-        const bool on = (jj == (t & 3));
-        const XOp<ACT> &src = (t < 4) ? xa : xb;
-        XOp<ACT> av;
-        av.hi = on ? src.hi : (u32x4){0, 0, 0, 0};
-        if constexpr (ActTraits<ACT>::PARTS == 2) av.lo = on ? src.lo : (u32x4){0, 0, 0, 0};
-        cq[t >> 2] = mfma_x<ACT>(av, wb, cq[t >> 2]);
-        cs[t >> 2] = mfma_x<ACT>(av, ones, cs[t >> 2]);
+        for (int t = 0; t < 8; ++t) {
+          const u32x4 wb = nib8_to_bf16_off128(qd[2 * (t >> 1)], qd[2 * (t >> 1) + 1], (t & 1) ? 4 : 0);
+          const lds_u8 *src = (jj == (t & 3) && row < cx.mrows) ? rowp + 64 * t : cx.zero;
+          XOp<ACT> av;
+          av.hi = *(const u32x4 __attribute__((address_space(3))) *)src;
+          cq[t >> 2] = mfma_x<ACT>(av, wb, cq[t >> 2]);
+          if constexpr (!XS) cs[t >> 2] = mfma_x<ACT>(av, ones, cs[t >> 2]);
+        }
+      } else {
+        XOp<ACT> xa, xb;
+        if constexpr (XL) {
+          xa = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, 4 * q + mq, xk(sl.c, 0, lane), true));
+          xb = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, 4 * q + mq, xk(sl.c, 1, lane), true));
+        } else {
+          xa = xraw_to_op<ACT>(sl.x.v[2 * q]);
+          xb = xraw_to_op<ACT>(sl.x.v[2 * q + 1]);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const u32x4 wb = nib8_to_bf16_off128(qd[2 * (t >> 1)], qd[2 * (t >> 1) + 1], (t & 1) ? 4 : 0);
+          const bool on = (jj == (t & 3));
+          const XOp<ACT> &src = (t < 4) ? xa : xb;
+          XOp<ACT> av;
+          av.hi = on ? src.hi : (u32x4){0, 0, 0, 0};
+          if constexpr (ActTraits<ACT>::PARTS == 2) av.lo = on ? src.lo : (u32x4){0, 0, 0, 0};
+          cq[t >> 2] = mfma_x<ACT>(av, wb, cq[t >> 2]);
+          if constexpr (!XS) cs[t >> 2] = mfma_x<ACT>(av, ones, cs[t >> 2]);
+        }
       }
-      // lane (g, r) holds rows 4g+i: m' = g, sub-block i (+4 in [1])
-      float sum = acc.v[q];
+      if constexpr (XS) {
+        // rows 4g+i of the accumulators: m' = g, sub-blocks i and i + 4
+        const int g = lane >> 4, mr = (4 * q + g) < cx.mrows ? 4 * q + g : cx.mrows - 1;
+        const lds_f32 *xr = cx.xs + mr * cx.nsub + sl.c * 8;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          cs[0][i] = xr[i];
+          cs[1][i] = xr[4 + i];
+        }
+      }
+      // lane (g, r) holds rows 4g+i: m' = g, sub-block i (+4 in [1]);
+      // s1*D - (128*s1 + dmin*m)*X = d*sc*(D - 128 X) - dmin*m*X
+      float sa = 0.0f, sm = 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float s1a = d * (float)((sc_lo >> (8 * i)) & 0xffu);
-        const float s2a = __builtin_fmaf(128.0f, s1a, dmin * (float)((m_lo >> (8 * i)) & 0xffu));
-        const float s1b = d * (float)((sc_hi >> (8 * i)) & 0xffu);
-        const float s2b = __builtin_fmaf(128.0f, s1b, dmin * (float)((m_hi >> (8 * i)) & 0xffu));
-        sum = __builtin_fmaf(s1a, cq[0][i], __builtin_fmaf(-s2a, cs[0][i], sum));
-        sum = __builtin_fmaf(s1b, cq[1][i], __builtin_fmaf(-s2b, cs[1][i], sum));
+        sa = __builtin_fmaf((float)((sc_lo >> (8 * i)) & 0xffu), __builtin_fmaf(-128.0f, cs[0][i], cq[0][i]), sa);
+        sa = __builtin_fmaf((float)((sc_hi >> (8 * i)) & 0xffu), __builtin_fmaf(-128.0f, cs[1][i], cq[1][i]), sa);
+        sm = __builtin_fmaf((float)((m_lo >> (8 * i)) & 0xffu), cs[0][i], sm);
+        sm = __builtin_fmaf((float)((m_hi >> (8 * i)) & 0xffu), cs[1][i], sm);
       }
-      acc.v[q] = sum;
+      acc.v[q] = __builtin_fmaf(d, sa, __builtin_fmaf(-dmin, sm, acc.v[q]));
     }
   }
   static __device__ __forceinline__ void values(const Acc &a, float (&v)[NV], int (&mrow)[NV], int lane) {
@@ -272,10 +327,11 @@ struct Q4kRowsPolicy {
 // (t = 2u + jj/2), and MFMAs 2u, 2u+1 leave D_{4u+jj}[m'][n] in rows
 // 4m' + jj of accumulator u.  Weights enter as bf16(128 + q); with X the
 // sub-block's activation sums (ones operand), y += d*sc*(D - 160 X).
-template <int ACT, int RP, bool XL>
+template <int ACT, int RP, bool XL, bool XS>
 struct Q6kRowsPolicy {
   static constexpr int XACT = ACT;
   static constexpr int NV = RP;
+  static constexpr int XSUB = XS ? 16 : 0;  // XS: sums from the staged table, no ones-operand MFMA
   struct Slot {
     RawTile t;
     int c;
@@ -318,10 +374,13 @@ struct Q6kRowsPolicy {
 #pragma unroll
     for (int q = 0; q < RP; ++q) {
       f32x4 cq[4], cs[4];
+      const int row = 4 * q + mq;
+      const lds_u8 *rowp = cx.xl + row * cx.pitch + (sl.c * 256 + 8 * (lane >> 4)) * 2;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         XOp<ACT> src;
-        if constexpr (XL) src = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, 4 * q + mq, xk(sl.c, u, lane), true));
+        if constexpr (XL && ACT == DIALQ_BF16) (void)src;
+        else if constexpr (XL) src = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, 4 * q + mq, xk(sl.c, u, lane), true));
         else src = xraw_to_op<ACT>(sl.x.v[4 * q + u]);
         cq[u] = zero;
         cs[u] = zero;
@@ -329,11 +388,27 @@ struct Q6kRowsPolicy {
         for (int v = 0; v < 2; ++v) {
           const bool on = gmatch && (v == (jj >> 1));
           XOp<ACT> av;
-          av.hi = on ? src.hi : z4;
-          if constexpr (ActTraits<ACT>::PARTS == 2) av.lo = on ? src.lo : z4;
+          if constexpr (XL && ACT == DIALQ_BF16) {
+            // bf16 operands straight from the staged rows; lanes that feed
+            // zeros (or rows past the last) read the zero block
+            const lds_u8 *p = (on && row < cx.mrows) ? rowp + 64 * (2 * u + v) : cx.zero;
+            av.hi = *(const u32x4 __attribute__((address_space(3))) *)p;
+          } else {
+            av.hi = on ? src.hi : z4;
+            if constexpr (ActTraits<ACT>::PARTS == 2) av.lo = on ? src.lo : z4;
+          }
           cq[u] = mfma_x<ACT>(av, wb[2 * u + v], cq[u]);
-          cs[u] = mfma_x<ACT>(av, ones, cs[u]);
+          if constexpr (!XS) cs[u] = mfma_x<ACT>(av, ones, cs[u]);
         }
+      }
+      if constexpr (XS) {
+        // rows 4g+i of accumulator u: m' = g, sub-block 4u + i
+        const int g = lane >> 4, mr = (4 * q + g) < cx.mrows ? 4 * q + g : cx.mrows - 1;
+        const lds_f32 *xr = cx.xs + mr * cx.nsub + sl.c * 16;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) cs[u][i] = xr[4 * u + i];
       }
       // lane (g, r) holds rows 4g+i: m' = g, sub-block 4u + i = byte i of sc[u]
       float sum = 0.0f;
@@ -410,7 +485,12 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
   cx.pitch = p.x_pitch;
   cx.xl = (const lds_u8 *)smem;
   cx.zero = (const lds_u8 *)smem + (XL ? mrows * p.x_pitch : 0);
-  float *part = (float *)(smem + (XL ? mrows * p.x_pitch + 32 : 0));
+  // LDS: [staged x][32 zero bytes][activation sums (XSUB)][parked accumulators]
+  constexpr bool XSUMS = XL && Pol::XSUB > 0;
+  cx.nsub = XSUMS ? (int)(w.k_chunks * FmtTraits<FMT>::CHUNK / (XSUMS ? Pol::XSUB : 1)) : 0;
+  lds_f32 *xsums = (lds_f32 *)(smem + (XL ? mrows * p.x_pitch + 32 : 0));
+  cx.xs = xsums;
+  float *part = (float *)(smem + (XL ? mrows * p.x_pitch + 32 : 0) + (size_t)mrows * cx.nsub * 4);
   cx.rt = make_rsrc(w.tiles, (uint32_t)(total * 64 * FmtTraits<FMT>::LANE));
   cx.ra = cx.rt;
   if constexpr (FMT == DIALQ_FORMAT_Q8_0 || FMT == DIALQ_FORMAT_MXFP4)
@@ -461,6 +541,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
     }
   }
   if constexpr (XL) lds_barrier();  // staged x visible to all waves
+  if constexpr (XSUMS) {
+    stage_xsums<Pol::XACT>(cx, xsums, Pol::XSUB, 64 * W);
+    lds_barrier();
+  }
   typename Pol::Acc acc;
   Pol::zero(acc);
   int cur = slot_s[0];
@@ -788,6 +872,8 @@ __global__ __launch_bounds__(64 * (kDynWaves + 1)) void k_gemv_dyn(DynParams p) 
   cx.pitch = p.x_pitch;
   cx.xl = (const lds_u8 *)xbase;
   cx.zero = (const lds_u8 *)xbase + (XL ? mrows * p.x_pitch : 0);
+  cx.xs = nullptr;  // the dynamic kernel's policies take their sums from MFMAs
+  cx.nsub = 0;
   const int64_t total = w.n_strips * w.k_chunks;
   cx.rt = make_rsrc(w.tiles, (uint32_t)(total * 64 * FmtTraits<FMT>::LANE));
   cx.ra = cx.rt;
@@ -961,7 +1047,10 @@ static hipError_t launch_ranges(GemvParams &p, hipStream_t st) {
   const size_t park = (size_t)nseg * kGemvWaves * mrows * 16 * sizeof(float);
   if (park > (size_t)kGemvParkBytes) return hipErrorInvalidConfiguration;
   if (p.spw == 0 && (size_t)p.G * 2 * mrows * 16 * sizeof(float) > p.ws_bytes) return hipErrorInvalidValue;
-  const size_t lds = park + (XL ? (size_t)mrows * p.x_pitch + 32 : 0);
+  const size_t xsums = (XL && Pol::XSUB > 0)
+                           ? (size_t)mrows * (p.w.k_chunks * FmtTraits<FMT>::CHUNK / (Pol::XSUB > 0 ? Pol::XSUB : 1)) * 4
+                           : 0;
+  const size_t lds = park + (XL ? (size_t)mrows * p.x_pitch + 32 : 0) + xsums;
   k_gemv<FMT, Pol, U, XL><<<(unsigned)p.G, 64 * kGemvWaves, lds, st>>>(p);
   return hipGetLastError();
 }
@@ -985,28 +1074,28 @@ static hipError_t launch_dyn(DynParams &p, int64_t mrows, hipStream_t st) {
 // Matrices with at least one strip per CU: static whole-strip ranges (no
 // strip shared between workgroups).  Smaller ones: the dynamic kernel, whose
 // small units keep every CU busy.
-template <int FMT, int ACT, template <int, int, bool> class PolT, int A, int U_XL, int U_X>
+template <int FMT, int ACT, template <int, int, bool, bool> class PolT, int A, int U_XL, int U_X>
 static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
   constexpr int BY = ActTraits<ACT>::BYTES;
   const bool xl = mrows * stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) + 32 <= kGemvStageBytes;
   if (d.w.n_strips >= device_cus()) {
     GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
     p.x_pitch = xl ? stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) : 0;
-    if (xl) return launch_ranges<FMT, PolT<A, ACT, true>, (U_XL < kRangeRing ? U_XL : kRangeRing), true>(p, st);
-    return launch_ranges<FMT, PolT<A, ACT, false>, (U_X < kRangeRing ? U_X : kRangeRing), false>(p, st);
+    if (xl) return launch_ranges<FMT, PolT<A, ACT, true, true>, (U_XL < kRangeRing ? U_XL : kRangeRing), true>(p, st);
+    return launch_ranges<FMT, PolT<A, ACT, false, false>, (U_X < kRangeRing ? U_X : kRangeRing), false>(p, st);
   }
   d.x_pitch = xl ? stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) : 0;
-  if (xl) return launch_dyn<FMT, PolT<A, ACT, true>, U_XL, true>(d, mrows, st);
-  return launch_dyn<FMT, PolT<A, ACT, false>, U_X, false>(d, mrows, st);
+  if (xl) return launch_dyn<FMT, PolT<A, ACT, true, false>, U_XL, true>(d, mrows, st);
+  return launch_dyn<FMT, PolT<A, ACT, false, false>, U_X, false>(d, mrows, st);
 }
 
 // Adapters so both policies take <first, ACT, XL> template arguments.
-template <int FMT, int ACT, bool XL>
+template <int FMT, int ACT, bool XL, bool XS>
 using GenericPol = GenericPolicy<FMT, ACT, XL>;
-template <int RP, int ACT, bool XL>
-using Q4kRowsPol = Q4kRowsPolicy<ACT, RP, XL>;
-template <int RP, int ACT, bool XL>
-using Q6kRowsPol = Q6kRowsPolicy<ACT, RP, XL>;
+template <int RP, int ACT, bool XL, bool XS>
+using Q4kRowsPol = Q4kRowsPolicy<ACT, RP, XL, XS>;
+template <int RP, int ACT, bool XL, bool XS>
+using Q6kRowsPol = Q6kRowsPolicy<ACT, RP, XL, XS>;
 
 template <int FMT, int ACT>
 static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype,
