@@ -13,8 +13,10 @@ Layer copies rotate so the weight working set (COPIES x 341 MB) exceeds the
 256 MB Infinity Cache and the figure measures HBM.  `value` = algorithmic
 weight bytes streamed / wall time of the timed steps, in GB/s.  Extra keys
 report the same decode for Q4_K / FP8-128 / MXFP4, the prefill GEMM TFLOP/s
-(W8A16 and Q4_K at M = 2048, FP8-128 and MXFP4 native at M = 1024), the
-roofline of the dominant kernel and the CPU baseline.
+(W8A16 and Q4_K at M = 2048, FP8-128 and MXFP4 native at M = 1024; also over
+the fused qkv / o / gate_up / down projections DIAL's layers call), the
+quantized lm_head decode GEMV (vocab 248320 x 5120), the roofline of the
+dominant kernel and the CPU baseline.
 
 `--profile` runs only the dominant kernel (W8A16 gate GEMV, eager launches
 over rotating copies) plus a 256 MiB device-to-device copy used to scale the
@@ -40,6 +42,7 @@ LAYER_27B = [("q", 6144, 5120), ("k", 1024, 5120), ("v", 1024, 5120), ("o", 5120
 # The same weights as the fused projections DIAL's Qwen3-VL layers run
 # (cat(q, k, v) rows and cat(gate, up) rows, qwen3_vl/text.rs): four linears.
 LAYER_27B_FUSED = [("qkv", 8192, 5120), ("o", 5120, 6144), ("gate_up", 34816, 5120), ("down", 5120, 17408)]
+LM_HEAD_27B = (248320, 5120)  # vocab x hidden
 METRIC = "quant GEMV weight GB/s (% HBM peak) + prefill GEMM TFLOP/s, 27B shapes, 1 GPU"
 
 
@@ -51,6 +54,7 @@ def parse():
     ap.add_argument("--copies", type=int, default=3, help="layer copies rotated per step")
     ap.add_argument("--prefill-iters", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-lm-head", action="store_true", help="skip the lm_head decode line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--sweep", default="w8a16,q4_k,fp8_block,mxfp4",
                     help="formats for the extra decode / prefill numbers ('' = none)")
@@ -203,14 +207,14 @@ def profile_prefill_run(dq, torch, dev, iters=5):
         torch.cuda.empty_cache()
 
 
-def time_prefill(dq, torch, lins, m, iters, dev, path):
+def time_prefill(dq, torch, lins, m, iters, dev, path, shapes=LAYER_27B):
     """Device time of one prefill pass over the layer's seven linears
     (activation quantization included for the native paths), captured in a
     HIP graph like the decode step and replayed `iters` times between HIP
     events on the replay stream."""
     stream = torch.cuda.current_stream()
-    xs = [torch.randn(m, k, device=dev).to(torch.bfloat16) for _, n, k in LAYER_27B]
-    ys = [torch.empty(m, n, device=dev, dtype=torch.bfloat16) for _, n, k in LAYER_27B]
+    xs = [torch.randn(m, k, device=dev).to(torch.bfloat16) for _, n, k in shapes]
+    ys = [torch.empty(m, n, device=dev, dtype=torch.bfloat16) for _, n, k in shapes]
 
     def body(st):
         for lin, x, y in zip(lins, xs, ys):
@@ -227,7 +231,7 @@ def time_prefill(dq, torch, lins, m, iters, dev, path):
     e1.record(stream)
     e1.synchronize()
     secs = e0.elapsed_time(e1) * 1e-3 / iters
-    flops = 2.0 * m * sum(n * k for _, n, k in LAYER_27B)
+    flops = 2.0 * m * sum(n * k for _, n, k in shapes)
     return flops / secs / 1e12, secs
 
 
@@ -315,8 +319,27 @@ def main():
     extra["decode_gbs_fused_qkv_gate_up"] = {"w8a16": round(layer_bytes(dq, dq.W8A16, LAYER_27B_FUSED) * fsteps / fs / 1e9, 1)}
     print(f"# w8a16 decode, fused qkv / gate_up: {extra['decode_gbs_fused_qkv_gate_up']['w8a16']} GB/s",
           file=sys.stderr, flush=True)
+    if "w8a16" in sweep:
+        tf, s2 = time_prefill(dq, torch, fl[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, shapes=LAYER_27B_FUSED)
+        extra.setdefault("prefill_tflops_fused_qkv_gate_up", {})["w8a16_m2048"] = round(tf, 1)
     del fl
     torch.cuda.empty_cache()
+    # quantized lm_head GEMV (vocab 248320 x hidden 5120): one copy is 1.27 GB
+    # (W8A16) / 0.68 GB (MXFP4), far past the 256 MB last-level cache
+    if not a.no_lm_head:
+        vn, vk = LM_HEAD_27B
+        extra["decode_lm_head"] = {}
+        for name, fmt in (("w8a16", dq.W8A16), ("mxfp4", dq.MXFP4)):
+            gl = torch.Generator(device=dev).manual_seed(21)
+            lin = dq.Linear.quantize(fmt, torch.randn(vn, vk, device=dev, generator=gl) * 0.02, scale_dtype=dq.BF16)
+            torch.cuda.empty_cache()
+            ls_ = time_launches(dq, torch, [lin], vk, vn, dev, reps=20)
+            gbs = dq.raw_weight_bytes(fmt, vn, vk) / ls_ / 1e9
+            extra["decode_lm_head"][name] = {"us": round(ls_ * 1e6, 1), "gbs": round(gbs, 1),
+                                             "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 1)}
+            print(f"# lm_head {vn}x{vk} {name} decode: {ls_ * 1e6:.1f} us, {gbs:.1f} GB/s", file=sys.stderr, flush=True)
+            del lin
+            torch.cuda.empty_cache()
     for name in sweep:
         if name == "w8a16":
             continue
@@ -330,6 +353,13 @@ def main():
             extra["prefill_tflops"][name + "_native_m1024"] = round(tf, 1)
             peak = MFMA_PEAK_TFLOPS["fp8" if fmt == dq.FP8_BLOCK else "fp4"]
             extra["prefill_pct_mfma_peak"][name + "_native_m1024"] = round(100.0 * tf / peak, 1)
+            # the fused projections DIAL's layers call (qkv, o, gate_up, down)
+            del ls
+            torch.cuda.empty_cache()
+            ls = build_layers(dq, torch, fmt, 1, dev, seed=5, shapes=LAYER_27B_FUSED)
+            tff, _ = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE,
+                                  shapes=LAYER_27B_FUSED)
+            extra.setdefault("prefill_tflops_fused_qkv_gate_up", {})[name + "_native_m1024"] = round(tff, 1)
         else:
             tf, s2 = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
             extra["prefill_tflops"][name + "_m2048"] = round(tf, 1)

@@ -7,6 +7,7 @@
 
 #include "dial_host.hpp"
 #include "gguf.hpp"
+#include "safetensors.hpp"
 
 namespace py = pybind11;
 using namespace dial;
@@ -133,6 +134,10 @@ PYBIND11_MODULE(dialq_host, m) {
   py::class_<VarStore>(m, "VarStore")
       .def(py::init<DType, Device>())
       .def("insert", &VarStore::insert)
+      .def("get", &VarStore::get)
+      .def("load_safetensors", [](VarStore &vs, const std::vector<std::string> &paths) {
+        safetensors::load_into(vs, paths);
+      })
       .def("pp", &VarStore::pp)
       .def("contains_tensor", &VarStore::contains_tensor)
       .def_property_readonly("prefix", &VarStore::prefix);
@@ -195,6 +200,18 @@ PYBIND11_MODULE(dialq_host, m) {
   m.def("worker_gguf_summary", &worker_gguf_summary);
   m.def("load_worker_gguf_linear", &load_worker_gguf_linear);
   m.def("gguf_read", &gguf_read);
+  m.def("safetensors_read_header", [](const std::string &path) {
+    const safetensors::Header h = safetensors::read_header(path);
+    py::dict tensors;
+    for (const auto &kv : h.tensors)
+      tensors[py::str(kv.first)] = py::make_tuple(kv.second.dtype, kv.second.shape, kv.second.begin, kv.second.end);
+    py::dict out;
+    out["data_start"] = h.data_start;
+    out["tensors"] = tensors;
+    out["metadata"] = h.metadata;
+    return out;
+  });
+  m.def("safetensors_paths_from_index", &safetensors::paths_from_index);
   m.def("gguf_tensor_bytes", &gguf_tensor_bytes);
   m.def("worker_gguf_prefill_for_dims", &worker_gguf_prefill_for_dims);
   m.def("forward_worker_gguf", &forward_worker_gguf);

@@ -117,3 +117,11 @@ def test_q6_k_full_size(shape, torch_dev):
         got = yt[:, torch.from_numpy(rows).to(torch_dev)].float().cpu().numpy()
         ref = O.round_bf16((x.astype(np.float64) @ deq.astype(np.float64).T).astype(np.float32))
         assert O.rel_l2(got, ref) <= 1e-3, (n, k, m)
+
+
+@pytest.mark.parametrize("fmt", [dq.W8A16, dq.MXFP4], ids=["w8a16", "mxfp4"])
+def test_lm_head_27b(fmt, torch_dev):
+    # the quantized output head (vocab 248320 x hidden 5120,
+    # qwen3_8/model.rs:433-438): 1.27 GB of W8A16 tiles, the largest GEMV
+    for m in (1, 8):
+        _check(fmt, 248320, 5120, m, torch_dev)

@@ -231,3 +231,45 @@ def test_worker_gguf_file_linears_load_and_match_oracle(tmp_path, torch_dev):
         assert H.worker_gguf_summary()[2:] == (1, 2 * i * h * 2)
     finally:
         H.configure_worker_gguf_from_args(None, False, False, False, True, ROCM, H.DType.F16, 1)
+
+
+def test_linear_no_bias_from_safetensors_checkpoint(tmp_path, torch_dev):
+    # The reference's KATs (quant.rs:564-594 ModelOpt NVFP4, 650-680
+    # compressed-tensors NVFP4, 596-619 FP8 per-row) stored the way real
+    # checkpoints store them -- U8 packed codes, F8_E4M3 weights and group
+    # scales, F32 global / row scales -- in a safetensors file read by the
+    # host layer's reader, then decoded dense and run quantized.
+    import torch
+    from safetensors.torch import save_file
+    e4 = torch.float8_e4m3fn
+    path = tmp_path / "model.safetensors"
+    save_file({
+        "model.layers.0.mlp.down_proj.weight": torch.full((1, 8), 0x92, dtype=torch.uint8),
+        "model.layers.0.mlp.down_proj.weight_scale": torch.tensor([[2.0]]).to(e4),
+        "model.layers.0.mlp.down_proj.weight_scale_2": torch.tensor([4.0]),
+        "model.layers.0.mlp.up_proj.weight_packed": torch.full((1, 8), 0x92, dtype=torch.uint8),
+        "model.layers.0.mlp.up_proj.weight_scale": torch.tensor([[2.0]]).to(e4),
+        "model.layers.0.mlp.up_proj.weight_global_scale": torch.tensor([4.0]),
+        "model.layers.0.self_attn.q_proj.weight": torch.tensor([[1.0, 2.0], [3.0, 4.0]]).to(e4),
+        "model.layers.0.self_attn.q_proj.weight_scale": torch.tensor([2.0, 0.5]),
+    }, str(path))
+    try:
+        H.configure_quant_linear(H.Qwen38QuantLinear.Dense, ROCM, H.DType.F32)
+        vb = H.VarStore(H.DType.F32, ROCM)
+        vb.load_safetensors([str(path)])
+        layer = vb.pp("model").pp("layers").pp("0")
+        assert _dense_values(H.linear_no_bias(16, 1, layer.pp("mlp").pp("down_proj"))) == [8.0, -4.0] * 8
+        assert _dense_values(H.linear_no_bias(16, 1, layer.pp("mlp").pp("up_proj"))) == [0.5, -0.25] * 8
+        assert _dense_values(H.linear_no_bias(2, 2, layer.pp("self_attn").pp("q_proj"))) == [2.0, 4.0, 1.5, 2.0]
+        H.configure_quant_linear(H.Qwen38QuantLinear.Rocm, ROCM, H.DType.F16)
+        vb16 = H.VarStore(H.DType.F16, ROCM)
+        vb16.load_safetensors([str(path)])
+        q = H.linear_no_bias(16, 1, vb16.pp("model.layers.0.mlp.down_proj"))
+        assert q.is_quantized_rocm()
+        x = _t(np.cos(np.arange(2 * 16) * 0.3).astype(np.float16).reshape(2, 16)).to_device(ROCM)
+        got = q.forward(x).numpy().astype(np.float32).ravel()
+        want = (np.cos(np.arange(2 * 16) * 0.3).astype(np.float16).astype(np.float64).reshape(2, 16)
+                @ np.array([8.0, -4.0] * 8))
+        assert np.abs(got - want).max() <= 2e-3 * np.abs(want).max()
+    finally:
+        H.configure_quant_linear(H.Qwen38QuantLinear.Dense, ROCM, H.DType.F16)
