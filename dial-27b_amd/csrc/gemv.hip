@@ -11,10 +11,11 @@
 // weight bytes are read exactly once per launch.
 //
 // Work split: the n_strips * k_chunks tiles, in resident (strip-major)
-// order, are cut into G equal contiguous ranges, one per workgroup (stream-K
-// over the whole matrix, so every workgroup streams the same number of
-// bytes whatever the strip count).  The 4 waves of a workgroup take
-// interleaved tiles of its range; each keeps a register ring of U slots --
+// order, are cut into ranges of whole strips, one strip per workgroup (the
+// kernel also takes equal tile ranges that split strips -- stream-K -- with
+// the fix-up below; the launcher uses whole strips, which measured faster).
+// The 4 (8 below one strip per CU) waves of a workgroup take interleaved
+// tiles of its range; each keeps a register ring of U slots --
 // one weight tile, its scales and the activation operands it multiplies, all
 // fetched with raw buffer loads whose out-of-range offsets return zeros in
 // hardware (no branch, no traffic) -- and refills a slot as soon as it has
@@ -46,7 +47,8 @@ struct GemvParams {
   int *cnt;        // [n_strips] arrival counters (zero between launches)
 };
 
-constexpr int kGemvWaves = 4;  // waves per workgroup
+constexpr int kGemvWaves = 4;       // waves per workgroup, whole-strip kernel at >= 1 strip per CU
+constexpr int kGemvSmallWaves = 8;  // the same kernel below one strip per CU
 
 // ---------------------------------------------------------------------------
 // Activation source.  Small activations (XL) are staged once per workgroup
@@ -435,14 +437,14 @@ struct Q6kRowsPolicy {
 // [part[j][wave][m][16]: the accumulator of wave `wave` for the j-th strip
 // of the range, rows m < mrows only].
 // ---------------------------------------------------------------------------
-template <typename Pol>
+template <typename Pol, int W>
 __device__ __forceinline__ void park(float *part, int j, int wave, int mrows, const typename Pol::Acc &acc) {
   constexpr int NV = Pol::NV;
   const int lane = threadIdx.x & 63, r = lane & 15;
   float v[NV];
   int mrow[NV];
   Pol::values(acc, v, mrow, lane);
-  float *dst = part + (size_t)(j * kGemvWaves + wave) * mrows * 16;
+  float *dst = part + (size_t)(j * W + wave) * mrows * 16;
 #pragma unroll
   for (int i = 0; i < NV; ++i)
     if (mrow[i] < mrows) dst[mrow[i] * 16 + r] = v[i];
@@ -455,10 +457,10 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int FMT, typename Pol, int U, bool XL>
-__global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
+template <int FMT, typename Pol, int U, bool XL, int WV>
+__global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  constexpr int W = kGemvWaves;
+  constexpr int W = WV;
   constexpr int BY = ActTraits<Pol::XACT>::BYTES;
   const WeightView &w = p.w;
   const int lane = threadIdx.x & 63;
@@ -553,7 +555,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
     for (int u = 0; u < U; ++u) {
       if (slot_s[u] >= 0) {
         if (slot_s[u] != cur) {
-          park<Pol>(part, cur - s_first, wave, mrows, acc);
+          park<Pol, W>(part, cur - s_first, wave, mrows, acc);
           Pol::zero(acc);
           cur = slot_s[u];
         }
@@ -570,7 +572,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemvParams p) {
       }
     }
   }
-  if (cur >= 0) park<Pol>(part, cur - s_first, wave, mrows, acc);
+  if (cur >= 0) park<Pol, W>(part, cur - s_first, wave, mrows, acc);
   lds_barrier();
 
   // finish: wave j % W takes strip j of the range
@@ -1002,6 +1004,7 @@ constexpr int kGemvWgPerCu = 2;          // target ranges per CU
 constexpr int kRangeRing = 4;            // ring depth cap of the whole-strip kernel
 constexpr int kGemvParkBytes = 16384;    // parking LDS per workgroup
 constexpr int kGemvStageBytes = 65536;   // staged-activation LDS per workgroup
+constexpr int kGemvSmallStageBytes = 131072;  // the same below one strip per CU (about one workgroup per CU)
 
 // Ranges for one pass of mrows rows: kGemvWgPerCu per CU, more when a range
 // would span more strips than its parking LDS holds, never more than tiles.
@@ -1023,35 +1026,37 @@ static int stage_pitch(const WeightView &w, int by, int chunk) {
   return (int)(((kpad_bytes + 1023) / 1024) * 1024 + 64);
 }
 
-// Whole strips per range when there is at least one strip per CU: one strip
-// per workgroup (no strip is shared, so no cross-workgroup fix-up).  Measured
-// on the 27B gate shape: one strip per workgroup and four loads in flight per
-// wave stream 17% faster than two strips and eight loads -- several resident
-// workgroups per CU, each with a shallow ring, keep more of HBM busy than a
-// few deep ones (a plain read kernel shows the same).  0 selects equal tile
-// ranges (stream-K).
-static int gemv_spw(const WeightView &w, int64_t mrows) {
-  (void)mrows;
-  if (w.n_strips < device_cus()) return 0;
-  return 1;
+// Strips per workgroup.  One (no strip is shared, so no cross-workgroup
+// fix-up): measured on the 27B gate shape, one strip per workgroup and four
+// loads in flight per wave stream 17% faster than two strips and eight loads
+// -- several resident workgroups per CU, each with a shallow ring, keep more
+// of HBM busy than a few deep ones (a plain read kernel shows the same).
+// 0 selects equal tile ranges (stream-K), used when several activation rows
+// ride the ring with the weights (too large to stage): there each tile's
+// activation fetch lengthens the loop, and balancing the tiles over 2
+// workgroups per CU measured 17-23 % faster on the 27B down shape at M = 4-8
+// (10-18 % for Q4_K); with staged activations it is slower.
+static int gemv_spw(const WeightView &w, int64_t mrows, bool staged) {
+  (void)w;
+  return (!staged && mrows > 1) ? 0 : 1;
 }
 
-template <int FMT, typename Pol, int U, bool XL>
+template <int FMT, typename Pol, int U, bool XL, int WV>
 static hipError_t launch_ranges(GemvParams &p, hipStream_t st) {
   const int64_t mrows = (p.M - p.m_base) < 16 ? (p.M - p.m_base) : 16;
   const int64_t total = p.w.n_strips * p.w.k_chunks;
-  p.spw = gemv_spw(p.w, mrows);
+  p.spw = gemv_spw(p.w, mrows, XL);
   p.G = p.spw > 0 ? (int)((p.w.n_strips + p.spw - 1) / p.spw) : gemv_grid(p.w, mrows);
   const int64_t per = p.spw > 0 ? p.spw * p.w.k_chunks : (total + p.G - 1) / p.G;
   const int64_t nseg = p.spw > 0 ? p.spw : per / p.w.k_chunks + 2;
-  const size_t park = (size_t)nseg * kGemvWaves * mrows * 16 * sizeof(float);
+  const size_t park = (size_t)nseg * WV * mrows * 16 * sizeof(float);
   if (park > (size_t)kGemvParkBytes) return hipErrorInvalidConfiguration;
   if (p.spw == 0 && (size_t)p.G * 2 * mrows * 16 * sizeof(float) > p.ws_bytes) return hipErrorInvalidValue;
   const size_t xsums = (XL && Pol::XSUB > 0)
                            ? (size_t)mrows * (p.w.k_chunks * FmtTraits<FMT>::CHUNK / (Pol::XSUB > 0 ? Pol::XSUB : 1)) * 4
                            : 0;
   const size_t lds = park + (XL ? (size_t)mrows * p.x_pitch + 32 : 0) + xsums;
-  k_gemv<FMT, Pol, U, XL><<<(unsigned)p.G, 64 * kGemvWaves, lds, st>>>(p);
+  k_gemv<FMT, Pol, U, XL, WV><<<(unsigned)p.G, 64 * WV, lds, st>>>(p);
   return hipGetLastError();
 }
 
@@ -1071,21 +1076,35 @@ static hipError_t launch_dyn(DynParams &p, int64_t mrows, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Matrices with at least one strip per CU: static whole-strip ranges (no
-// strip shared between workgroups).  Smaller ones: the dynamic kernel, whose
-// small units keep every CU busy.
+// Whole-strip ranges (no strip shared between workgroups) whenever the
+// activations can be staged: 4 waves per workgroup at one strip per CU or
+// more, 8 below.  The dynamic kernel, whose small units keep every CU busy,
+// takes the matrices with fewer strips than CUs whose activations are too
+// large to stage.
 template <int FMT, int ACT, template <int, int, bool, bool> class PolT, int A, int U_XL, int U_X>
 static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
   constexpr int BY = ActTraits<ACT>::BYTES;
   const bool xl = mrows * stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) + 32 <= kGemvStageBytes;
+  constexpr int UR = U_XL < kRangeRing ? U_XL : kRangeRing;
   if (d.w.n_strips >= device_cus()) {
     GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
     p.x_pitch = xl ? stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) : 0;
-    if (xl) return launch_ranges<FMT, PolT<A, ACT, true, true>, (U_XL < kRangeRing ? U_XL : kRangeRing), true>(p, st);
-    return launch_ranges<FMT, PolT<A, ACT, false, false>, (U_X < kRangeRing ? U_X : kRangeRing), false>(p, st);
+    if (xl) return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvWaves>(p, st);
+    return launch_ranges<FMT, PolT<A, ACT, false, false>, (U_X < kRangeRing ? U_X : kRangeRing), false, kGemvWaves>(
+        p, st);
   }
-  d.x_pitch = xl ? stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) : 0;
-  if (xl) return launch_dyn<FMT, PolT<A, ACT, true, false>, U_XL, true>(d, mrows, st);
+  if (mrows * stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) + 32 <= kGemvSmallStageBytes) {
+    // Fewer strips than CUs, activations staged: one strip per workgroup of
+    // kGemvSmallWaves waves, so each wave streams a short run of tiles and
+    // nothing is reduced across workgroups.  Measured at M = 1..4 with
+    // K = 5120: 5.3 us for 256..2048 rows where the work queue took 6.8-9.4
+    // (3072 rows: 5.7 against 12.0); K = 17408 at 1024-2048 rows 25-35 %
+    // faster.
+    GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
+    p.x_pitch = stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK);
+    return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvSmallWaves>(p, st);
+  }
+  d.x_pitch = 0;
   return launch_dyn<FMT, PolT<A, ACT, false, false>, U_X, false>(d, mrows, st);
 }
 
@@ -1132,10 +1151,13 @@ static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, v
 }
 
 size_t gemv_workspace_bytes(const WeightView &w, int64_t M) {
-  // pieces per strip are at most ceil(k_chunks / (kDynWaves * 2)) (ring depth >= 2)
+  // work queue: pieces per strip are at most ceil(k_chunks / (kDynWaves * 2))
+  // (ring depth >= 2); equal tile ranges: two partial slots per workgroup
   const int64_t mrows = M < 16 ? M : 16;
   const int64_t pmax = (w.k_chunks + kDynWaves * 2 - 1) / (kDynWaves * 2);
-  return (size_t)w.n_strips * pmax * mrows * 16 * sizeof(float);
+  const size_t dyn = (size_t)w.n_strips * pmax * mrows * 16 * sizeof(float);
+  const size_t ranges = (size_t)gemv_grid(w, mrows) * 2 * mrows * 16 * sizeof(float);
+  return dyn > ranges ? dyn : ranges;
 }
 
 template <int FMT>
