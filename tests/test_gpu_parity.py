@@ -139,6 +139,19 @@ def test_gemv_parity_whole_strip_ranges(fmt, torch_dev):
 
 
 @pytest.mark.parametrize("fmt", ALL_FORMATS, ids=lambda f: dq.FORMAT_NAMES[f])
+def test_gemv_parity_work_queue(fmt, torch_dev):
+    """Fewer strips (19) than CUs with activations too large to stage in LDS
+    (M x K x bytes > 128 KB): the work-queue kernel, whose strips are split
+    into pieces reduced across workgroups."""
+    n, k = 300, 8704
+    lin, _, _, deq = _linear(fmt, n, k, seed=27 + fmt)
+    for m, x_dtype in ((9, dq.BF16), (16, dq.BF16), (4, dq.F32), (20, dq.F16)):
+        y_dtype = dq.F16 if x_dtype == dq.F16 else dq.BF16
+        rel = _run(lin, deq, m, x_dtype, y_dtype, dq.PATH_GEMV, torch_dev, seed=m)
+        assert rel <= TOL_BF16, (dq.FORMAT_NAMES[fmt], m, rel)
+
+
+@pytest.mark.parametrize("fmt", ALL_FORMATS, ids=lambda f: dq.FORMAT_NAMES[f])
 def test_gemv_f32_output(fmt, torch_dev):
     n, k = 64, 256
     lin, _, _, deq = _linear(fmt, n, k, seed=30 + fmt)
