@@ -20,7 +20,8 @@ dominant kernel and the CPU baseline.
 
 `--profile` runs only the dominant kernel (W8A16 gate GEMV, eager launches
 over rotating copies) plus a 256 MiB device-to-device copy used to scale the
-HBM byte counters; `--profile-prefill` runs only the prefill GEMMs of one
+HBM byte counters; `--profile-lm-head` the same for the lm_head GEMV;
+`--profile-prefill` runs only the prefill GEMMs of one
 layer per format.  They are the programs the committed rocprofv3 summaries
 run.
 """
@@ -61,6 +62,8 @@ def parse():
     ap.add_argument("--profile", action="store_true",
                     help="only the dominant kernel's launches and the calibration copy (for rocprofv3)")
     ap.add_argument("--profile-launches", type=int, default=50)
+    ap.add_argument("--profile-lm-head", action="store_true",
+                    help="run only the W8A16 lm_head GEMV (vocab 248320 x 5120) for rocprofv3")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="only the prefill GEMMs of one layer per format (for rocprofv3)")
     return ap.parse_args()
@@ -193,6 +196,29 @@ def profile_run(dq, torch, dev, launches):
           "(calibration: 268435456 bytes read and written per copy)", flush=True)
 
 
+def profile_lm_head_run(dq, torch, dev, launches=20):
+    """The quantized lm_head GEMV (vocab 248320 x 5120, W8A16, one 1.27 GB
+    copy, eager launches) plus the calibration copy."""
+    vn, vk = LM_HEAD_27B
+    g = torch.Generator(device=dev).manual_seed(21)
+    lin = dq.Linear.quantize(dq.W8A16, torch.randn(vn, vk, device=dev, generator=g) * 0.02, scale_dtype=dq.BF16)
+    torch.cuda.empty_cache()
+    x = torch.randn(1, vk, device=dev).to(torch.bfloat16)
+    y = torch.empty(1, vn, device=dev, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream()
+    for _ in range(launches):
+        lin.forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+    torch.cuda.synchronize()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"# profile: {launches} launches of W8A16 lm_head [{vn}x{vk}] M=1 "
+          f"({dq.raw_weight_bytes(dq.W8A16, vn, vk)} weight bytes per launch); 3 copies of 256 MiB "
+          "(calibration: 268435456 bytes read and written per copy)", flush=True)
+
+
 def profile_prefill_run(dq, torch, dev, iters=5):
     """Prefill GEMMs of one 27B layer: FP8-128 and MXFP4 native at M = 1024,
     W8A16 and Q4_K weight-only at M = 2048; each layer runs once eagerly,
@@ -272,6 +298,9 @@ def main():
     dev = torch.device("cuda:0")
     if a.profile:
         profile_run(dq, torch, dev, a.profile_launches)
+        return
+    if a.profile_lm_head:
+        profile_lm_head_run(dq, torch, dev)
         return
     if a.profile_prefill:
         profile_prefill_run(dq, torch, dev)
