@@ -272,9 +272,12 @@ Content Content::read(std::istream &in, uint64_t file_size) {
     const uint32_t n_dims = r.get<uint32_t>();
     if (n_dims > 8) fail("tensor " + name + " has " + std::to_string(n_dims) + " dimensions");
     std::vector<int64_t> dims(n_dims);
+    uint64_t elems = 1;
     for (uint32_t d = 0; d < n_dims; ++d) {
       const uint64_t v = c.version == 1 ? r.get<uint32_t>() : r.get<uint64_t>();
       if (v > (uint64_t)1 << 40) fail("tensor " + name + " has an invalid dimension " + std::to_string(v));
+      if (v != 0 && elems > ((uint64_t)1 << 50) / v) fail("tensor " + name + " has too many elements");
+      elems *= v;
       dims[n_dims - 1 - d] = (int64_t)v;  // candle reverses the ggml order
     }
     const uint32_t ty = r.get<uint32_t>();
@@ -302,8 +305,9 @@ Content Content::read(std::istream &in, uint64_t file_size) {
         break;
     }
   }
-  if (alignment == 0) fail("general.alignment is zero");
+  if (alignment == 0 || alignment > ((uint64_t)1 << 30)) fail("invalid general.alignment " + std::to_string(alignment));
   c.tensor_data_offset = (r.pos() + alignment - 1) / alignment * alignment;
+  c.file_size = file_size;
   return c;
 }
 
@@ -312,6 +316,10 @@ std::vector<uint8_t> Content::tensor_bytes(std::istream &in, const std::string &
   if (it == tensor_infos.end()) fail("cannot find tensor info for " + name);
   const TensorInfo &ti = it->second;
   const int64_t n = ti.size_in_bytes();
+  if (ti.offset > file_size || tensor_data_offset > file_size - ti.offset ||
+      (uint64_t)n > file_size - tensor_data_offset - ti.offset)
+    fail("truncated GGUF tensor " + name + ": " + std::to_string(n) + " bytes at offset " +
+         std::to_string(tensor_data_offset + ti.offset) + " of a " + std::to_string(file_size) + "-byte file");
   std::vector<uint8_t> out((size_t)n);
   in.clear();
   in.seekg((std::streamoff)(tensor_data_offset + ti.offset));

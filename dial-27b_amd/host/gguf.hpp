@@ -99,6 +99,7 @@ struct Content {
   std::map<std::string, Value> metadata;
   std::map<std::string, TensorInfo> tensor_infos;
   uint64_t tensor_data_offset = 0;
+  uint64_t file_size = 0;
 
   // Parses header, metadata and tensor infos from the start of `in`.
   // `file_size` bounds every length read from the file.

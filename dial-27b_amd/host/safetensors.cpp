@@ -254,6 +254,7 @@ Header read_header(const std::string &path) {
     int64_t elems = 1;
     for (const Json &d : sh->arr) {
       if (d.kind != Json::Num || d.num < 0) fail(path + ": bad shape for tensor " + kv.first);
+      if (d.num != 0 && elems > ((int64_t)1 << 50) / d.num) fail(path + ": tensor " + kv.first + " has too many elements");
       ti.shape.push_back(d.num);
       elems *= d.num;
     }

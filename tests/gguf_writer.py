@@ -55,20 +55,22 @@ def tensor_nbytes(ggml: str, dims) -> int:
 
 
 def write_gguf(path, metadata, tensors, version: int = 3, alignment: int = 32,
-               nul_strings: bool = False, ggml_type_ids=None, truncate: int = 0) -> int:
+               nul_strings: bool = False, ggml_type_ids=None, truncate: int = 0,
+               check_sizes: bool = True) -> int:
     """metadata: [(key, value type name, value)] (ARRAY values are
     (element type name, [items])); tensors: [(name, ggml type name, dims in
     candle order [outer, ..., contiguous], raw bytes)].  A general.alignment
     entry in `metadata` must agree with `alignment`.  ggml_type_ids overrides
     the type id written per tensor name; truncate drops that many bytes from
-    the end.  Returns the data start offset."""
+    the end; check_sizes=False writes tensor infos whose bytes do not match
+    their dims (for reader error tests).  Returns the data start offset."""
     head = b"GGUF" + struct.pack("<I", version) + _len(len(tensors), version) + _len(len(metadata), version)
     body = b""
     for key, vtype, value in metadata:
         body += _str(key, version, nul_strings) + struct.pack("<I", VT[vtype]) + _value(vtype, value, version, nul_strings)
     offsets, off = [], 0
     for name, ggml, dims, raw in tensors:
-        assert len(raw) == tensor_nbytes(ggml, dims), (name, len(raw))
+        assert not check_sizes or len(raw) == tensor_nbytes(ggml, dims), (name, len(raw))
         offsets.append(off)
         off += len(raw)
         off = (off + alignment - 1) // alignment * alignment

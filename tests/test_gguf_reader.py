@@ -110,6 +110,17 @@ def test_reader_errors(tmp_path):
     _tiny(p, tensors=[("x.weight", "Q8_0", [2, 32], bytes(68))])
     with pytest.raises(H.DialError, match="cannot find tensor info for y.weight"):
         H.gguf_tensor_bytes(str(p), "y.weight")
+    # sizes come from the file: element counts that overflow and alignments
+    # that cannot be honoured are refused before anything is allocated
+    _tiny(p, tensors=[("x.weight", "F32", [2 ** 30, 2 ** 30], b"")], check_sizes=False)
+    with pytest.raises(H.DialError, match="too many elements"):
+        H.gguf_read(str(p))
+    _tiny(p, tensors=[("x.weight", "F32", [2 ** 20, 64], b"")], check_sizes=False)
+    with pytest.raises(H.DialError, match="truncated GGUF tensor x.weight"):
+        H.gguf_tensor_bytes(str(p), "x.weight")
+    _tiny(p, tensors=[], extra_meta=[("general.alignment", "U32", 0)])
+    with pytest.raises(H.DialError, match="invalid general.alignment 0"):
+        H.gguf_read(str(p))
 
 
 def _configure(path, **kw):

@@ -113,3 +113,8 @@ def test_malformed_files_are_rejected(tmp_path):
     p.write_bytes(struct.pack("<Q", 1 << 40) + b"{}")
     with pytest.raises(H.DialError, match="header length"):
         H.safetensors_read_header(str(p))
+    # a shape whose element count overflows is refused, not wrapped round
+    hdr = json.dumps({"w": {"dtype": "F32", "shape": [2 ** 40, 2 ** 40, 16], "data_offsets": [0, 0]}}).encode()
+    p.write_bytes(struct.pack("<Q", len(hdr)) + hdr)
+    with pytest.raises(H.DialError, match="too many elements"):
+        H.safetensors_read_header(str(p))
