@@ -268,8 +268,9 @@ void ensure_native_scratch(Linear *L, size_t part_bytes, size_t cnt_count, hipSt
 }
 
 void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, int y_dtype, int path,
-                 hipStream_t st) {
+                 hipStream_t st, bool swiglu = false) {
   WeightView w = L->view();
+  if (swiglu) w.pair = L->desc.out_dim / 32;  // gate / up halves of out_dim / 2 rows, 16 rows per strip
   const int fmt = L->desc.format;
   if (path == DIALQ_PATH_AUTO) {
     if (rows <= 64) path = DIALQ_PATH_GEMV;
@@ -327,15 +328,18 @@ void check_ptr_align(const void *p, const char *what) {
 }
 
 void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void *y, int32_t y_dtype,
-                  int32_t path, void *stream, int device_io, bool local_q8) {
+                  int32_t path, void *stream, int device_io, bool local_q8, bool swiglu = false) {
   if (!L) fail("linear handle is NULL");
   if (rows < 0) fail("rows must be >= 0, got %lld", (long long)rows);
   size_t xs = dtype_size(x_dtype), ys = dtype_size(y_dtype);
+  if (swiglu && L->desc.out_dim % 128 != 0)
+    fail("SwiGLU forward needs a fused gate_up weight whose out_dim (%lld) is a multiple of 128: gate and up "
+         "halves of a multiple of 64 rows", (long long)L->desc.out_dim);
   if (rows == 0) return;
   if (!x || !y) fail("x and y must not be NULL");
   DeviceGuard dg(L->device);
   hipStream_t st = (hipStream_t)stream;
-  const int64_t N = L->desc.out_dim, K = L->desc.in_dim;
+  const int64_t N = swiglu ? L->desc.out_dim / 2 : L->desc.out_dim, K = L->desc.in_dim;
   size_t xbytes = (size_t)(rows * K) * xs, ybytes = (size_t)(rows * N) * ys;
   DevBuf dx, dy;
   const void *xp = x;
@@ -357,7 +361,7 @@ void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void 
     ensure_scratch(L, (size_t)((k_pad + 255) / 256 * 256 + 256));
     hip_check(launch_local_q8(L->view(), xp, x_dtype, yp, y_dtype, L->scratch.p, st), "local q8 launch");
   } else {
-    run_forward(L, xp, x_dtype, rows, yp, y_dtype, path, st);
+    run_forward(L, xp, x_dtype, rows, yp, y_dtype, path, st, swiglu);
   }
   if (!device_io) {
     hip_check(hipMemcpyAsync(y, yp, ybytes, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
@@ -534,6 +538,14 @@ int dialq_linear_forward_ex(void *linear, const void *x, int32_t x_dtype, int64_
                             size_t error_size) {
   return guarded(error, error_size, [&] {
     forward_impl((Linear *)linear, x, x_dtype, rows, y, y_dtype, path, stream, device_io, false);
+  });
+}
+
+int dialq_linear_forward_swiglu(void *linear, const void *x, int32_t x_dtype, int64_t rows, void *y,
+                                int32_t y_dtype, int32_t path, void *stream, int device_io, char *error,
+                                size_t error_size) {
+  return guarded(error, error_size, [&] {
+    forward_impl((Linear *)linear, x, x_dtype, rows, y, y_dtype, path, stream, device_io, false, true);
   });
 }
 

@@ -115,6 +115,36 @@ __device__ __forceinline__ void tile_of(int b, int G, int nt, int mt, int &tm, i
   tile_coords(xcd_rank(b, G), nt, mt, tm, tn);
 }
 
+// SwiGLU epilogue (w.pair > 0, fused gate_up weight with gate rows [0, I)
+// and up rows [I, 2I), I = 16 * pair).  A column tile of SW strips covers
+// output columns of SW/2 strips: waves 0-1 multiply gate strips
+// j0 .. j0 + SW/2 - 1 and waves 2-3 the up strips pair + j0 .. of the same
+// outputs, with identical register layouts, so an up wave's value v of lane
+// l belongs to the gate wave (wave - 2)'s value v of lane l.  Each wave owns
+// SW/4 consecutive strips; `ps0` is its first physical strip and strips at
+// or past `slim` read zeros.
+template <int SW>
+__device__ __forceinline__ void swiglu_strips(const WeightView &w, int tn, int wave, int &ps0, int &slim, int &j0) {
+  const int pair = (int)w.pair;
+  j0 = tn * (SW / 2) + (wave & 1) * (SW / 4);
+  ps0 = wave < 2 ? j0 : pair + j0;
+  slim = wave < 2 ? pair : 2 * pair;
+}
+
+// Hand 16 values per lane from the up waves (2, 3) to the gate waves (0, 1)
+// through LDS (8 KB at `xch`).  Every wave calls it; the first barrier also
+// ends the k loop's reads of the staging buffers.
+__device__ __forceinline__ void swiglu_exchange(float *xch, int wave, int lane, const float (&up)[16], float (&got)[16]) {
+  __syncthreads();
+  if (wave >= 2)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) xch[((wave - 2) * 16 + v) * 64 + lane] = up[v];
+  __syncthreads();
+  if (wave < 2)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) got[v] = xch[(wave * 16 + v) * 64 + lane];
+}
+
 // Weight-only prefill GEMM.  A 256-thread workgroup computes a
 // (16*MS) x (64*NS) tile of y; wave v owns strips s0 + v*NS .. + NS-1.
 // The k loop runs in stages of KS chunks, software-pipelined:
@@ -126,7 +156,7 @@ __device__ __forceinline__ void tile_of(int b, int G, int nt, int mt, int &tm, i
 //     refilled with stage t+2 right after each tile has been multiplied.
 // All global reads are buffer loads; out-of-range rows, k and strips read
 // zeros, so no load is conditional.
-template <int FMT, int ACT, int MS, int NS>
+template <int FMT, int ACT, int MS, int NS, bool SWI>
 __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   typedef GemmShape<FMT, ACT> S;
   typedef FmtTraits<FMT> T;
@@ -137,10 +167,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, r = lane & 15;
   int tm, tn;
-  tile_of(blockIdx.x, gridDim.x, (int)((w.n_strips + 4 * NS - 1) / (4 * NS)), (int)((p.M + S::ROWS - 1) / S::ROWS), tm,
-          tn);
+  const int nt = SWI ? (int)((w.pair + 2 * NS - 1) / (2 * NS)) : (int)((w.n_strips + 4 * NS - 1) / (4 * NS));
+  tile_of(blockIdx.x, gridDim.x, nt, (int)((p.M + S::ROWS - 1) / S::ROWS), tm, tn);
   const int m0 = tm * S::ROWS;
-  const int s0 = tn * (4 * NS) + wave * NS;
+  int s0 = tn * (4 * NS) + wave * NS, slim = (int)w.n_strips, j0 = 0;
+  if constexpr (SWI) swiglu_strips<4 * NS>(w, tn, wave, s0, slim, j0);
   const int kc = (int)w.k_chunks;
   const int K = (int)w.K;
   const int nstage = (kc + KS - 1) / KS;
@@ -195,7 +226,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 #pragma unroll
       for (int n = 0; n < NS; ++n) {
         const int c = st * KS + j, sn = s0 + n;
-        const bool valid = st < nstage && c < kc && sn < w.n_strips;
+        const bool valid = st < nstage && c < kc && sn < slim;
         slot[j][n] = gemm_tile<FMT>(w, rt, ra, valid ? sn : 0, valid ? c : 0, valid, lane);
       }
   };
@@ -228,7 +259,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 #pragma unroll
       for (int n = 0; n < NS; ++n) {
         const int c = (st + 2) * KS + j, sn = s0 + n;
-        const bool valid = st + 2 < nstage && c < kc && sn < w.n_strips;
+        const bool valid = st + 2 < nstage && c < kc && sn < slim;
         slot[j][n] = gemm_tile<FMT>(w, rt, ra, valid ? sn : 0, valid ? c : 0, valid, lane);
       }
       if constexpr (FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW || FMT == DIALQ_FORMAT_NVFP4 ||
@@ -270,6 +301,37 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   if (st < nstage) stage(wb[0], st);
 
   // lane (g, r) holds rows 16ms + 4g + i of column 16(s0 + n) + r
+  if constexpr (SWI) {
+    // y[m, j] = silu(gate) * up; the NS tiles of one 16-row group per exchange
+    static_assert(NS * 4 <= 16, "one exchange holds 16 values per lane");
+    const int64_t I = w.pair * 16;
+    float *xch = (float *)lds;
+    float scale[NS];
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      const int64_t col = (int64_t)(s0 + n) * 16 + r;
+      scale[n] = col < w.N ? epilogue_scale<FMT>(w, col) : 0.0f;
+    }
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) {
+      float mine[16], up[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mine[v] = v < NS * 4 ? acc[ms][v / 4][v % 4] * scale[v / 4] : 0.0f;
+      swiglu_exchange(xch, wave, lane, mine, up);
+      if (wave < 2) {
+        const int64_t rb = m0 + ms * 16 + g * 4;
+#pragma unroll
+        for (int n = 0; n < NS; ++n) {
+          const int64_t j = (int64_t)(j0 + n) * 16 + r;
+          if (j >= I) continue;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (rb + i < p.M) store_out(p.y, (rb + i) * I + j, p.y_dtype, silu_mul(mine[n * 4 + i], up[n * 4 + i]));
+        }
+      }
+    }
+    return;
+  }
   const bool full = m0 + S::ROWS <= p.M;
   auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
     typedef decltype(yd) Y;
@@ -316,7 +378,7 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
                                                  0, 0);
 }
 
-template <int FMT, int ACT, int MT, int KS, int OCC>
+template <int FMT, int ACT, int MT, int KS, int OCC, bool SWI>
 __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   constexpr int CHUNK = 64, SK = KS * CHUNK, STEPS = SK / 16;
   constexpr int PARTS = ActTraits<ACT>::PARTS, BY = ActTraits<ACT>::BYTES;
@@ -328,9 +390,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
   int tm, tn;
-  tile_of(blockIdx.x, gridDim.x, (int)((w.n_strips + 15) / 16), (int)((p.M + ROWS - 1) / ROWS), tm, tn);
+  const int nt = SWI ? (int)((w.pair + 7) / 8) : (int)((w.n_strips + 15) / 16);
+  tile_of(blockIdx.x, gridDim.x, nt, (int)((p.M + ROWS - 1) / ROWS), tm, tn);
   const int m0 = tm * ROWS;
-  const int s0 = tn * 16 + wave * 4;
+  int s0 = tn * 16 + wave * 4, slim = (int)w.n_strips, j0 = 0;
+  if constexpr (SWI) swiglu_strips<16>(w, tn, wave, s0, slim, j0);
   const int kc = (int)w.k_chunks, K = (int)w.K;
   const int nstage = (kc + KS - 1) / KS;
   const int64_t total = w.n_strips * w.k_chunks;
@@ -361,7 +425,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   auto bload = [&](int st, int j, int q) -> u32x2 {
     const int c = st * KS + j / 4, strip = s0 + 2 * q + sub;
-    const bool valid = st < nstage && c < kc && strip < w.n_strips;
+    const bool valid = st < nstage && c < kc && strip < slim;
     const uint32_t off = valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * 1024u +
                                      (uint32_t)(((j % 4) * 16 + r) * 16 + 8 * h)
                                : kOOB;
@@ -429,6 +493,33 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   }
   if (st < nstage) stage(wb[0], st);
 
+  if constexpr (SWI) {
+    // y[m, j] = silu(gate) * up, one 32x32 tile per exchange
+    const int64_t I = w.pair * 16;
+    float *xch = (float *)lds;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);  // weight row of this lane
+      const int64_t j = (int64_t)(j0 + 2 * q) * 16 + (lane & 31);     // output column
+      const float scale = col < w.N ? w.row_scale[col] : 0.0f;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float mine[16], up[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mine[v] = acc[mt][q][v] * scale;
+        swiglu_exchange(xch, wave, lane, mine, up);
+        if (wave < 2 && j < I) {
+          const int64_t rb = m0 + mt * 32 + 4 * h;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int64_t row = rb + 8 * (v / 4) + (v % 4);
+            if (row < p.M) store_out(p.y, row * I + j, p.y_dtype, silu_mul(mine[v], up[v]));
+          }
+        }
+      }
+    }
+    return;
+  }
   const bool full = m0 + ROWS <= p.M;
   auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
     typedef decltype(yd) Y;
@@ -465,15 +556,21 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
     if (w.n_strips * w.k_chunks * 1024 <= 0xffffffffLL) {
       constexpr int MT = GEMM32_MT, KS = GEMM32_KS, ROWS = 32 * MT;
       constexpr int BUF = ActTraits<ACT>::PARTS * ROWS * (KS * 64 + 8);
-      dim3 grid((unsigned)(((w.n_strips + 15) / 16) * ((M + ROWS - 1) / ROWS)));
+      static_assert(2 * BUF * 2 >= 8192, "the SwiGLU exchange reuses the staging LDS");
+      const int64_t nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
+      dim3 grid((unsigned)(nt * ((M + ROWS - 1) / ROWS)));
       GemmParams p{w, x, y, M, y_dtype};
-      k_gemm32<FMT, ACT, MT, KS, GEMM32_OCC><<<grid, 256, 2 * BUF * 2, st>>>(p);
+      if (w.pair) k_gemm32<FMT, ACT, MT, KS, GEMM32_OCC, true><<<grid, 256, 2 * BUF * 2, st>>>(p);
+      else k_gemm32<FMT, ACT, MT, KS, GEMM32_OCC, false><<<grid, 256, 2 * BUF * 2, st>>>(p);
       return hipGetLastError();
     }
   }
-  dim3 grid((unsigned)(((w.n_strips + 4 * S::NS - 1) / (4 * S::NS)) * ((M + S::ROWS - 1) / S::ROWS)));
+  static_assert(S::LDS_BYTES >= 8192, "the SwiGLU exchange reuses the staging LDS");
+  const int64_t nt = w.pair ? (w.pair + 2 * S::NS - 1) / (2 * S::NS) : (w.n_strips + 4 * S::NS - 1) / (4 * S::NS);
+  dim3 grid((unsigned)(nt * ((M + S::ROWS - 1) / S::ROWS)));
   GemmParams p{w, x, y, M, y_dtype};
-  k_gemm<FMT, ACT, S::MS, S::NS><<<grid, 256, S::LDS_BYTES, st>>>(p);
+  if (w.pair) k_gemm<FMT, ACT, S::MS, S::NS, true><<<grid, 256, S::LDS_BYTES, st>>>(p);
+  else k_gemm<FMT, ACT, S::MS, S::NS, false><<<grid, 256, S::LDS_BYTES, st>>>(p);
   return hipGetLastError();
 }
 
@@ -580,7 +677,7 @@ constexpr int kNativeAcc = 64;       // f32 accumulators per thread (MT = 2: 2 x
 // at 27B shapes are faster unsplit, the 136-chunk down projection split).
 constexpr int native_min_chunks(int fmt) { return fmt == DIALQ_FORMAT_FP8_BLOCK ? 8 : 32; }
 
-template <int FMT, int MT, int OCC, int DEPTH>
+template <int FMT, int MT, int OCC, int DEPTH, bool SWI>
 __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
   constexpr bool FP8 = FMT == DIALQ_FORMAT_FP8_BLOCK;
   constexpr int ROWB = FP8 ? 128 : 64;  // activation code bytes per row and chunk
@@ -600,7 +697,8 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
   const int kc = (int)w.k_chunks;
-  const int nt = (int)((w.n_strips + 15) / 16), mtiles = (int)((p.M + ROWS - 1) / ROWS);
+  const int nt = SWI ? (int)((w.pair + 7) / 8) : (int)((w.n_strips + 15) / 16);
+  const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
   // One workgroup per (tile, k piece).  P == 1: whole tiles in the
   // XCD-aware order of tile_of.  P > 1: each tile's chunks split evenly into
   // P pieces; units go (column tile, piece, row block) over XCD-contiguous
@@ -624,7 +722,8 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
   if constexpr (!FP8) rb = make_rsrc(w.aux, (uint32_t)(w.n_strips * w.k_chunks * 64));
   {
     const int m0 = tm * ROWS;
-    const int s0 = tn * 16 + wave * 4;
+    int s0 = tn * 16 + wave * 4, slim = (int)w.n_strips, j0 = 0;
+    if constexpr (SWI) swiglu_strips<16>(w, tn, wave, s0, slim, j0);
     const int mrows = (int)((p.M - m0) < ROWS ? (p.M - m0) : ROWS);
     const rsrc_t rx = make_rsrc(p.xq + (int64_t)m0 * pitch, (uint32_t)mrows * pitch);
     rsrc_t rs = rx;
@@ -658,7 +757,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
     // that read it, so the ring keeps its registers across the loop.
     auto bload = [&](int c, int j, int q, int i) -> u32x4 {
       const int strip = s0 + 2 * q + sub;
-      const bool valid = c < c1 && strip < w.n_strips;
+      const bool valid = c < c1 && strip < slim;
       const uint32_t off = valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * TILE +
                                        (uint32_t)(((2 * j + h) * 16 + r) * (16 * BW) + 16 * i)
                                  : kOOB;
@@ -666,7 +765,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
     };
     auto sbload = [&](int c, int q) -> uint32_t {  // MXFP4 weight scales of row r, k blocks 0..3
       const int strip = s0 + 2 * q + sub;
-      const bool valid = c < c1 && strip < w.n_strips;
+      const bool valid = c < c1 && strip < slim;
       return bload4(rb, valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * 64u + (uint32_t)(r * 4) : kOOB);
     };
     i32x8 wb[DEPTH][2][2];
@@ -676,7 +775,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
     uint32_t wsv[DEPTH];
     rsrc_t rw = rx;
     if constexpr (FP8) {
-      const int sb = s0 < w.n_strips ? s0 : (int)w.n_strips - 1;
+      const int sb = s0 < slim ? s0 : slim - 1;
       rw = make_rsrc(w.block_scale + (int64_t)(sb / 8) * w.nbk, (uint32_t)(kc * 4));
     }
     auto wsload = [&](int c) -> uint32_t { return bload4(rw, c < c1 ? (uint32_t)(c * 4) : kOOB); };
@@ -888,6 +987,31 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
         for (int e = 0; e < 16; ++e)
           rowf[mt][e] = __builtin_bit_cast(float, bload4(rxs, (uint32_t)(mt * 32 + 8 * (e / 4) + 4 * h + (e % 4)) * 4u));
     }
+    if constexpr (SWI) {
+      // y[m, j] = silu(gate) * up, one 32x32 tile per exchange
+      const int64_t I = w.pair * 16;
+      float *xch = (float *)lds;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int64_t j = (int64_t)(j0 + 2 * q) * 16 + (lane & 31);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          float mine[16], up[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mine[e] = sum[(mt * 2 + q) * 16 + e] * rowf[mt][e];
+          swiglu_exchange(xch, wave, lane, mine, up);
+          if (wave < 2 && j < I) {
+            const int64_t rbase = m0 + mt * 32 + 4 * h;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int64_t row = rbase + 8 * (e / 4) + (e % 4);
+              if (row < p.M) store_out(p.y, row * I + j, p.y_dtype, silu_mul(mine[e], up[e]));
+            }
+          }
+        }
+      }
+      return;
+    }
     const bool full = m0 + ROWS <= p.M;
     auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
       typedef decltype(yd) Y;
@@ -936,20 +1060,25 @@ static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const vo
   // 32-bit buffer offsets, with 0x80000000 reserved as the out-of-range offset
   if (w.n_strips * w.k_chunks * TILE >= ((int64_t)1 << 31) || ROWS * pitch >= ((int64_t)1 << 31))
     return hipErrorInvalidValue;
-  const int64_t tiles = ((w.n_strips + 15) / 16) * ((M + ROWS - 1) / ROWS);
+  static_assert(2 * ROWS * ((FMT == DIALQ_FORMAT_FP8_BLOCK ? 128 : 64) + 16) >= 8192,
+                "the SwiGLU exchange reuses the staging LDS");
+  const int64_t nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
+  const int64_t tiles = nt * ((M + ROWS - 1) / ROWS);
   const int P = native_pieces(FMT, OCC, tiles, w.k_chunks);
   if (tiles * P > 0x7fffffffLL) return hipErrorInvalidValue;
   if (P > 1 && ((size_t)tiles > cnt_count || (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) > part_bytes))
     return hipErrorInvalidValue;
   NativeParams p{w, xq, xs, M, k_pad, y, y_dtype, P, part, cnt};
-  k_gemm_native<FMT, MT, OCC, DEPTH><<<dim3((unsigned)(tiles * P)), 256, 0, st>>>(p);
+  if (w.pair) k_gemm_native<FMT, MT, OCC, DEPTH, true><<<dim3((unsigned)(tiles * P)), 256, 0, st>>>(p);
+  else k_gemm_native<FMT, MT, OCC, DEPTH, false><<<dim3((unsigned)(tiles * P)), 256, 0, st>>>(p);
   return hipGetLastError();
 }
 
 void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count) {
   const int occ = w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4;
   const int rows = 32 * (w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
-  const int64_t tiles = ((w.n_strips + 15) / 16) * ((M + rows - 1) / rows);
+  const int64_t nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
+  const int64_t tiles = nt * ((M + rows - 1) / rows);
   const int P = native_pieces(w.fmt, occ, tiles, w.k_chunks);
   part_bytes = P > 1 ? (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) : 0;
   cnt_count = P > 1 ? (size_t)tiles : 0;

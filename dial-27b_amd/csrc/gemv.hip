@@ -478,6 +478,10 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
   }
   const int s_first = lo / kc;
   const int nseg = (hi > lo) ? (hi - 1) / kc - s_first + 1 : 0;
+  // SwiGLU epilogue (w.pair > 0): the tile ranges run over virtual strips,
+  // 2j = gate strip j and 2j+1 = up strip pair + j, two per workgroup.
+  const int pair = (int)w.pair;
+  auto phys = [&](int vs) -> int { return pair ? ((vs & 1) ? pair + (vs >> 1) : (vs >> 1)) : vs; };
   const int mrows = (int)((p.M - p.m_base) < 16 ? (p.M - p.m_base) : 16);
   const int slot_floats = mrows * 16;
 
@@ -533,7 +537,7 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const bool valid = t < hi;
-    Pol::fill(ring[u], w, cx, s, c, valid, lane);
+    Pol::fill(ring[u], w, cx, phys(s), c, valid, lane);
     slot_s[u] = valid ? s : -1;
     t += W;
     c += W;
@@ -562,7 +566,7 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
         Pol::compute(ring[u], acc, cx);
       }
       const bool valid = t < hi;
-      Pol::fill(ring[u], w, cx, s, c, valid, lane);
+      Pol::fill(ring[u], w, cx, phys(s), c, valid, lane);
       slot_s[u] = valid ? s : -1;
       t += W;
       c += W;
@@ -574,6 +578,28 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
   }
   if (cur >= 0) park<Pol, W>(part, cur - s_first, wave, mrows, acc);
   lds_barrier();
+
+  if (pair) {
+    // whole gate / up strip pair j (segments 0 and 1): wave 0 writes
+    // silu(gate) * up for rows j*16 .. j*16+15 of the [M, 16*pair] output
+    if (wave == 0 && nseg == 2) {
+      const int r = lane & 15;
+      const int64_t ng = (int64_t)(s_first >> 1) * 16 + r, nu = ng + (int64_t)pair * 16;
+      const float sg = epilogue_scale<FMT>(w, ng), su = epilogue_scale<FMT>(w, nu);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = lane + 64 * q, m = e >> 4;
+        if (e >= slot_floats) continue;
+        float gs = 0.0f, us = 0.0f;
+        for (int ww = 0; ww < W; ++ww) {
+          gs += part[(size_t)ww * slot_floats + e];
+          us += part[(size_t)(W + ww) * slot_floats + e];
+        }
+        store_out(p.y, (p.m_base + m) * ((int64_t)pair * 16) + ng, p.y_dtype, silu_mul(gs * sg, us * su));
+      }
+    }
+    return;
+  }
 
   // finish: wave j % W takes strip j of the range
   const int r = lane & 15;
@@ -1045,7 +1071,7 @@ template <int FMT, typename Pol, int U, bool XL, int WV>
 static hipError_t launch_ranges(GemvParams &p, hipStream_t st) {
   const int64_t mrows = (p.M - p.m_base) < 16 ? (p.M - p.m_base) : 16;
   const int64_t total = p.w.n_strips * p.w.k_chunks;
-  p.spw = gemv_spw(p.w, mrows, XL);
+  p.spw = p.w.pair ? 2 : gemv_spw(p.w, mrows, XL);  // SwiGLU: whole gate / up strip pairs
   p.G = p.spw > 0 ? (int)((p.w.n_strips + p.spw - 1) / p.spw) : gemv_grid(p.w, mrows);
   const int64_t per = p.spw > 0 ? p.spw * p.w.k_chunks : (total + p.G - 1) / p.G;
   const int64_t nseg = p.spw > 0 ? p.spw : per / p.w.k_chunks + 2;
@@ -1086,6 +1112,20 @@ static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
   constexpr int BY = ActTraits<ACT>::BYTES;
   const bool xl = mrows * stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) + 32 <= kGemvStageBytes;
   constexpr int UR = U_XL < kRangeRing ? U_XL : kRangeRing;
+  if (d.w.pair) {
+    // SwiGLU epilogue: one gate / up strip pair per workgroup, never split
+    // (the pair's two sums meet in the workgroup's parking LDS)
+    GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
+    const bool small = d.w.pair < device_cus();
+    const int pitch = stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK);
+    if (mrows * pitch + 32 <= (small ? kGemvSmallStageBytes : kGemvStageBytes)) {
+      p.x_pitch = pitch;
+      if (small) return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvSmallWaves>(p, st);
+      return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvWaves>(p, st);
+    }
+    return launch_ranges<FMT, PolT<A, ACT, false, false>, (U_X < kRangeRing ? U_X : kRangeRing), false, kGemvWaves>(
+        p, st);
+  }
   if (d.w.n_strips >= device_cus()) {
     GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
     p.x_pitch = xl ? stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) : 0;

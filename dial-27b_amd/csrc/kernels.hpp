@@ -30,6 +30,11 @@ struct WeightView {
   const float *row_scale;    // W8A16, FP8_ROW: [n_strips*16]
   const float *block_scale;  // FP8_BLOCK: [ceil(N/128), nbk]
   float global;              // NVFP4 multiplier (1 otherwise)
+  // 0: y = x W^T.  > 0: W is a fused gate_up weight whose rows [0, I) are
+  // the gate and [I, 2I) the up projection, I = 16 * pair, and the product
+  // writes y[m, j] = silu(gate[m, j]) * up[m, j], j < I (the MLP's
+  // mlp_mid_from_gate_up, qwen3_vl/text.rs:816-820).
+  int64_t pair = 0;
 };
 
 hipError_t launch_quantize(int fmt, const void *dense, int dtype, int64_t N, int64_t K, void *raw_w,

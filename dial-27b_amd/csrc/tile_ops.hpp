@@ -511,6 +511,10 @@ __device__ __forceinline__ void with_y_dtype(int y_dtype, F &&body) {
   else body(YDtype<DIALQ_F32>{});
 }
 
+// silu(g) * u in f32, silu(g) = g / (1 + exp(-g)) (candle_nn::ops::silu),
+// from the unrounded gate and up sums; one rounding at the store.
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 template <int FMT>
 __device__ __forceinline__ float epilogue_scale(const WeightView &w, int64_t n) {
   if constexpr (FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW) return w.row_scale[n];

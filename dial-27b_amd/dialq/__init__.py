@@ -69,6 +69,7 @@ def _load():
         "dialq_linear_forward_ex": (C.c_int, [P, P, I32, I64, P, I32, I32, P, C.c_int, CH, SZ]),
         "dialq_linear_dequantize": (C.c_int, [P, P, I32, P, C.c_int, CH, SZ]),
         "dialq_linear_export": (C.c_int, [P, P, SZ, P, SZ, CH, SZ]),
+        "dialq_linear_forward_swiglu": (C.c_int, [P, P, I32, I64, P, I32, I32, P, C.c_int, CH, SZ]),
         "dialq_local_q8_forward": (C.c_int, [P, P, I32, I64, P, I32, P, C.c_int, CH, SZ]),
     }
     for name, (res, args) in sigs.items():
@@ -223,6 +224,20 @@ class Linear:
         err = _err()
         rc = lib.dialq_linear_forward_ex(self.h, _ptr(x), xd, rows, _ptr(y), yd, path,
                                          _stream_ptr(stream), int(dev), err, 512)
+        _check(rc, err)
+        return y
+
+    def forward_swiglu(self, x, y, rows=None, *, path=PATH_AUTO, stream=None, x_dtype=None, y_dtype=None):
+        """y[:, j] = silu(x W[j]^T) * (x W[N/2 + j]^T) for a fused gate_up
+        weight (gate rows first); y has out_dim / 2 columns."""
+        dev = _is_torch(x)
+        if rows is None:
+            rows = (x.numel() if dev else np.asarray(x).size) // self.in_dim
+        xd = dtype_code(x) if x_dtype is None else x_dtype
+        yd = dtype_code(y) if y_dtype is None else y_dtype
+        err = _err()
+        rc = lib.dialq_linear_forward_swiglu(self.h, _ptr(x), xd, rows, _ptr(y), yd, path,
+                                             _stream_ptr(stream), int(dev), err, 512)
         _check(rc, err)
         return y
 

@@ -154,6 +154,20 @@ int dialq_linear_forward_ex(void *linear, const void *x, int32_t x_dtype,
                             int32_t path, void *stream, int device_io,
                             char *error, size_t error_size);
 
+/* Fused gate_up projection with the SwiGLU epilogue: for a weight whose rows
+ * [0, N/2) are the MLP's gate and [N/2, N) its up projection (the
+ * MlpGateUpProjection::Fused weight, qwen3_vl/text.rs:424-469),
+ *   y[m, j] = silu(g[m, j]) * u[m, j],  g = x W[0:N/2]^T,  u = x W[N/2:N]^T,
+ * silu(g) = g / (1 + exp(-g)), computed in f32 from the unrounded products
+ * and rounded once to y_dtype.  Replaces gate_up_proj.forward followed by
+ * Mlp::mlp_mid_from_gate_up (qwen3_vl/text.rs:816-820: narrow, silu, mul).
+ *   y: [rows, N/2] of y_dtype.  N must be a multiple of 128.
+ * Paths and the other arguments as dialq_linear_forward_ex. */
+int dialq_linear_forward_swiglu(void *linear, const void *x, int32_t x_dtype,
+                                int64_t rows, void *y, int32_t y_dtype,
+                                int32_t path, void *stream, int device_io,
+                                char *error, size_t error_size);
+
 /* Dequantize the resident weight into a dense [N,K] matrix of out_dtype
  * (F32, F16 or BF16, each rounded once to nearest-even from the exact f32
  * value).  Replaces QMatMul::dequantize_f16 (worker_w8a16.rs:125, used by

@@ -288,6 +288,21 @@ def matmul_f64(x, w):
     return y
 
 
+def swiglu(gate_up):
+    """Mlp::mlp_mid_from_gate_up (qwen3_vl/text.rs:816-820): the fused gate_up
+    output's first half is the gate, its second half the up projection;
+    returns silu(gate) * up with silu(g) = g / (1 + exp(-g))
+    (candle_nn::ops::silu), in float64.  Pinned by known answers and by the
+    identity silu(g) - silu(-g) = g (tests/test_oracle_formats.py)."""
+    y = np.asarray(gate_up, np.float64)
+    n = y.shape[-1]
+    if n % 2:
+        raise ValueError(f"gate_up width {n} is odd")
+    g, u = y[..., : n // 2], y[..., n // 2:]
+    with np.errstate(over="ignore"):
+        return g / (1.0 + np.exp(-g)) * u
+
+
 def w8a16_linear(x, q, scale):
     x = _f32(x)
     q = np.ascontiguousarray(q, np.int8)

@@ -256,6 +256,33 @@ def test_matmul_oracle_matches_numpy(O):
     assert y.shape == (3, 7)
 
 
+def test_swiglu_oracle_known_answers(O):
+    """silu(g) = g * sigmoid(g): known values, the odd-part identity
+    silu(g) - silu(-g) = g (a sign slip in the exponent breaks it), torch's
+    own silu, and the gate / up halves (swapping them changes the answer)."""
+    g = np.array([0.0, 1.0, -1.0, 20.0, -100.0, 3.5, -0.25])
+    u = np.ones_like(g)
+    y = O.swiglu(np.concatenate([g, u])[None, :])[0]
+    want = np.array([0.0, 0.7310585786300049, -0.2689414213699951, 20.0 / (1.0 + np.exp(-20.0)),
+                     -100.0 * np.exp(-100.0) / (1.0 + np.exp(-100.0)), 3.5 / (1.0 + np.exp(-3.5)),
+                     -0.25 / (1.0 + np.exp(0.25))])
+    assert np.allclose(y, want, rtol=1e-15, atol=0)
+    rng = np.random.default_rng(12)
+    gg = rng.normal(0, 4, (3, 64))
+    ones = np.ones_like(gg)
+    pos = O.swiglu(np.concatenate([gg, ones], 1))
+    neg = O.swiglu(np.concatenate([-gg, ones], 1))
+    assert np.allclose(pos - neg, gg, rtol=0, atol=1e-12)
+    ref = torch.nn.functional.silu(torch.from_numpy(gg)).numpy()
+    assert np.allclose(pos, ref, rtol=1e-12, atol=1e-15)
+    uu = rng.normal(size=gg.shape)
+    y = O.swiglu(np.concatenate([gg, uu], 1))
+    assert np.allclose(y, ref * uu, rtol=1e-12, atol=1e-15)
+    assert not np.allclose(y, O.swiglu(np.concatenate([uu, gg], 1)))
+    with pytest.raises(ValueError):
+        O.swiglu(np.zeros((1, 3)))
+
+
 def test_w8a16_linear_oracle(O):
     rng = np.random.default_rng(8)
     w = rng.normal(0, 0.02, (9, 64)).astype(np.float32)
