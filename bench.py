@@ -115,21 +115,35 @@ def layer_bytes(dq, fmt, shapes=LAYER_27B):
     return sum(dq.raw_weight_bytes(fmt, n, k) for _, n, k in shapes)
 
 
-def decode_pass(dq, lins, xs, ys, stream):
-    for lin, x, y in zip(lins, xs, ys):
-        lin.forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+def out_cols(name, n, swiglu):
+    """Output width of a linear: half the rows when the fused gate_up runs
+    with the SwiGLU epilogue (silu(gate) * up)."""
+    return n // 2 if name in swiglu else n
 
 
-def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B):
+def run_linear(lin, name, x, y, swiglu, **kw):
+    if name in swiglu:
+        lin.forward_swiglu(x, y, **kw)
+    else:
+        lin.forward(x, y, **kw)
+
+
+def decode_pass(dq, lins, xs, ys, stream, shapes=LAYER_27B, swiglu=()):
+    for lin, x, y, (name, _, _) in zip(lins, xs, ys, shapes):
+        run_linear(lin, name, x, y, swiglu, rows=1, path=dq.PATH_GEMV, stream=stream)
+
+
+def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B, swiglu=()):
     """Wall time of `steps` decode passes, one HIP-graph replay per pass,
-    rotating layer copies."""
+    rotating layer copies.  Linears named in `swiglu` (a fused gate_up) run
+    with the SwiGLU epilogue."""
     xs = [torch.randn(1, k, device=dev).to(torch.bfloat16) for _, n, k in shapes]
-    ys = [torch.empty(1, n, device=dev, dtype=torch.bfloat16) for _, n, k in shapes]
+    ys = [torch.empty(1, out_cols(name, n, swiglu), device=dev, dtype=torch.bfloat16) for name, n, k in shapes]
     stream = torch.cuda.current_stream()
     for lins in layers:  # eager first: sizes the GEMV workspaces outside capture
-        decode_pass(dq, lins, xs, ys, stream)
+        decode_pass(dq, lins, xs, ys, stream, shapes, swiglu)
     torch.cuda.synchronize()
-    graphs = [capture(torch, lambda st, l=lins: decode_pass(dq, l, xs, ys, st)) for lins in layers]
+    graphs = [capture(torch, lambda st, l=lins: decode_pass(dq, l, xs, ys, st, shapes, swiglu)) for lins in layers]
     for i in range(warmup):
         graphs[i % len(graphs)].replay()
     torch.cuda.synchronize()
@@ -233,18 +247,18 @@ def profile_prefill_run(dq, torch, dev, iters=5):
         torch.cuda.empty_cache()
 
 
-def time_prefill(dq, torch, lins, m, iters, dev, path, shapes=LAYER_27B):
+def time_prefill(dq, torch, lins, m, iters, dev, path, shapes=LAYER_27B, swiglu=()):
     """Device time of one prefill pass over the layer's seven linears
     (activation quantization included for the native paths), captured in a
     HIP graph like the decode step and replayed `iters` times between HIP
     events on the replay stream."""
     stream = torch.cuda.current_stream()
     xs = [torch.randn(m, k, device=dev).to(torch.bfloat16) for _, n, k in shapes]
-    ys = [torch.empty(m, n, device=dev, dtype=torch.bfloat16) for _, n, k in shapes]
+    ys = [torch.empty(m, out_cols(name, n, swiglu), device=dev, dtype=torch.bfloat16) for name, n, k in shapes]
 
     def body(st):
-        for lin, x, y in zip(lins, xs, ys):
-            lin.forward(x, y, path=path, stream=st)
+        for lin, x, y, (name, _, _) in zip(lins, xs, ys, shapes):
+            run_linear(lin, name, x, y, swiglu, path=path, stream=st)
     body(stream)  # eager first: sizes the handles' scratch outside capture
     torch.cuda.synchronize()
     g = capture(torch, body)
@@ -346,11 +360,18 @@ def main():
     fsteps = max(a.steps // 3, 10)
     fs = time_decode(dq, torch, fl, fsteps, 10, dev, shapes=LAYER_27B_FUSED)
     extra["decode_gbs_fused_qkv_gate_up"] = {"w8a16": round(layer_bytes(dq, dq.W8A16, LAYER_27B_FUSED) * fsteps / fs / 1e9, 1)}
-    print(f"# w8a16 decode, fused qkv / gate_up: {extra['decode_gbs_fused_qkv_gate_up']['w8a16']} GB/s",
-          file=sys.stderr, flush=True)
+    # ... and with gate_up's SwiGLU epilogue, which writes silu(gate) * up
+    # (the down projection's input) instead of the [M, 34816] gate_up output
+    fs2 = time_decode(dq, torch, fl, fsteps, 10, dev, shapes=LAYER_27B_FUSED, swiglu=("gate_up",))
+    extra["decode_gbs_fused_swiglu"] = {"w8a16": round(layer_bytes(dq, dq.W8A16, LAYER_27B_FUSED) * fsteps / fs2 / 1e9, 1)}
+    print(f"# w8a16 decode, fused qkv / gate_up: {extra['decode_gbs_fused_qkv_gate_up']['w8a16']} GB/s; "
+          f"with the SwiGLU epilogue: {extra['decode_gbs_fused_swiglu']['w8a16']} GB/s", file=sys.stderr, flush=True)
     if "w8a16" in sweep:
         tf, s2 = time_prefill(dq, torch, fl[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, shapes=LAYER_27B_FUSED)
         extra.setdefault("prefill_tflops_fused_qkv_gate_up", {})["w8a16_m2048"] = round(tf, 1)
+        tf2, _ = time_prefill(dq, torch, fl[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, shapes=LAYER_27B_FUSED,
+                              swiglu=("gate_up",))
+        extra.setdefault("prefill_tflops_fused_swiglu", {})["w8a16_m2048"] = round(tf2, 1)
     del fl
     torch.cuda.empty_cache()
     # quantized lm_head GEMV (vocab 248320 x hidden 5120): one copy is 1.27 GB
@@ -389,6 +410,9 @@ def main():
             tff, _ = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE,
                                   shapes=LAYER_27B_FUSED)
             extra.setdefault("prefill_tflops_fused_qkv_gate_up", {})[name + "_native_m1024"] = round(tff, 1)
+            tff2, _ = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE,
+                                   shapes=LAYER_27B_FUSED, swiglu=("gate_up",))
+            extra.setdefault("prefill_tflops_fused_swiglu", {})[name + "_native_m1024"] = round(tff2, 1)
         else:
             tf, s2 = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
             extra["prefill_tflops"][name + "_m2048"] = round(tf, 1)
