@@ -18,7 +18,7 @@ OUT = os.path.join(HERE, "lib")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT, "libdialq.so")
 
-SOURCES = ["abi.hip", "prep.hip", "gemv.hip", "gemm.hip", "local_q8.hip"]
+SOURCES = ["abi.hip", "prep.hip", "gemv.hip", "gemm.hip", "local_q8.hip", "select.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <mutex>
 #include <new>
 #include <stdexcept>
@@ -546,6 +547,78 @@ int dialq_linear_forward_swiglu(void *linear, const void *x, int32_t x_dtype, in
                                 size_t error_size) {
   return guarded(error, error_size, [&] {
     forward_impl((Linear *)linear, x, x_dtype, rows, y, y_dtype, path, stream, device_io, false, true);
+  });
+}
+
+size_t dialq_logits_select_workspace_bytes(int64_t vocab, int64_t n_repeat) {
+  if (vocab < 1) return 0;
+  const size_t ids = (size_t)(n_repeat > 0 ? n_repeat : 0) * sizeof(uint32_t);
+  return (select_workspace_bytes(vocab) + 255) / 256 * 256 + ids;
+}
+
+int dialq_logits_select(const void *logits, int32_t dtype, int64_t vocab, const uint32_t *repeat_ids,
+                        int64_t n_repeat, float repeat_penalty, float temperature, int32_t rule, int64_t k,
+                        uint32_t *out_idx, float *out_val, float *out_stats, void *workspace,
+                        size_t workspace_bytes, int32_t device, void *stream, int device_io, char *error,
+                        size_t error_size) {
+  return guarded(error, error_size, [&] {
+    size_t ls = dtype_size(dtype);
+    if (rule != DIALQ_SELECT_FIRST_MAX && rule != DIALQ_SELECT_TOTAL_LAST_MAX) fail("unknown selection rule %d", rule);
+    if (k < 1 || k > DIALQ_SELECT_MAX_K) fail("k must be in [1, %d], got %lld", DIALQ_SELECT_MAX_K, (long long)k);
+    if (vocab < k || vocab > 0xFFFFFFFFLL)
+      fail("vocab %lld must be at least k (%lld) and below 2^32", (long long)vocab, (long long)k);
+    if (!logits || !out_idx || !out_val || !out_stats) fail("logits and outputs must not be NULL");
+    if (n_repeat < 0 || (n_repeat > 0 && !repeat_ids)) fail("repeat context of %lld ids without a pointer", (long long)n_repeat);
+    // apply_repeat_penalty_in_place: each distinct id once, ids past the vocabulary ignored
+    std::vector<uint32_t> ids;
+    if (repeat_penalty != 1.0f && n_repeat > 0) {
+      ids.assign(repeat_ids, repeat_ids + n_repeat);
+      std::sort(ids.begin(), ids.end());
+      ids.erase(std::unique(ids.begin(), ids.end()), ids.end());
+      while (!ids.empty() && (int64_t)ids.back() >= vocab) ids.pop_back();
+    }
+    DeviceGuard dg(device);
+    hipStream_t st = (hipStream_t)stream;
+    const size_t need = dialq_logits_select_workspace_bytes(vocab, (int64_t)ids.size());
+    const size_t ws_off = (select_workspace_bytes(vocab) + 255) / 256 * 256;
+    DevBuf own_ws, dl, di, dv, ds;
+    void *ws = workspace;
+    if (!device_io || !ws) {
+      own_ws.alloc(need);
+      ws = own_ws.p;
+    } else if (workspace_bytes < need) {
+      fail("workspace of %zu bytes is smaller than the %zu bytes dialq_logits_select_workspace_bytes asks for",
+           workspace_bytes, need);
+    }
+    const void *lp = logits;
+    uint32_t *ip = out_idx;
+    float *vp = out_val, *sp = out_stats;
+    if (!device_io) {
+      stage_in(dl, logits, (size_t)vocab * ls, true, st);
+      lp = dl.p;
+      di.alloc((size_t)k * 4);
+      dv.alloc((size_t)k * 4);
+      ds.alloc(8);
+      ip = (uint32_t *)di.p;
+      vp = (float *)dv.p;
+      sp = (float *)ds.p;
+    }
+    uint32_t *dids = (uint32_t *)((uint8_t *)ws + ws_off);
+    if (!ids.empty()) {
+      hip_check(hipMemcpyAsync(dids, ids.data(), ids.size() * 4, hipMemcpyHostToDevice, st), "hipMemcpyAsync");
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");  // the host list dies with this call
+    }
+    hip_check(launch_select(lp, dtype, vocab, dids, (int)ids.size(), repeat_penalty, temperature, rule, (int)k, ws,
+                            ws_off, ip, vp, sp, st),
+              "selection launch");
+    if (!device_io) {
+      hip_check(hipMemcpyAsync(out_idx, ip, (size_t)k * 4, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+      hip_check(hipMemcpyAsync(out_val, vp, (size_t)k * 4, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+      hip_check(hipMemcpyAsync(out_stats, sp, 8, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+    } else if (!workspace) {
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");  // the call's own workspace is freed on return
+    }
   });
 }
 

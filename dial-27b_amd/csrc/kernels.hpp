@@ -69,6 +69,13 @@ void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t
 hipError_t launch_gemm_native(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M,
                               int64_t k_pad, void *y, int y_dtype, float *part, size_t part_bytes, int *cnt,
                               size_t cnt_count, hipStream_t st);
+// Token selection over one row of logits (repeat penalty, top-k keys,
+// softmax statistics); k <= 256.  ids: distinct context tokens below vocab.
+int select_slices(int64_t vocab);
+size_t select_workspace_bytes(int64_t vocab);
+hipError_t launch_select(const void *logits, int dtype, int64_t vocab, const uint32_t *ids, int n_ids, float penalty,
+                         float temperature, int rule, int k, void *ws, size_t ws_bytes, uint32_t *out_idx,
+                         float *out_val, float *out_stats, hipStream_t st);
 // Compute units of the current device (cached at first use).
 int device_cus();
 // Local q8 W8A8 decode (one row).

@@ -31,6 +31,8 @@ FLAG_GLOBAL_IS_DIVISOR = 0x1
 FLAG_WEIGHT_ONLY_PREFILL = 0x2
 # enum dialq_path
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GEMM_NATIVE = 0, 1, 2, 3
+SELECT_FIRST_MAX, SELECT_TOTAL_LAST_MAX = 0, 1
+SELECT_MAX_K = 256
 
 
 class Desc(C.Structure):
@@ -71,6 +73,9 @@ def _load():
         "dialq_linear_export": (C.c_int, [P, P, SZ, P, SZ, CH, SZ]),
         "dialq_linear_forward_swiglu": (C.c_int, [P, P, I32, I64, P, I32, I32, P, C.c_int, CH, SZ]),
         "dialq_local_q8_forward": (C.c_int, [P, P, I32, I64, P, I32, P, C.c_int, CH, SZ]),
+        "dialq_logits_select_workspace_bytes": (SZ, [I64, I64]),
+        "dialq_logits_select": (C.c_int, [P, I32, I64, P, I64, C.c_float, C.c_float, I32, I64, P, P, P, P, SZ,
+                                          I32, P, C.c_int, CH, SZ]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -287,6 +292,40 @@ class Linear:
                                      err, 512)
         _check(rc, err)
         return w, s
+
+
+def logits_select(logits, k=1, *, rule=SELECT_FIRST_MAX, repeat_ids=(), repeat_penalty=1.0, temperature=0.0,
+                  dtype=None, workspace=None, device=0, stream=None):
+    """Device token selection over one row of logits (dialq_logits_select).
+
+    logits: a torch device tensor (asynchronous; outputs are device tensors)
+    or a host numpy array (synchronous; outputs are numpy).  Returns
+    (indices uint32 [k], logits f32 [k], stats f32 [2] = (max, sum) of the
+    temperature-scaled softmax)."""
+    dev = _is_torch(logits)
+    vocab = logits.numel() if dev else np.asarray(logits).size
+    ld = dtype_code(logits) if dtype is None else dtype
+    ids = np.ascontiguousarray(np.asarray(list(repeat_ids), dtype=np.uint32))
+    if dev:
+        import torch
+        out_idx = torch.empty(k, dtype=torch.int32, device=logits.device)
+        out_val = torch.empty(k, dtype=torch.float32, device=logits.device)
+        out_stats = torch.empty(2, dtype=torch.float32, device=logits.device)
+    else:
+        out_idx = np.empty(k, np.uint32)
+        out_val = np.empty(k, np.float32)
+        out_stats = np.empty(2, np.float32)
+    err = _err()
+    rc = lib.dialq_logits_select(_ptr(logits), ld, vocab, _ptr(ids) if ids.size else None, ids.size,
+                                 float(repeat_penalty), float(temperature), rule, k, _ptr(out_idx), _ptr(out_val),
+                                 _ptr(out_stats), _ptr(workspace), _nbytes(workspace), device,
+                                 _stream_ptr(stream), int(dev), err, 512)
+    _check(rc, err)
+    return out_idx, out_val, out_stats
+
+
+def logits_select_workspace_bytes(vocab, n_repeat=0) -> int:
+    return int(lib.dialq_logits_select_workspace_bytes(vocab, n_repeat))
 
 
 def raw_weight_bytes(fmt, n, k) -> int:

@@ -168,6 +168,42 @@ int dialq_linear_forward_swiglu(void *linear, const void *x, int32_t x_dtype,
                                 int32_t path, void *stream, int device_io,
                                 char *error, size_t error_size);
 
+/* Token selection over one row of logits, after the lm_head.  Replaces the
+ * selection steps of sample_remote_logits / FastLogitsProcessor::sample
+ * (qwen3_vl/qwen3_vl.rs:130-174,282-323): the repeat penalty
+ * (apply_repeat_penalty_in_place, :225-240: the logit of each distinct
+ * context id below vocab divided by the penalty when >= 0, else multiplied),
+ * the greedy argmax, the top-k candidates and the softmax normaliser of
+ * softmax_in_place (:325-345).
+ *   logits: [vocab] of dtype; repeat_ids: HOST array of n_repeat ids (used
+ *   only when repeat_penalty != 1)
+ *   rule: DIALQ_SELECT_FIRST_MAX -- candle's argmax (the reference's greedy
+ *         device path): -0 == +0, NaN never chosen, ties to the smaller index;
+ *         DIALQ_SELECT_TOTAL_LAST_MAX -- max_by(f32::total_cmp) (its host
+ *         path): IEEE total order, ties to the larger index
+ *   k: 1 .. DIALQ_SELECT_MAX_K; out_idx[k], out_val[k]: indices and
+ *      (penalised) logits in descending order of the rule
+ *   temperature > 0: out_stats = {M, S}, M = max over the vocabulary of
+ *      logit / temperature, S = sum of exp(logit / temperature - M), so that
+ *      softmax_in_place's probability of candidate i is
+ *      exp(out_val[i] / temperature - M) / S; otherwise out_stats = {-inf, 0}
+ *   workspace: device memory of dialq_logits_select_workspace_bytes(vocab,
+ *      n_repeat) bytes (device_io = 1); NULL lets the call allocate its own
+ *      and synchronise
+ *   device_io: 1 = logits and outputs are device pointers on `device`,
+ *      asynchronous on `stream` (synchronous when repeat ids are uploaded);
+ *      0 = host pointers, synchronous. */
+enum dialq_select_rule { DIALQ_SELECT_FIRST_MAX = 0, DIALQ_SELECT_TOTAL_LAST_MAX = 1 };
+#define DIALQ_SELECT_MAX_K 256
+size_t dialq_logits_select_workspace_bytes(int64_t vocab, int64_t n_repeat);
+int dialq_logits_select(const void *logits, int32_t dtype, int64_t vocab,
+                        const uint32_t *repeat_ids, int64_t n_repeat,
+                        float repeat_penalty, float temperature, int32_t rule,
+                        int64_t k, uint32_t *out_idx, float *out_val,
+                        float *out_stats, void *workspace,
+                        size_t workspace_bytes, int32_t device, void *stream,
+                        int device_io, char *error, size_t error_size);
+
 /* Dequantize the resident weight into a dense [N,K] matrix of out_dtype
  * (F32, F16 or BF16, each rounded once to nearest-even from the exact f32
  * value).  Replaces QMatMul::dequantize_f16 (worker_w8a16.rs:125, used by

@@ -303,6 +303,66 @@ def swiglu(gate_up):
         return g / (1.0 + np.exp(-g)) * u
 
 
+# ---- token selection after the lm_head (qwen3_vl/qwen3_vl.rs) --------------
+def repeat_penalty(logits, penalty, context):
+    """apply_repeat_penalty_in_place (qwen3_vl.rs:225-240): for each distinct
+    id of `context` below len(logits), logit / penalty when logit >= 0, else
+    logit * penalty, in f32."""
+    out = np.array(logits, np.float32, copy=True)
+    p = np.float32(penalty)
+    seen = set()
+    for t in context:
+        t = int(t)
+        if t in seen:
+            continue
+        seen.add(t)
+        if t < out.size:
+            v = out[t]
+            out[t] = v / p if v >= 0 else v * p
+    return out
+
+
+def _total_key(v):
+    """f32::total_cmp as an unsigned integer order."""
+    u = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return np.where(u & 0x80000000, (~u) & 0xFFFFFFFF, u | 0x80000000)
+
+
+def select_total_last(logits, k=1):
+    """Iterator::max_by(f32::total_cmp) (qwen3_vl.rs:152-157) generalised to
+    the k best: descending IEEE total order, equal values in descending
+    index order (max_by returns the last maximum).  Returns (indices,
+    values)."""
+    v = np.asarray(logits, np.float32)
+    key = _total_key(v)
+    order = np.lexsort((-np.arange(v.size), -key.astype(np.float64)))  # key desc, then index desc
+    idx = order[:k]
+    return idx.astype(np.uint32), v[idx]
+
+
+def select_first_max(logits, k=1):
+    """candle's Tensor::argmax as the greedy device path calls it
+    (qwen3_vl.rs:137-142), generalised to the k best: the largest value by
+    `>`, so -0 and +0 are equal and NaN is never larger; equal values in
+    ascending index order.  Returns (indices, values)."""
+    v = np.asarray(logits, np.float32)
+    w = np.where(v == 0, np.float32(0), v)
+    key = np.where(np.isnan(w), 0, _total_key(w))
+    order = np.lexsort((np.arange(v.size), -key.astype(np.float64)))
+    idx = order[:k]
+    return idx.astype(np.uint32), v[idx]
+
+
+def softmax_stats(logits, temperature):
+    """softmax_in_place (qwen3_vl.rs:325-345) before its division: the max M
+    of logits / max(temperature, 1e-7) and S = sum exp(logit / t - M), in
+    float64 from the f32 quotients."""
+    t = np.float32(max(np.float32(temperature), np.float32(1e-7)))
+    x = (np.asarray(logits, np.float32) / t).astype(np.float64)
+    m = np.max(x)
+    return m, float(np.sum(np.exp(x - m)))
+
+
 def w8a16_linear(x, q, scale):
     x = _f32(x)
     q = np.ascontiguousarray(q, np.int8)
