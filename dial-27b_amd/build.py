@@ -65,7 +65,7 @@ def build(jobs: int = 0) -> str:
 
 
 def build_host() -> str:
-    """g++ build of host/dial_host.cpp, gguf.cpp, safetensors.cpp and bind.cpp into the pybind11
+    """g++ build of host/dial_host.cpp, gguf.cpp, safetensors.cpp, sampling.cpp and bind.cpp into the pybind11
     module dialq_host, linked against libdialq.so, the HIP runtime and
     rocBLAS (RUNPATH: the library directory, then /opt/rocm/lib)."""
     import sysconfig
@@ -77,7 +77,7 @@ def build_host() -> str:
            "-I", os.path.join(HERE, "..", "include"), "-I", "/opt/rocm/include",
            "-I", pybind11.get_include(), "-I", sysconfig.get_paths()["include"],
            os.path.join(host, "dial_host.cpp"), os.path.join(host, "gguf.cpp"), os.path.join(host, "safetensors.cpp"),
-           os.path.join(host, "bind.cpp"),
+           os.path.join(host, "sampling.cpp"), os.path.join(host, "bind.cpp"),
            "-o", out + ".tmp", "-L", OUT, "-ldialq", "-L", "/opt/rocm/lib", "-lamdhip64", "-lrocblas",
            "-Wl,-rpath,$ORIGIN:/opt/rocm/lib"]
     r = subprocess.run(cmd, capture_output=True, text=True)

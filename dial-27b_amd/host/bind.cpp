@@ -8,6 +8,7 @@
 #include "dial_host.hpp"
 #include "gguf.hpp"
 #include "safetensors.hpp"
+#include "sampling.hpp"
 
 namespace py = pybind11;
 using namespace dial;
@@ -217,4 +218,37 @@ PYBIND11_MODULE(dialq_host, m) {
   m.def("forward_worker_gguf", &forward_worker_gguf);
   m.def("build_worker_gguf_fp16_prefill_linear", &build_worker_gguf_fp16_prefill_linear);
   m.def("last_warning", &last_warning);
+
+  py::class_<SamplingRequest>(m, "SamplingRequest")
+      .def(py::init([](uint64_t seed, uint64_t sample_index, double temperature, std::optional<uint64_t> top_k,
+                       std::optional<double> top_p, float repeat_penalty, std::vector<uint32_t> repeat_context) {
+             return SamplingRequest{seed, sample_index, temperature, top_k, top_p, repeat_penalty,
+                                    std::move(repeat_context)};
+           }),
+           py::arg("seed") = 0, py::arg("sample_index") = 0, py::arg("temperature") = 0.0,
+           py::arg("top_k") = py::none(), py::arg("top_p") = py::none(), py::arg("repeat_penalty") = 1.0f,
+           py::arg("repeat_context") = std::vector<uint32_t>{})
+      .def_readwrite("seed", &SamplingRequest::seed)
+      .def_readwrite("sample_index", &SamplingRequest::sample_index)
+      .def_readwrite("temperature", &SamplingRequest::temperature)
+      .def_readwrite("top_k", &SamplingRequest::top_k)
+      .def_readwrite("top_p", &SamplingRequest::top_p)
+      .def_readwrite("repeat_penalty", &SamplingRequest::repeat_penalty)
+      .def_readwrite("repeat_context", &SamplingRequest::repeat_context);
+  m.def("sample_remote_logits", &sample_remote_logits);
+  m.def("sampling_mode", &sampling_mode);
+  m.def("last_sample_used_host_logits", &last_sample_used_host_logits);
+  m.def("chacha_block", [](std::array<uint32_t, 8> key, uint32_t counter, std::array<uint32_t, 3> nonce, int rounds) {
+    return ChaChaRng::block(key, counter, nonce, rounds);
+  });
+  m.def("rng_u32_stream", [](uint64_t seed, int n) {
+    ChaChaRng r = ChaChaRng::seed_from_u64(seed);
+    std::vector<uint32_t> out((size_t)n);
+    for (auto &v : out) v = r.next_u32();
+    return out;
+  });
+  m.def("sample_weighted", [](const std::vector<float> &w, uint64_t seed) {
+    ChaChaRng r = ChaChaRng::seed_from_u64(seed);
+    return sample_weighted(w, r);
+  });
 }
