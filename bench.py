@@ -14,8 +14,9 @@ Layer copies rotate so the weight working set (COPIES x 341 MB) exceeds the
 weight bytes streamed / wall time of the timed steps, in GB/s.  Extra keys
 report the same decode for Q4_K / FP8-128 / MXFP4, the prefill GEMM TFLOP/s
 (W8A16 and Q4_K at M = 2048, FP8-128 and MXFP4 native at M = 1024; also over
-the fused qkv / o / gate_up / down projections DIAL's layers call), the
-quantized lm_head decode GEMV (vocab 248320 x 5120), the roofline of the
+the fused qkv / o / gate_up / down projections DIAL's layers call, with and
+without gate_up's SwiGLU epilogue), the quantized lm_head decode GEMV (vocab
+248320 x 5120) and the device token selection after it, the roofline of the
 dominant kernel and the CPU baseline.
 
 `--profile` runs only the dominant kernel (W8A16 gate GEMV, eager launches
@@ -275,6 +276,33 @@ def time_prefill(dq, torch, lins, m, iters, dev, path, shapes=LAYER_27B, swiglu=
     return flops / secs / 1e12, secs
 
 
+def time_select(dq, torch, vocab, dev, reps=50):
+    """Device time of dialq_logits_select over one row of bf16 logits: the
+    greedy argmax and the top-50 candidates with softmax statistics (what
+    sampling with top_k = 50 reads back), captured in a graph and replayed."""
+    x = (torch.randn(vocab, device=dev) * 3).to(torch.bfloat16)
+    ws = torch.empty(dq.logits_select_workspace_bytes(vocab), dtype=torch.uint8, device=dev)
+    out = {}
+    for name, k, rule, t in (("argmax", 1, dq.SELECT_FIRST_MAX, 0.0), ("top50_t0.8", 50, dq.SELECT_TOTAL_LAST_MAX, 0.8)):
+        stream = torch.cuda.current_stream()
+        dq.logits_select(x, k, rule=rule, temperature=t, workspace=ws, stream=stream)
+        torch.cuda.synchronize()
+
+        def body(st):
+            for _ in range(reps):
+                dq.logits_select(x, k, rule=rule, temperature=t, workspace=ws, stream=st)
+        g = capture(torch, body)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        out[name] = round(e0.elapsed_time(e1) * 1e3 / reps, 2)
+    return out
+
+
 def cpu_baseline(seconds):
     """The oracle's multi-threaded CPU GEMV (oracle/cpu_baseline.c) on this
     host, W8A16 at the gate shape [17408, 5120], M = 1, repeated for a
@@ -390,6 +418,9 @@ def main():
             print(f"# lm_head {vn}x{vk} {name} decode: {ls_ * 1e6:.1f} us, {gbs:.1f} GB/s", file=sys.stderr, flush=True)
             del lin
             torch.cuda.empty_cache()
+        extra["select_after_lm_head_us"] = time_select(dq, torch, vn, dev)
+        print(f"# token selection over {vn} bf16 logits (us): {extra['select_after_lm_head_us']}",
+              file=sys.stderr, flush=True)
     for name in sweep:
         if name == "w8a16":
             continue

@@ -71,7 +71,6 @@ hipError_t launch_gemm_native(const WeightView &w, const uint8_t *xq, const void
                               size_t cnt_count, hipStream_t st);
 // Token selection over one row of logits (repeat penalty, top-k keys,
 // softmax statistics); k <= 256.  ids: distinct context tokens below vocab.
-int select_slices(int64_t vocab);
 size_t select_workspace_bytes(int64_t vocab);
 hipError_t launch_select(const void *logits, int dtype, int64_t vocab, const uint32_t *ids, int n_ids, float penalty,
                          float temperature, int rule, int k, void *ws, size_t ws_bytes, uint32_t *out_idx,

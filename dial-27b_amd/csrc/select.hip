@@ -12,15 +12,19 @@
 //
 // Here the whole selection stays on the device and only k (index, logit)
 // pairs and two statistics cross to the host:
-//   1. k_select_slices: slice s of the vocabulary, in chunks of 3840 logits
-//      behind the 256 best keys so far, is converted to f32, penalised, and
-//      bitonic-sorted as 64-bit keys in LDS; the slice's 256 best keys and
-//      the (max, sum of exp(x - max)) of its temperature-scaled logits go out;
-//   2. k_select_merge: one workgroup loads every slice's keys into LDS
-//      (at most 72 x 256 x 8 B = 144 KB), finds the k-th largest key by an
-//      8-bit radix select over the 64-bit keys, gathers the k keys above it,
-//      sorts them and writes indices and logits in descending order, plus
-//      the merged softmax statistics.
+//   1. k_select_slices: slice s of the vocabulary is converted to f32,
+//      penalised and turned into 64-bit keys; for k = 1 the slice keeps its
+//      largest key (a block max), otherwise chunks of C - KC keys behind the
+//      KC best so far (KC = k rounded up to a power of two) are
+//      bitonic-sorted in LDS (C = 512 for k <= 32, 1024 for k <= 64, 4096
+//      above, doubled while the slices would not fit the merge).  The
+//      slice's k best keys, descending, and the (max, sum of exp(x - max))
+//      of its temperature-scaled logits go out;
+//   2. k_select_merge: one workgroup stages the slices' sorted lists in LDS
+//      (at most 18432 keys, 144 KB), merges the statistics, and merges the
+//      lists pairwise in a tree that keeps the k best at each level (every
+//      output element placed by a merge-path binary search, all in
+//      parallel), writing indices and logits in descending order.
 //
 // Key of logit v at index i: the f32 bits mapped to an unsigned order
 // (sign set: ~u, else u | 2^31), then the index in the low word:
@@ -33,10 +37,9 @@
 
 namespace dialq {
 
-constexpr int kSelKP = 256;           // keys kept per slice; the largest k
-constexpr int kSelChunk = 4096;       // keys sorted per chunk step
-constexpr int kSelPayload = kSelChunk - kSelKP;
-constexpr int kSelMaxSlices = 72;     // 72 x 256 keys fill 144 KB of the merge's LDS
+constexpr int kSelMaxK = 256;          // largest k
+constexpr int kSelMaxSlices = 1024;    // one statistics pair per thread of the merge
+constexpr int kSelMaxKeys = 18432;     // slices x k staged by the merge: 144 KB of LDS
 
 struct SelectParams {
   const void *logits;
@@ -49,7 +52,8 @@ struct SelectParams {
   int rule;
   int slices;
   int64_t slice_len;
-  uint64_t *cand;       // [slices][kSelKP] keys, descending
+  int kc;               // carried keys per chunk: k rounded up to a power of two
+  uint64_t *cand;       // [slices][k] keys, descending
   float *stats;         // [slices][2] (max, sum of exp(x - max)) of the scaled logits
   int k;
   uint32_t *out_idx;
@@ -116,18 +120,48 @@ __device__ __forceinline__ float block_reduce256(float v, float *sh) {
   return MAX ? fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3])) : (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
 
+// One DPP step of a wave max: each enabled lane takes the max of its key and
+// the key of the lane CTRL names (row_shr:n = 0x110 + n, row_bcast:15 =
+// 0x142, row_bcast:31 = 0x143); lanes without a source keep their own.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_max_step(uint64_t v) {
+  const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+  const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xf, false);
+  const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xf, false);
+  const uint64_t o = ((uint64_t)ohi << 32) | olo;
+  return o > v ? o : v;
+}
+
+// Max of a 64-bit key over the wave, in every lane: row_shr 1, 2, 4, 8 leave
+// each 16-lane row's max in its lane 15, row_bcast 15 / 31 carry it into the
+// rows above, and lane 63 ends with the wave's max.
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
+  v = dpp_max_step<0x111, 0xf>(v);
+  v = dpp_max_step<0x112, 0xf>(v);
+  v = dpp_max_step<0x114, 0xf>(v);
+  v = dpp_max_step<0x118, 0xf>(v);
+  v = dpp_max_step<0x142, 0xa>(v);
+  v = dpp_max_step<0x143, 0xc>(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int C>
 __global__ __launch_bounds__(256) void k_select_slices(SelectParams p) {
-  __shared__ uint64_t keys[kSelChunk];
-  __shared__ float vals[kSelPayload];
+  __shared__ uint64_t keys[C];
+  __shared__ float vals[C];
   __shared__ float sh[4];
+  __shared__ uint64_t shk[4];
   const int tid = threadIdx.x;
+  const int kc = p.kc, payload = C - kc;
   const int64_t lo = (int64_t)blockIdx.x * p.slice_len;
   const int64_t hi = (lo + p.slice_len < p.vocab) ? lo + p.slice_len : p.vocab;
-  for (int i = tid; i < kSelKP; i += 256) keys[i] = 0;
+  for (int i = tid; i < kc; i += 256) keys[i] = 0;
   float run_m = -INFINITY, run_s = 0.0f;
   const bool stats = p.temperature > 0.0f;
-  for (int64_t base = lo; base < hi; base += kSelPayload) {
-    const int n = (int)((hi - base) < kSelPayload ? (hi - base) : kSelPayload);
+  for (int64_t base = lo; base < hi; base += payload) {
+    const int n = (int)((hi - base) < payload ? (hi - base) : payload);
     for (int i = tid; i < n; i += 256) vals[i] = load_in(p.logits, base + i, p.dtype);
     __syncthreads();
     if (p.penalty != 1.0f) {
@@ -144,108 +178,153 @@ __global__ __launch_bounds__(256) void k_select_slices(SelectParams p) {
       float m = -INFINITY;
       for (int i = tid; i < n; i += 256) m = fmaxf(m, vals[i] / p.temperature);
       m = block_reduce256<true>(m, sh);
-      float s = 0.0f;
-      for (int i = tid; i < n; i += 256) s += expf(vals[i] / p.temperature - m);
-      s = block_reduce256<false>(s, sh);
+      float sum = 0.0f;
+      for (int i = tid; i < n; i += 256) sum += expf(vals[i] / p.temperature - m);
+      sum = block_reduce256<false>(sum, sh);
       if (m > run_m) {
-        run_s = run_s * expf(run_m - m) + s;
+        run_s = run_s * expf(run_m - m) + sum;
         run_m = m;
       } else {
-        run_s += s * expf(m - run_m);
+        run_s += sum * expf(m - run_m);
       }
     }
-    for (int i = tid; i < kSelPayload; i += 256)
-      keys[kSelKP + i] = i < n ? select_key(vals[i], (uint32_t)(base + i), p.rule) : 0;
+    if (p.k == 1) {
+      // the largest key of the chunk and the one carried
+      uint64_t best = tid == 0 ? keys[0] : 0;
+      for (int i = tid; i < n; i += 256) {
+        const uint64_t key = select_key(vals[i], (uint32_t)(base + i), p.rule);
+        best = key > best ? key : best;
+      }
+      best = wave_max_u64_dpp(best);
+      if ((tid & 63) == 0) shk[tid >> 6] = best;
+      __syncthreads();
+      if (tid == 0) {
+        uint64_t b = shk[0];
+        for (int w = 1; w < 4; ++w) b = shk[w] > b ? shk[w] : b;
+        keys[0] = b;
+      }
+      __syncthreads();
+      continue;
+    }
+    for (int i = tid; i < payload; i += 256) keys[kc + i] = i < n ? select_key(vals[i], (uint32_t)(base + i), p.rule) : 0;
     __syncthreads();
-    bitonic_desc(keys, kSelChunk, 256);
+    bitonic_desc(keys, C, 256);
   }
-  uint64_t *out = p.cand + (size_t)blockIdx.x * kSelKP;
-  for (int i = tid; i < kSelKP; i += 256) out[i] = keys[i];
+  uint64_t *out = p.cand + (size_t)blockIdx.x * p.k;
+  for (int i = tid; i < p.k; i += 256) out[i] = keys[i];
   if (tid == 0) {
     p.stats[2 * blockIdx.x] = run_m;
     p.stats[2 * blockIdx.x + 1] = run_s;
   }
 }
 
-__global__ __launch_bounds__(1024) void k_select_merge(SelectParams p) {
-  extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
-  uint64_t *keys = smem;                                   // [slices * kSelKP]
-  uint64_t *sel = smem + (size_t)p.slices * kSelKP;        // [kSelKP]
-  int *hist = (int *)(sel + kSelKP);                       // [256]
-  __shared__ uint64_t s_prefix;
-  __shared__ int s_need, s_count;
-  const int tid = threadIdx.x;
-  const int n = p.slices * kSelKP;
-  for (int i = tid; i < n; i += 1024) keys[i] = p.cand[i];
-  if (tid < kSelKP) sel[tid] = 0;
-  if (tid == 0) {
-    float m = -INFINITY;
-    for (int s = 0; s < p.slices; ++s) m = fmaxf(m, p.stats[2 * s]);
-    float sum = 0.0f;
-    for (int s = 0; s < p.slices; ++s)
-      if (p.stats[2 * s + 1] > 0.0f) sum += p.stats[2 * s + 1] * expf(p.stats[2 * s] - m);
-    p.out_stats[0] = m;
-    p.out_stats[1] = sum;
-    s_prefix = 0;
-    s_need = p.k;
-    s_count = 0;
+// Sum (or max) of one value per thread over a 1024-thread workgroup.
+template <bool MAX>
+__device__ __forceinline__ float block_reduce1024(float v, float *sh) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(v, off);
+    v = MAX ? fmaxf(v, o) : v + o;
   }
   __syncthreads();
-  // 8-bit radix select of the k-th largest key (keys are distinct)
-  uint64_t prefix = 0, mask = 0;
-  for (int shift = 56; shift >= 0; shift -= 8) {
-    if (tid < 256) hist[tid] = 0;
-    __syncthreads();
-    for (int i = tid; i < n; i += 1024) {
-      const uint64_t key = keys[i];
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
-    }
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = sh[0];
+  for (int w = 1; w < 16; ++w) r = MAX ? fmaxf(r, sh[w]) : r + sh[w];
+  return r;
+}
+
+// Element r (0-based) of the descending merge of two descending lists a, b of
+// k distinct keys each (merge path: i keys come from a, r - i from b).
+__device__ __forceinline__ uint64_t merge_at(const uint64_t *a, const uint64_t *b, int k, int r) {
+  int lo = r > k ? r - k : 0, hi = r < k ? r : k;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1, j = r - mid;
+    if (mid < k && j > 0 && a[mid] > b[j - 1]) lo = mid + 1;
+    else hi = mid;
+  }
+  const int i = lo, j = r - lo;
+  return (i < k && (j >= k || a[i] > b[j])) ? a[i] : b[j];
+}
+
+constexpr int kSelMergeItems = 10;  // per thread and level: (18432 / 2 + 256) / 1024 rounded up
+
+__global__ __launch_bounds__(1024) void k_select_merge(SelectParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint64_t lists[];  // [slices][k]
+  __shared__ float sh[16];
+  const int tid = threadIdx.x;
+  const int G = p.slices, k = p.k;
+  for (int i = tid; i < G * k; i += 1024) lists[i] = p.cand[i];
+  // softmax statistics: max of the slice maxima, then their rescaled sums
+  const float ms = tid < G ? p.stats[2 * tid] : -INFINITY, ss = tid < G ? p.stats[2 * tid + 1] : 0.0f;
+  const float M = block_reduce1024<true>(ms, sh);
+  const float S = block_reduce1024<false>(ss > 0.0f ? ss * expf(ms - M) : 0.0f, sh);
+  if (tid == 0) {
+    p.out_stats[0] = M;
+    p.out_stats[1] = S;
+  }
+  __syncthreads();
+  if (k == 1) {  // argmax: the largest of the slice maxima
+    __shared__ uint64_t shk[16];
+    const uint64_t best = wave_max_u64_dpp(tid < G ? lists[tid] : 0);
+    if ((tid & 63) == 0) shk[tid >> 6] = best;
     __syncthreads();
     if (tid == 0) {
-      int need = s_need, cum = 0, d = 255;
-      for (; d > 0; --d) {
-        if (cum + hist[d] >= need) break;
-        cum += hist[d];
+      uint64_t b = shk[0];
+      for (int w = 1; w < 16; ++w) b = shk[w] > b ? shk[w] : b;
+      p.out_idx[0] = key_index(b, p.rule);
+      p.out_val[0] = key_logit(b);
+    }
+    return;
+  }
+  // Pairwise tree merge keeping the k best: at each level list q of the next
+  // level is the top k of lists 2q and 2q+1 (an odd last list moves down
+  // unchanged); every output element is found independently by merge_at,
+  // held in registers over a barrier, then written in place.
+  for (int nl = G; nl > 1; nl = (nl + 1) >> 1) {
+    const int pairs = nl >> 1, items = ((nl + 1) >> 1) * k;
+    uint64_t v[kSelMergeItems];
+#pragma unroll
+    for (int t = 0; t < kSelMergeItems; ++t) {
+      const int it = tid + 1024 * t;
+      v[t] = 0;
+      if (it < items) {
+        const int q = it / k, r = it - q * k;
+        v[t] = q < pairs ? merge_at(lists + (size_t)(2 * q) * k, lists + (size_t)(2 * q + 1) * k, k, r)
+                         : lists[(size_t)(2 * q) * k + r];
       }
-      s_need = need - cum;
-      s_prefix = prefix | ((uint64_t)d << shift);
     }
     __syncthreads();
-    prefix = s_prefix;
-    mask |= (uint64_t)0xFF << shift;
-  }
-  // the k keys at or above the k-th largest
-  for (int i = tid; i < n; i += 1024) {
-    const uint64_t key = keys[i];
-    if (key >= prefix) {
-      const int slot = atomicAdd(&s_count, 1);
-      if (slot < kSelKP) sel[slot] = key;
+#pragma unroll
+    for (int t = 0; t < kSelMergeItems; ++t) {
+      const int it = tid + 1024 * t;
+      if (it < items) lists[it] = v[t];
     }
+    __syncthreads();
   }
-  __syncthreads();
-  bitonic_desc(sel, kSelKP, 1024);
-  if (tid < p.k) {
-    p.out_idx[tid] = key_index(sel[tid], p.rule);
-    p.out_val[tid] = key_logit(sel[tid]);
+  if (tid < k) {
+    p.out_idx[tid] = key_index(lists[tid], p.rule);
+    p.out_val[tid] = key_logit(lists[tid]);
   }
 }
 
 size_t select_workspace_bytes(int64_t vocab) {
-  const int64_t slices = select_slices(vocab);
-  return (size_t)slices * kSelKP * sizeof(uint64_t) + (size_t)slices * 2 * sizeof(float);
-}
-
-int select_slices(int64_t vocab) {
-  int64_t s = (vocab + kSelPayload - 1) / kSelPayload;
-  if (s > kSelMaxSlices) s = kSelMaxSlices;
-  return (int)(s < 1 ? 1 : s);
+  (void)vocab;
+  return (size_t)kSelMaxKeys * sizeof(uint64_t) + (size_t)kSelMaxSlices * 2 * sizeof(float);
 }
 
 hipError_t launch_select(const void *logits, int dtype, int64_t vocab, const uint32_t *ids, int n_ids, float penalty,
                          float temperature, int rule, int k, void *ws, size_t ws_bytes, uint32_t *out_idx,
                          float *out_val, float *out_stats, hipStream_t st) {
-  if (k < 1 || k > kSelKP || vocab < k || vocab > 0xFFFFFFFFLL || ws_bytes < select_workspace_bytes(vocab))
+  if (k < 1 || k > kSelMaxK || vocab < k || vocab > 0xFFFFFFFFLL || ws_bytes < select_workspace_bytes(vocab))
     return hipErrorInvalidValue;
+  int kc = 1;
+  while (kc < k) kc <<= 1;
+  // slices: their k-key lists must fit the merge's LDS; chunks grow (1024, 2048, 4096 keys) until one chunk covers a slice
+  const int64_t cap = kSelMaxKeys / k < kSelMaxSlices ? kSelMaxKeys / k : kSelMaxSlices;
+  int C = kc <= 32 ? 512 : (kc <= 64 ? 1024 : 4096);
+  while (C < 4096 && (vocab + (C - kc) - 1) / (C - kc) > cap) C <<= 1;
+  int64_t g = (vocab + (C - kc) - 1) / (C - kc);
+  if (g > cap) g = cap;
   SelectParams p;
   p.logits = logits;
   p.dtype = dtype;
@@ -255,19 +334,22 @@ hipError_t launch_select(const void *logits, int dtype, int64_t vocab, const uin
   p.penalty = penalty;
   p.temperature = temperature;
   p.rule = rule;
-  p.slices = select_slices(vocab);
+  p.slices = (int)(g < 1 ? 1 : g);
   p.slice_len = (vocab + p.slices - 1) / p.slices;
+  p.kc = kc;
   p.cand = (uint64_t *)ws;
-  p.stats = (float *)((uint8_t *)ws + (size_t)p.slices * kSelKP * sizeof(uint64_t));
+  p.stats = (float *)((uint8_t *)ws + (size_t)kSelMaxKeys * sizeof(uint64_t));
   p.k = k;
   p.out_idx = out_idx;
   p.out_val = out_val;
   p.out_stats = out_stats;
-  k_select_slices<<<p.slices, 256, 0, st>>>(p);
+  if (C == 512) k_select_slices<512><<<p.slices, 256, 0, st>>>(p);
+  else if (C == 1024) k_select_slices<1024><<<p.slices, 256, 0, st>>>(p);
+  else if (C == 2048) k_select_slices<2048><<<p.slices, 256, 0, st>>>(p);
+  else k_select_slices<4096><<<p.slices, 256, 0, st>>>(p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const size_t lds = (size_t)p.slices * kSelKP * 8 + kSelKP * 8 + 256 * 4;
-  k_select_merge<<<1, 1024, lds, st>>>(p);
+  k_select_merge<<<1, 1024, (size_t)p.slices * k * sizeof(uint64_t), st>>>(p);
   return hipGetLastError();
 }
 
