@@ -41,7 +41,10 @@ struct GemmShape {
   static constexpr int STRIDE = SK + 8;                // bf16 elements per LDS row
   static constexpr bool KQ = FMT == DIALQ_FORMAT_Q4_K || FMT == DIALQ_FORMAT_Q6_K;
   static constexpr int MS = KQ ? 2 : 8;  // 16-row groups per workgroup
-  static constexpr int NS = KQ ? 2 : 4;  // 16-col strips per wave
+  // 16-col strips per wave.  Q6_K: one -- its three-plane tiles, 8 operands
+  // and 16 scales per strip spill at two strips (f16 / f32 activations:
+  // ~4 KB of scratch per lane)
+  static constexpr int NS = FMT == DIALQ_FORMAT_Q6_K ? 1 : (KQ ? 2 : 4);
   static constexpr int ROWS = 16 * MS;
   static constexpr int BUF = PARTS * ROWS * STRIDE;   // bf16 elements per LDS buffer
   static constexpr int LDS_BYTES = 2 * BUF * 2;
@@ -278,18 +281,28 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
               for (int n = 0; n < NS; ++n) acc[ms][n] = mfma_bf16(xa, o[n].b[t], acc[ms][n]);
             }
       } else {
+        // Q6_K walks its 8 slices in two halves, so only 4 activation
+        // operands per row group are live next to the weight operands
+        constexpr int NH = FMT == DIALQ_FORMAT_Q6_K ? 2 : 1, NXH = T::NX / NH;
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms) {
-          XOp<ACT> xo[T::NX];
+        for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-          for (int t = 0; t < T::NX; ++t) {
-            const int row = ms * 16 + r, kk = j * S::CHUNK + T::xk(t, g);
-            xo[t].hi = *(const u32x4 *)(base + row * S::STRIDE + kk);
-            if constexpr (S::PARTS == 2) xo[t].lo = *(const u32x4 *)(base + (S::ROWS + row) * S::STRIDE + kk);
+          for (int ms = 0; ms < MS; ++ms) {
+            XOp<ACT> xo[NXH];
+#pragma unroll
+            for (int tt = 0; tt < NXH; ++tt) {
+              const int t = hh * NXH + tt;
+              const int row = ms * 16 + r, kk = j * S::CHUNK + T::xk(t, g);
+              xo[tt].hi = *(const u32x4 *)(base + row * S::STRIDE + kk);
+              if constexpr (S::PARTS == 2) xo[tt].lo = *(const u32x4 *)(base + (S::ROWS + row) * S::STRIDE + kk);
+            }
+#pragma unroll
+            for (int n = 0; n < NS; ++n) {
+              if constexpr (NH == 1) bops_mac<FMT, ACT>(o[n], xo, acc[ms][n]);
+              else if (hh == 0) bops_mac<FMT, ACT, 0, NXH>(o[n], xo, acc[ms][n]);
+              else bops_mac<FMT, ACT, NXH, NXH>(o[n], xo, acc[ms][n]);
+            }
           }
-#pragma unroll
-          for (int n = 0; n < NS; ++n) bops_mac<FMT, ACT>(o[n], xo, acc[ms][n]);
-        }
       }
     }
   };

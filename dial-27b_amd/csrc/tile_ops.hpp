@@ -436,9 +436,12 @@ __device__ __forceinline__ BOps<FMT> make_bops(const RawTile &t) {
   return o;
 }
 
-// acc += (x slices) . (weight tile) for one 16-row group of x.
-template <int FMT, int ACT>
+// acc += (x slices) . (weight tile) for one 16-row group of x; the k-quants
+// can take the slices T0 .. T0 + TN - 1 only (xo[0] is slice T0).
+template <int FMT, int ACT, int T0 = 0, int TN = FmtTraits<FMT>::NX>
 __device__ __forceinline__ void bops_mac(const BOps<FMT> &o, const XOp<ACT> *xo, f32x4 &acc) {
+  static_assert(T0 == 0 && TN == FmtTraits<FMT>::NX || FMT == DIALQ_FORMAT_Q4_K || FMT == DIALQ_FORMAT_Q6_K,
+                "slice ranges are for the k-quants");
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   if constexpr (FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW ||
                 FMT == DIALQ_FORMAT_NVFP4 || FMT == DIALQ_FORMAT_MXFP4) {
@@ -459,9 +462,9 @@ __device__ __forceinline__ void bops_mac(const BOps<FMT> &o, const XOp<ACT> *xo,
   } else if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
     const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      f32x4 pq = mfma_x<ACT>(xo[j], o.b[j], zero);
-      f32x4 px = mfma_x<ACT>(xo[j], ones, zero);
+    for (int j = T0; j < T0 + TN; ++j) {
+      f32x4 pq = mfma_x<ACT>(xo[j - T0], o.b[j], zero);
+      f32x4 px = mfma_x<ACT>(xo[j - T0], ones, zero);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         acc[i] = __builtin_fmaf(o.s1[j], pq[i], __builtin_fmaf(-o.s2[j], px[i], acc[i]));
@@ -475,11 +478,12 @@ __device__ __forceinline__ void bops_mac(const BOps<FMT> &o, const XOp<ACT> *xo,
     const u32x4 z4 = {0, 0, 0, 0};
     const bool lower = (threadIdx.x & 32) == 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = T0; j < T0 + TN; ++j) {
+      const XOp<ACT> &xj = xo[j - T0];
       XOp<ACT> xl;
-      xl.hi = lower ? xo[j].hi : z4;
-      if constexpr (ActTraits<ACT>::PARTS == 2) xl.lo = lower ? xo[j].lo : z4;
-      const f32x4 pa = mfma_x<ACT>(xo[j], o.b[j], zero), ca = mfma_x<ACT>(xo[j], ones, zero);
+      xl.hi = lower ? xj.hi : z4;
+      if constexpr (ActTraits<ACT>::PARTS == 2) xl.lo = lower ? xj.lo : z4;
+      const f32x4 pa = mfma_x<ACT>(xj, o.b[j], zero), ca = mfma_x<ACT>(xj, ones, zero);
       const f32x4 pl = mfma_x<ACT>(xl, o.b[j], zero), cl = mfma_x<ACT>(xl, ones, zero);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
