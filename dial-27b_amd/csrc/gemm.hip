@@ -257,7 +257,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
     for (int j = 0; j < KS; ++j) {
       BOps<FMT> o[NS];
 #pragma unroll
-      for (int n = 0; n < NS; ++n) o[n] = make_bops<FMT>(slot[j][n]);
+      for (int n = 0; n < NS; ++n) o[n] = make_bops<FMT, ActTraits<ACT>::F16OP>(slot[j][n]);
       // refill this chunk's ring slot with stage st+2 as soon as it is unpacked
 #pragma unroll
       for (int n = 0; n < NS; ++n) {
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
               const int row = ms * 16 + r, kk = j * S::CHUNK + T::xk(t, g);
               const u32x4 xa = *(const u32x4 *)(base + (part * S::ROWS + row) * S::STRIDE + kk);
 #pragma unroll
-              for (int n = 0; n < NS; ++n) acc[ms][n] = mfma_bf16(xa, o[n].b[t], acc[ms][n]);
+              for (int n = 0; n < NS; ++n) acc[ms][n] = mfma_op<ACT>(xa, o[n].b[t], acc[ms][n]);
             }
       } else {
         // Q6_K walks its 8 slices in two halves, so only 4 activation
@@ -390,6 +390,13 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                  0, 0);
 }
+template <int ACT>
+__device__ __forceinline__ f32x16 mfma32_op(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (ActTraits<ACT>::F16OP)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  else return mfma32(a, b, c);
+}
 
 template <int FMT, int ACT, int MT, int KS, int OCC, bool SWI>
 __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
@@ -483,8 +490,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
       u32x4 b[NQ];
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
-        if constexpr (FMT == DIALQ_FORMAT_W8A16) b[q] = i8x8_to_bf16(slot[j][q][0], slot[j][q][1]);
-        else b[q] = e4m3x8_to_bf16(slot[j][q][0], slot[j][q][1]);
+        constexpr bool F16 = ActTraits<ACT>::F16OP;
+        if constexpr (FMT == DIALQ_FORMAT_W8A16)
+          b[q] = F16 ? i8x8_to_f16(slot[j][q][0], slot[j][q][1]) : i8x8_to_bf16(slot[j][q][0], slot[j][q][1]);
+        else
+          b[q] = F16 ? e4m3x8_to_f16(slot[j][q][0], slot[j][q][1]) : e4m3x8_to_bf16(slot[j][q][0], slot[j][q][1]);
         slot[j][q] = bload(st + 2, j, q);  // refill with stage st+2
       }
 #pragma unroll
@@ -494,7 +504,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
           const int row = mt * 32 + (lane & 31), kk = j * 16 + 8 * h;
           const u32x4 a = *(const u32x4 *)(base + (part * ROWS + row) * STRIDE + kk);
 #pragma unroll
-          for (int q = 0; q < NQ; ++q) acc[mt][q] = mfma32(a, b[q], acc[mt][q]);
+          for (int q = 0; q < NQ; ++q) acc[mt][q] = mfma32_op<ACT>(a, b[q], acc[mt][q]);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -592,7 +602,10 @@ static hipError_t gemm_act(const WeightView &w, const void *x, int x_dtype, int6
                            int y_dtype, hipStream_t st) {
   switch (x_dtype) {
     case DIALQ_BF16: return gemm_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, st);
-    case DIALQ_F16: return gemm_dispatch<FMT, DIALQ_F16>(w, x, M, y, y_dtype, st);
+    // f16 activations go to f16 MFMAs as they are, against f16 weight
+    // operands; MXFP4's scaled codes need bf16's exponent range (hi / lo parts)
+    case DIALQ_F16:
+      return gemm_dispatch<FMT, FMT == DIALQ_FORMAT_MXFP4 ? DIALQ_F16 : kActF16N>(w, x, M, y, y_dtype, st);
     case DIALQ_F32: return gemm_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, st);
   }
   return hipErrorInvalidValue;

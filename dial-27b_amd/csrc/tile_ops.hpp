@@ -32,9 +32,21 @@ __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+
 // ---- activation operands ----------------------------------------------------
 // ACT = DIALQ_BF16: one bf16 part.  DIALQ_F16 / DIALQ_F32: bf16 hi + lo parts
 // (exact for f16, 2^-17 relative for f32), two MFMAs per product.
+// kActF16N: f16 activations taken as they are by f16 MFMAs, against weight
+// operands built in f16 (the prefill GEMMs; every code except MXFP4's
+// E8M0-scaled values is exact in f16).
+constexpr int kActF16N = 16;
+
 template <int ACT>
 struct XOp {
   u32x4 hi;
@@ -44,11 +56,16 @@ template <>
 struct XOp<DIALQ_BF16> {
   u32x4 hi;
 };
+template <>
+struct XOp<kActF16N> {
+  u32x4 hi;
+};
 
 template <int ACT>
 struct ActTraits {
-  static constexpr int PARTS = (ACT == DIALQ_BF16) ? 1 : 2;
+  static constexpr int PARTS = (ACT == DIALQ_BF16 || ACT == kActF16N) ? 1 : 2;
   static constexpr int BYTES = (ACT == DIALQ_F32) ? 4 : 2;
+  static constexpr bool F16OP = ACT == kActF16N;  // weight operands in f16
 };
 
 __device__ __forceinline__ void split_f32(float v, uint32_t &h, uint32_t &l) {
@@ -113,9 +130,21 @@ __device__ __forceinline__ XOp<ACT> load_x8_clamped(const void *x, int64_t m, in
 
 template <int ACT>
 __device__ __forceinline__ f32x4 mfma_x(const XOp<ACT> &a, u32x4 b, f32x4 c) {
-  c = mfma_bf16(a.hi, b, c);
-  if constexpr (ACT != DIALQ_BF16) c = mfma_bf16(a.lo, b, c);
-  return c;
+  if constexpr (ACT == kActF16N) {
+    return mfma_f16(a.hi, b, c);
+  } else {
+    c = mfma_bf16(a.hi, b, c);
+    if constexpr (ACT != DIALQ_BF16) c = mfma_bf16(a.lo, b, c);
+    return c;
+  }
+}
+
+// One MFMA on a one-part activation operand and a weight operand of the
+// same type.
+template <int ACT>
+__device__ __forceinline__ f32x4 mfma_op(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (ACT == kActF16N) return mfma_f16(a, b, c);
+  else return mfma_bf16(a, b, c);
 }
 
 // ---- buffer loads -----------------------------------------------------------
@@ -176,7 +205,7 @@ __device__ __forceinline__ XRaw<ACT> xraw_load(rsrc_t r, uint32_t off) {
 template <int ACT>
 __device__ __forceinline__ XOp<ACT> xraw_to_op(const XRaw<ACT> &v) {
   XOp<ACT> o;
-  if constexpr (ACT == DIALQ_BF16) {
+  if constexpr (ACT == DIALQ_BF16 || ACT == kActF16N) {
     o.hi = v.a;
   } else if constexpr (ACT == DIALQ_F16) {
 #pragma unroll
@@ -253,21 +282,79 @@ __device__ __forceinline__ u32x4 e2m1x8_pow2_to_bf16(uint32_t d, float scale) {
   return r;
 }
 
-// 8 nibbles (shift 0 = low, 4 = high) of two dwords -> bf16 (128 + q).
-__device__ __forceinline__ u32x4 nib8_to_bf16_off128(uint32_t d0, uint32_t d1, int shift) {
-  uint32_t a = (d0 >> shift) & 0x0f0f0f0fu, b = (d1 >> shift) & 0x0f0f0f0fu;
+// ---- weight code -> exact f16 (kActF16N) ------------------------------------
+__device__ __forceinline__ uint32_t pack_f16_exact(float lo, float hi) {
+  // both values are exact in f16, so rounding toward zero changes nothing
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
+__device__ __forceinline__ u32x4 i8x8_to_f16(uint32_t d0, uint32_t d1) {
   u32x4 r;
-  r[0] = __builtin_amdgcn_perm(0x43434343u, a, 0x04010400u);
-  r[1] = __builtin_amdgcn_perm(0x43434343u, a, 0x04030402u);
-  r[2] = __builtin_amdgcn_perm(0x43434343u, b, 0x04010400u);
-  r[3] = __builtin_amdgcn_perm(0x43434343u, b, 0x04030402u);
+  uint32_t d[2] = {d0, d1};
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    float f0 = (float)((int32_t)(d[w] << 24) >> 24);
+    float f1 = (float)((int32_t)(d[w] << 16) >> 24);
+    float f2 = (float)((int32_t)(d[w] << 8) >> 24);
+    float f3 = (float)((int32_t)d[w] >> 24);
+    r[2 * w] = pack_f16_exact(f0, f1);
+    r[2 * w + 1] = pack_f16_exact(f2, f3);
+  }
   return r;
+}
+
+__device__ __forceinline__ u32x4 e4m3x8_to_f16(uint32_t d0, uint32_t d1) {
+  u32x4 r;
+  r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false));
+  r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true));
+  r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false));
+  r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true));
+  return r;
+}
+
+// E2M1 times an E4M3 scale: at most 5 significant bits between 2^-10 and
+// 2688, exact in f16.
+__device__ __forceinline__ u32x4 e2m1x8_to_f16(uint32_t d, float scale) {
+  u32x4 r;
+  f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 0);
+  f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 1);
+  f32x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 2);
+  f32x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 3);
+  r[0] = pack_f16_exact(v0[0] * scale, v0[1] * scale);
+  r[1] = pack_f16_exact(v1[0] * scale, v1[1] * scale);
+  r[2] = pack_f16_exact(v2[0] * scale, v2[1] * scale);
+  r[3] = pack_f16_exact(v3[0] * scale, v3[1] * scale);
+  return r;
+}
+
+// Byte-code pairs with a constant high byte: 0x43 gives bf16 (128 + q),
+// 0x64 gives f16 (1024 + q), q < 256.
+template <bool F16>
+__device__ __forceinline__ u32x4 bytes8_off(uint32_t a, uint32_t b) {
+  constexpr uint32_t HI = F16 ? 0x64646464u : 0x43434343u;
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(HI, a, 0x04010400u);
+  r[1] = __builtin_amdgcn_perm(HI, a, 0x04030402u);
+  r[2] = __builtin_amdgcn_perm(HI, b, 0x04010400u);
+  r[3] = __builtin_amdgcn_perm(HI, b, 0x04030402u);
+  return r;
+}
+
+// 8 nibbles (shift 0 = low, 4 = high) of two dwords -> bf16 (128 + q), or
+// f16 (1024 + q).
+template <bool F16 = false>
+__device__ __forceinline__ u32x4 nib8_off(uint32_t d0, uint32_t d1, int shift) {
+  return bytes8_off<F16>((d0 >> shift) & 0x0f0f0f0fu, (d1 >> shift) & 0x0f0f0f0fu);
+}
+__device__ __forceinline__ u32x4 nib8_to_bf16_off128(uint32_t d0, uint32_t d1, int shift) {
+  return nib8_off<false>(d0, d1, shift);
 }
 
 // Q6_K slice t of a lane (8 values k = 32t + 8g + j): 6-bit codes q from the
 // ql plane of half t/4 (bytes 8(qd&1).., nibble qd>>1) and the qh plane
-// (bytes 8h.., bits 2qd), qd = t%4, as bf16 (128 + q).
-__device__ __forceinline__ u32x4 q6x8_to_bf16_off128(const u32x4 &ql, const u32x4 &qh, int t) {
+// (bytes 8h.., bits 2qd), qd = t%4, as bf16 (128 + q) or f16 (1024 + q).
+template <bool F16 = false>
+__device__ __forceinline__ u32x4 q6x8_off(const u32x4 &ql, const u32x4 &qh, int t) {
   const int h = t >> 2, qd = t & 3, i = qd & 1;
   const int ns = 4 * (qd >> 1), hs = 2 * qd;
   uint32_t q[2];
@@ -276,12 +363,10 @@ __device__ __forceinline__ u32x4 q6x8_to_bf16_off128(const u32x4 &ql, const u32x
     const uint32_t hb = hs <= 4 ? (qh[2 * h + w] << (4 - hs)) : (qh[2 * h + w] >> (hs - 4));
     q[w] = ((ql[2 * i + w] >> ns) & 0x0f0f0f0fu) | (hb & 0x30303030u);
   }
-  u32x4 r;
-  r[0] = __builtin_amdgcn_perm(0x43434343u, q[0], 0x04010400u);
-  r[1] = __builtin_amdgcn_perm(0x43434343u, q[0], 0x04030402u);
-  r[2] = __builtin_amdgcn_perm(0x43434343u, q[1], 0x04010400u);
-  r[3] = __builtin_amdgcn_perm(0x43434343u, q[1], 0x04030402u);
-  return r;
+  return bytes8_off<F16>(q[0], q[1]);
+}
+__device__ __forceinline__ u32x4 q6x8_to_bf16_off128(const u32x4 &ql, const u32x4 &qh, int t) {
+  return q6x8_off<false>(ql, qh, t);
 }
 
 // Signed byte i of a dword as f32.
@@ -367,34 +452,39 @@ struct BOps {
 };
 
 // `t` must carry the lane row's scales (gemv tile_fill / gemm gemm_tile).
-template <int FMT>
+// F16: operands in f16 for kActF16N (the k-quant codes offset by 1024
+// instead of 128).
+template <int FMT, bool F16 = false>
 __device__ __forceinline__ BOps<FMT> make_bops(const RawTile &t) {
+  static_assert(!F16 || FMT != DIALQ_FORMAT_MXFP4, "E8M0-scaled codes leave the f16 range");
   BOps<FMT> o;
+  auto i8 = [](uint32_t a, uint32_t b) { return F16 ? i8x8_to_f16(a, b) : i8x8_to_bf16(a, b); };
+  auto e4 = [](uint32_t a, uint32_t b) { return F16 ? e4m3x8_to_f16(a, b) : e4m3x8_to_bf16(a, b); };
   if constexpr (FMT == DIALQ_FORMAT_W8A16) {
-    o.b[0] = i8x8_to_bf16(t.a[0], t.a[1]);
-    o.b[1] = i8x8_to_bf16(t.a[2], t.a[3]);
+    o.b[0] = i8(t.a[0], t.a[1]);
+    o.b[1] = i8(t.a[2], t.a[3]);
   } else if constexpr (FMT == DIALQ_FORMAT_FP8_ROW) {
-    o.b[0] = e4m3x8_to_bf16(t.a[0], t.a[1]);
-    o.b[1] = e4m3x8_to_bf16(t.a[2], t.a[3]);
+    o.b[0] = e4(t.a[0], t.a[1]);
+    o.b[1] = e4(t.a[2], t.a[3]);
   } else if constexpr (FMT == DIALQ_FORMAT_Q8_0) {
     const uint32_t dd = t.s0;
     o.s1[0] = f16_bits_to_f32(dd & 0xffffu);
     o.s1[1] = f16_bits_to_f32(dd >> 16);
-    o.b[0] = i8x8_to_bf16(t.a[0], t.a[1]);
-    o.b[1] = i8x8_to_bf16(t.a[2], t.a[3]);
+    o.b[0] = i8(t.a[0], t.a[1]);
+    o.b[1] = i8(t.a[2], t.a[3]);
   } else if constexpr (FMT == DIALQ_FORMAT_FP8_BLOCK) {
     o.s1[0] = __uint_as_float(t.s0);
-    o.b[0] = e4m3x8_to_bf16(t.a[0], t.a[1]);
-    o.b[1] = e4m3x8_to_bf16(t.a[2], t.a[3]);
-    o.b[2] = e4m3x8_to_bf16(t.b[0], t.b[1]);
-    o.b[3] = e4m3x8_to_bf16(t.b[2], t.b[3]);
+    o.b[0] = e4(t.a[0], t.a[1]);
+    o.b[1] = e4(t.a[2], t.a[3]);
+    o.b[2] = e4(t.b[0], t.b[1]);
+    o.b[3] = e4(t.b[2], t.b[3]);
   } else if constexpr (FMT == DIALQ_FORMAT_NVFP4) {
     const uint32_t sb = t.s0;
     float g0 = e4m3_to_f32(sb & 0xffu), g1 = e4m3_to_f32(sb >> 8);
-    o.b[0] = e2m1x8_to_bf16(t.a[0], g0);
-    o.b[1] = e2m1x8_to_bf16(t.a[1], g0);
-    o.b[2] = e2m1x8_to_bf16(t.a[2], g1);
-    o.b[3] = e2m1x8_to_bf16(t.a[3], g1);
+    o.b[0] = F16 ? e2m1x8_to_f16(t.a[0], g0) : e2m1x8_to_bf16(t.a[0], g0);
+    o.b[1] = F16 ? e2m1x8_to_f16(t.a[1], g0) : e2m1x8_to_bf16(t.a[1], g0);
+    o.b[2] = F16 ? e2m1x8_to_f16(t.a[2], g1) : e2m1x8_to_bf16(t.a[2], g1);
+    o.b[3] = F16 ? e2m1x8_to_f16(t.a[3], g1) : e2m1x8_to_bf16(t.a[3], g1);
   } else if constexpr (FMT == DIALQ_FORMAT_MXFP4) {
     float sc = e8m0_to_f32(t.s0);
 #pragma unroll
@@ -418,15 +508,15 @@ __device__ __forceinline__ BOps<FMT> make_bops(const RawTile &t) {
       }
       float s1 = d * (float)scj;
       o.s1[j] = s1;
-      o.s2[j] = __builtin_fmaf(128.0f, s1, dmin * (float)mj);
+      o.s2[j] = __builtin_fmaf(F16 ? 1024.0f : 128.0f, s1, dmin * (float)mj);
       const int i4 = j >> 1;
-      o.b[j] = nib8_to_bf16_off128(qd[2 * i4], qd[2 * i4 + 1], (j & 1) ? 4 : 0);
+      o.b[j] = nib8_off<F16>(qd[2 * i4], qd[2 * i4 + 1], (j & 1) ? 4 : 0);
     }
   } else if constexpr (FMT == DIALQ_FORMAT_Q6_K) {
     const float d = f16_bits_to_f32(t.s0 & 0xffffu);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      o.b[j] = q6x8_to_bf16_off128(j < 4 ? t.a : t.b, t.hdr, j);
+      o.b[j] = q6x8_off<F16>(j < 4 ? t.a : t.b, t.hdr, j);
       // sub-blocks 2j (lanes g < 2) and 2j + 1 (g >= 2): bytes 2j, 2j+1
       const float lo = sbyte_f32(t.sc[j >> 1], 2 * (j & 1)), hi = sbyte_f32(t.sc[j >> 1], 2 * (j & 1) + 1);
       o.s1[j] = d * hi;
@@ -460,7 +550,8 @@ __device__ __forceinline__ void bops_mac(const BOps<FMT> &o, const XOp<ACT> *xo,
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(o.s1[0], p[i], acc[i]);
   } else if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
-    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    constexpr uint32_t ONE = ActTraits<ACT>::F16OP ? 0x3c003c00u : 0x3f803f80u;  // 1.0 pairs
+    const u32x4 ones = {ONE, ONE, ONE, ONE};
 #pragma unroll
     for (int j = T0; j < T0 + TN; ++j) {
       f32x4 pq = mfma_x<ACT>(xo[j - T0], o.b[j], zero);
@@ -473,8 +564,11 @@ __device__ __forceinline__ void bops_mac(const BOps<FMT> &o, const XOp<ACT> *xo,
     // A 32-k slice spans two 16-value sub-blocks with their own scales:
     // lanes g < 2 hold the lower one.  With P = x.(128 + q) and C = sum(x),
     // over the whole slice (a) and over the lower sub-block only (l):
-    // y += s_hi*(Pa - 160 Ca) + (s_lo - s_hi)*(Pl - 160 Cl).
-    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    // y += s_hi*(Pa - 160 Ca) + (s_lo - s_hi)*(Pl - 160 Cl)  (1056 for the
+    // f16 operands, whose codes are offset by 1024).
+    constexpr uint32_t ONE = ActTraits<ACT>::F16OP ? 0x3c003c00u : 0x3f803f80u;
+    constexpr float OFF = ActTraits<ACT>::F16OP ? 1056.0f : 160.0f;
+    const u32x4 ones = {ONE, ONE, ONE, ONE};
     const u32x4 z4 = {0, 0, 0, 0};
     const bool lower = (threadIdx.x & 32) == 0;
 #pragma unroll
@@ -487,7 +581,7 @@ __device__ __forceinline__ void bops_mac(const BOps<FMT> &o, const XOp<ACT> *xo,
       const f32x4 pl = mfma_x<ACT>(xl, o.b[j], zero), cl = mfma_x<ACT>(xl, ones, zero);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float ua = __builtin_fmaf(-160.0f, ca[i], pa[i]), ul = __builtin_fmaf(-160.0f, cl[i], pl[i]);
+        const float ua = __builtin_fmaf(-OFF, ca[i], pa[i]), ul = __builtin_fmaf(-OFF, cl[i], pl[i]);
         acc[i] = __builtin_fmaf(o.s1[j], ua, __builtin_fmaf(o.s2[j], ul, acc[i]));
       }
     }
