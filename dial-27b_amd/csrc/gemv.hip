@@ -87,7 +87,8 @@ __device__ __forceinline__ void stage_xsums(const Ctx &cx, lds_f32 *xs, int sub,
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if constexpr (ACT == DIALQ_BF16) a += bf16_bits_to_f32(v[j] & 0xffffu) + bf16_bits_to_f32(v[j] >> 16);
-        else if constexpr (ACT == DIALQ_F16) a += f16_bits_to_f32(v[j] & 0xffffu) + f16_bits_to_f32(v[j] >> 16);
+        else if constexpr (ACT == DIALQ_F16 || ACT == kActF16N)
+          a += f16_bits_to_f32(v[j] & 0xffffu) + f16_bits_to_f32(v[j] >> 16);
         else a += __uint_as_float(v[j]);
       }
     }
@@ -185,7 +186,7 @@ struct GenericPolicy {
       if constexpr (XL) xo[t] = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, r, sl.c * T::CHUNK + T::xk(t, g), true));
       else xo[t] = xraw_to_op<ACT>(sl.x.v[t]);
     }
-    bops_mac<FMT, ACT>(make_bops<FMT>(sl.t), xo, a.v);
+    bops_mac<FMT, ACT>(make_bops<FMT, ActTraits<ACT>::F16OP>(sl.t), xo, a.v);
   }
   static __device__ __forceinline__ void values(const Acc &a, float (&v)[NV], int (&mrow)[NV], int lane) {
     const int g = lane >> 4;
@@ -203,7 +204,8 @@ struct GenericPolicy {
 // lanes feed zeros), and every lane ends up owning one output (m' = l/16) and
 // four sub-blocks (i = 0..3, plus 4..7 in the second accumulator): the
 // per-sub-block scales cost 4 FMAs per accumulator instead of 4 per row group
-// per sub-block.  Weights enter as bf16(128 + q); the offset and the dmin*m
+// per sub-block.  Weights enter as bf16(128 + q) (f16(1024 + q) for f16
+// activations); the offset and the dmin*m
 // term use the per-sub-block activation sums X_t[m'] from a second MFMA with
 // a ones operand:  y += s1*D - (128*s1 + dmin*m)*X.  RP passes cover rows
 // 4*pass + m'.
@@ -239,9 +241,13 @@ struct Q4kRowsPolicy {
         for (int h = 0; h < 2; ++h) sl.x.v[2 * q + h] = x_fetch<ACT, false>(cx, 4 * q + mq, xk(c, h, lane), valid);
     }
   }
+  static constexpr bool F16 = ActTraits<ACT>::F16OP;  // f16(1024 + q) codes, f16 MFMAs
+  static constexpr bool ONEPART = ACT == DIALQ_BF16 || F16;
   static __device__ __forceinline__ void compute(const Slot &sl, Acc &acc, const Ctx &cx) {
     const int lane = threadIdx.x & 63, jj = lane & 3, mq = (lane & 15) >> 2;
-    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    constexpr uint32_t ONE = F16 ? 0x3c003c00u : 0x3f803f80u;
+    constexpr float OFF = F16 ? 1024.0f : 128.0f;
+    const u32x4 ones = {ONE, ONE, ONE, ONE};
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     const u32x4 hd = sl.t.hdr;
     const float d = f16_bits_to_f32(hd[0] & 0xffffu), dmin = f16_bits_to_f32(hd[0] >> 16);
@@ -253,14 +259,14 @@ struct Q4kRowsPolicy {
 #pragma unroll
     for (int q = 0; q < RP; ++q) {
       f32x4 cq[2] = {zero, zero}, cs[2] = {zero, zero};
-      if constexpr (XL && ACT == DIALQ_BF16) {
-        // bf16 operands straight from the staged rows: a lane outside MFMA
-        // t's sub-block (or past the last row) reads the zero block
+      if constexpr (XL && ONEPART) {
+        // one-part operands straight from the staged rows: a lane outside
+        // MFMA t's sub-block (or past the last row) reads the zero block
         const int row = 4 * q + mq;
         const lds_u8 *rowp = cx.xl + row * cx.pitch + (sl.c * 256 + 8 * (lane >> 4)) * 2;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-          const u32x4 wb = nib8_to_bf16_off128(qd[2 * (t >> 1)], qd[2 * (t >> 1) + 1], (t & 1) ? 4 : 0);
+          const u32x4 wb = nib8_off<F16>(qd[2 * (t >> 1)], qd[2 * (t >> 1) + 1], (t & 1) ? 4 : 0);
           const lds_u8 *src = (jj == (t & 3) && row < cx.mrows) ? rowp + 64 * t : cx.zero;
           XOp<ACT> av;
           av.hi = *(const u32x4 __attribute__((address_space(3))) *)src;
@@ -278,7 +284,7 @@ struct Q4kRowsPolicy {
         }
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-          const u32x4 wb = nib8_to_bf16_off128(qd[2 * (t >> 1)], qd[2 * (t >> 1) + 1], (t & 1) ? 4 : 0);
+          const u32x4 wb = nib8_off<F16>(qd[2 * (t >> 1)], qd[2 * (t >> 1) + 1], (t & 1) ? 4 : 0);
           const bool on = (jj == (t & 3));
           const XOp<ACT> &src = (t < 4) ? xa : xb;
           XOp<ACT> av;
@@ -299,12 +305,12 @@ struct Q4kRowsPolicy {
         }
       }
       // lane (g, r) holds rows 4g+i: m' = g, sub-block i (+4 in [1]);
-      // s1*D - (128*s1 + dmin*m)*X = d*sc*(D - 128 X) - dmin*m*X
+      // s1*D - (OFF*s1 + dmin*m)*X = d*sc*(D - OFF X) - dmin*m*X
       float sa = 0.0f, sm = 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sa = __builtin_fmaf((float)((sc_lo >> (8 * i)) & 0xffu), __builtin_fmaf(-128.0f, cs[0][i], cq[0][i]), sa);
-        sa = __builtin_fmaf((float)((sc_hi >> (8 * i)) & 0xffu), __builtin_fmaf(-128.0f, cs[1][i], cq[1][i]), sa);
+        sa = __builtin_fmaf((float)((sc_lo >> (8 * i)) & 0xffu), __builtin_fmaf(-OFF, cs[0][i], cq[0][i]), sa);
+        sa = __builtin_fmaf((float)((sc_hi >> (8 * i)) & 0xffu), __builtin_fmaf(-OFF, cs[1][i], cq[1][i]), sa);
         sm = __builtin_fmaf((float)((m_lo >> (8 * i)) & 0xffu), cs[0][i], sm);
         sm = __builtin_fmaf((float)((m_hi >> (8 * i)) & 0xffu), cs[1][i], sm);
       }
@@ -327,7 +333,8 @@ struct Q4kRowsPolicy {
 // group u = t/2 from the lanes with g/2 == jj%2 in the slices with
 // t%2 == jj/2: each lane fetches four activation operands per row pass
 // (t = 2u + jj/2), and MFMAs 2u, 2u+1 leave D_{4u+jj}[m'][n] in rows
-// 4m' + jj of accumulator u.  Weights enter as bf16(128 + q); with X the
+// 4m' + jj of accumulator u.  Weights enter as bf16(128 + q) (f16(1024 + q)
+// for f16 activations, offset 1056 below); with X the
 // sub-block's activation sums (ones operand), y += d*sc*(D - 160 X).
 template <int ACT, int RP, bool XL, bool XS>
 struct Q6kRowsPolicy {
@@ -363,16 +370,20 @@ struct Q6kRowsPolicy {
         for (int u = 0; u < 4; ++u) sl.x.v[4 * q + u] = x_fetch<ACT, false>(cx, 4 * q + mq, xk(c, u, lane), used);
     }
   }
+  static constexpr bool F16 = ActTraits<ACT>::F16OP;  // f16(1024 + q) codes, f16 MFMAs
+  static constexpr bool ONEPART = ACT == DIALQ_BF16 || F16;
   static __device__ __forceinline__ void compute(const Slot &sl, Acc &acc, const Ctx &cx) {
     const int lane = threadIdx.x & 63, jj = lane & 3, mq = (lane & 15) >> 2;
-    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    constexpr uint32_t ONE = F16 ? 0x3c003c00u : 0x3f803f80u;
+    constexpr float OFF = F16 ? 1056.0f : 160.0f;  // code offset + 32
+    const u32x4 ones = {ONE, ONE, ONE, ONE};
     const u32x4 z4 = {0, 0, 0, 0};
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     const bool gmatch = ((lane >> 5) & 1) == (jj & 1);  // g/2 == jj%2
     const float d = f16_bits_to_f32(sl.t.s0 & 0xffffu);
     u32x4 wb[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) wb[t] = q6x8_to_bf16_off128(t < 4 ? sl.t.a : sl.t.b, sl.t.hdr, t);
+    for (int t = 0; t < 8; ++t) wb[t] = q6x8_off<F16>(t < 4 ? sl.t.a : sl.t.b, sl.t.hdr, t);
 #pragma unroll
     for (int q = 0; q < RP; ++q) {
       f32x4 cq[4], cs[4];
@@ -381,7 +392,7 @@ struct Q6kRowsPolicy {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         XOp<ACT> src;
-        if constexpr (XL && ACT == DIALQ_BF16) (void)src;
+        if constexpr (XL && ONEPART) (void)src;
         else if constexpr (XL) src = xraw_to_op<ACT>(x_fetch<ACT, true>(cx, 4 * q + mq, xk(sl.c, u, lane), true));
         else src = xraw_to_op<ACT>(sl.x.v[4 * q + u]);
         cq[u] = zero;
@@ -390,9 +401,9 @@ struct Q6kRowsPolicy {
         for (int v = 0; v < 2; ++v) {
           const bool on = gmatch && (v == (jj >> 1));
           XOp<ACT> av;
-          if constexpr (XL && ACT == DIALQ_BF16) {
-            // bf16 operands straight from the staged rows; lanes that feed
-            // zeros (or rows past the last) read the zero block
+          if constexpr (XL && ONEPART) {
+            // one-part operands straight from the staged rows; lanes that
+            // feed zeros (or rows past the last) read the zero block
             const lds_u8 *p = (on && row < cx.mrows) ? rowp + 64 * (2 * u + v) : cx.zero;
             av.hi = *(const u32x4 __attribute__((address_space(3))) *)p;
           } else {
@@ -418,7 +429,7 @@ struct Q6kRowsPolicy {
       for (int u = 0; u < 4; ++u)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          sum = __builtin_fmaf(sbyte_f32(sl.t.sc[u], i), __builtin_fmaf(-160.0f, cs[u][i], cq[u][i]), sum);
+          sum = __builtin_fmaf(sbyte_f32(sl.t.sc[u], i), __builtin_fmaf(-OFF, cs[u][i], cq[u][i]), sum);
       acc.v[q] = __builtin_fmaf(d, sum, acc.v[q]);
     }
   }
@@ -1205,7 +1216,11 @@ static hipError_t gemv_act(const WeightView &w, const void *x, int x_dtype, int6
                            int y_dtype, float *ws, size_t ws_bytes, int *cnt, hipStream_t st) {
   switch (x_dtype) {
     case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, st);
-    case DIALQ_F16: return gemv_dispatch<FMT, DIALQ_F16>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    // f16 activations feed f16 MFMAs as they are (f16 weight operands);
+    // MXFP4's scaled codes need bf16's exponent range (hi / lo parts)
+    case DIALQ_F16:
+      return gemv_dispatch<FMT, FMT == DIALQ_FORMAT_MXFP4 ? DIALQ_F16 : kActF16N>(w, x, M, y, y_dtype, ws, ws_bytes,
+                                                                                 cnt, st);
     case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, st);
   }
   return hipErrorInvalidValue;
