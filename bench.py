@@ -23,8 +23,9 @@ dominant kernel and the CPU baseline.
 over rotating copies) plus a 256 MiB device-to-device copy used to scale the
 HBM byte counters; `--profile-lm-head` the same for the lm_head GEMV;
 `--profile-prefill` runs only the prefill GEMMs of one
-layer per format.  They are the programs the committed rocprofv3 summaries
-run.
+layer per format, `--profile-swiglu` the fused gate_up with and without its
+SwiGLU epilogue, `--profile-select` the token selection.  They are the
+programs the committed rocprofv3 summaries run.
 """
 from __future__ import annotations
 
@@ -67,6 +68,10 @@ def parse():
                     help="run only the W8A16 lm_head GEMV (vocab 248320 x 5120) for rocprofv3")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="only the prefill GEMMs of one layer per format (for rocprofv3)")
+    ap.add_argument("--profile-swiglu", action="store_true",
+                    help="only the fused gate_up GEMV / GEMM, plain and with the SwiGLU epilogue (for rocprofv3)")
+    ap.add_argument("--profile-select", action="store_true",
+                    help="only the token selection over the 27B vocabulary (for rocprofv3)")
     return ap.parse_args()
 
 
@@ -134,12 +139,14 @@ def decode_pass(dq, lins, xs, ys, stream, shapes=LAYER_27B, swiglu=()):
         run_linear(lin, name, x, y, swiglu, rows=1, path=dq.PATH_GEMV, stream=stream)
 
 
-def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B, swiglu=()):
+def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B, swiglu=(), xdtype=None):
     """Wall time of `steps` decode passes, one HIP-graph replay per pass,
     rotating layer copies.  Linears named in `swiglu` (a fused gate_up) run
-    with the SwiGLU epilogue."""
-    xs = [torch.randn(1, k, device=dev).to(torch.bfloat16) for _, n, k in shapes]
-    ys = [torch.empty(1, out_cols(name, n, swiglu), device=dev, dtype=torch.bfloat16) for name, n, k in shapes]
+    with the SwiGLU epilogue; activations and outputs are bf16 unless
+    `xdtype` says otherwise."""
+    xdtype = xdtype or torch.bfloat16
+    xs = [torch.randn(1, k, device=dev).to(xdtype) for _, n, k in shapes]
+    ys = [torch.empty(1, out_cols(name, n, swiglu), device=dev, dtype=xdtype) for name, n, k in shapes]
     stream = torch.cuda.current_stream()
     for lins in layers:  # eager first: sizes the GEMV workspaces outside capture
         decode_pass(dq, lins, xs, ys, stream, shapes, swiglu)
@@ -209,6 +216,41 @@ def profile_run(dq, torch, dev, launches):
     torch.cuda.synchronize()
     print(f"# profile: {launches} launches of W8A16 {name} [{n}x{k}] M=1; 3 copies of 256 MiB "
           "(calibration: 268435456 bytes read and written per copy)", flush=True)
+
+
+def profile_swiglu_run(dq, torch, dev, launches=20):
+    """The 27B fused gate_up (34816 x 5120, W8A16), eager: decode (M = 1)
+    and prefill (M = 2048), plain then with the SwiGLU epilogue."""
+    n, k = 34816, 5120
+    g = torch.Generator(device=dev).manual_seed(13)
+    lins = [dq.Linear.quantize(dq.W8A16, torch.randn(n, k, device=dev, generator=g) * 0.02, scale_dtype=dq.BF16)
+            for _ in range(3)]
+    stream = torch.cuda.current_stream()
+    for m, path in ((1, dq.PATH_GEMV), (2048, dq.PATH_GEMM)):
+        x = torch.randn(m, k, device=dev).to(torch.bfloat16)
+        y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        h = torch.empty(m, n // 2, device=dev, dtype=torch.bfloat16)
+        for i in range(launches):
+            lins[i % 3].forward(x, y, path=path, stream=stream)
+        for i in range(launches):
+            lins[i % 3].forward_swiglu(x, h, path=path, stream=stream)
+        torch.cuda.synchronize()
+    print(f"# profile: W8A16 gate_up [{n}x{k}], {launches} launches each of M=1 GEMV and M=2048 GEMM, "
+          "plain then SwiGLU", flush=True)
+
+
+def profile_select_run(dq, torch, dev, calls=20):
+    """dialq_logits_select over 248320 bf16 logits: argmax, top-8, top-50 and
+    top-256 with temperature 0.8."""
+    vocab = LM_HEAD_27B[0]
+    x = (torch.randn(vocab, device=dev, generator=torch.Generator(device=dev).manual_seed(17)) * 3).to(torch.bfloat16)
+    ws = torch.empty(dq.logits_select_workspace_bytes(vocab), dtype=torch.uint8, device=dev)
+    for k, rule, t in ((1, dq.SELECT_FIRST_MAX, 0.0), (8, dq.SELECT_TOTAL_LAST_MAX, 0.8),
+                       (50, dq.SELECT_TOTAL_LAST_MAX, 0.8), (256, dq.SELECT_TOTAL_LAST_MAX, 0.8)):
+        for _ in range(calls):
+            dq.logits_select(x, k, rule=rule, temperature=t, workspace=ws)
+    torch.cuda.synchronize()
+    print(f"# profile: token selection over {vocab} bf16 logits, {calls} calls each of k = 1, 8, 50, 256", flush=True)
 
 
 def profile_lm_head_run(dq, torch, dev, launches=20):
@@ -347,6 +389,12 @@ def main():
     if a.profile_prefill:
         profile_prefill_run(dq, torch, dev)
         return
+    if a.profile_swiglu:
+        profile_swiglu_run(dq, torch, dev)
+        return
+    if a.profile_select:
+        profile_select_run(dq, torch, dev)
+        return
     fmt_of = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}
 
     # ---- headline: W8A16 decode over the 27B layer -----------------------
@@ -355,6 +403,10 @@ def main():
     lbytes = layer_bytes(dq, dq.W8A16)
     value = lbytes * a.steps / secs / 1e9
     per = time_per_linear(dq, torch, layers, dev)
+    # the same decode with f16 activations (the GGUF worker's runtime dtype)
+    fsteps16 = max(a.steps // 3, 10)
+    s16 = time_decode(dq, torch, layers, fsteps16, 10, dev, xdtype=torch.float16)
+    value_f16 = layer_bytes(dq, dq.W8A16) * fsteps16 / s16 / 1e9
     # dominant kernel: the gate GEMV (the largest linear), timed over
     # DOM_COPIES rotating copies so no launch finds its weight in the cache
     dom, dn, dk = DOM
@@ -373,7 +425,9 @@ def main():
     print(f"# w8a16 decode: {value:.1f} GB/s over the layer; per-launch us: "
           + ", ".join(f"{k}={v * 1e6:.1f}" for k, v in per.items()), file=sys.stderr, flush=True)
 
-    extra = {"decode_gbs": {"w8a16": round(value, 1)}, "decode_us_per_launch_w8a16":
+    print(f"# w8a16 decode with f16 activations: {value_f16:.1f} GB/s", file=sys.stderr, flush=True)
+    extra = {"decode_gbs": {"w8a16": round(value, 1)}, "decode_gbs_f16_activations": {"w8a16": round(value_f16, 1)},
+             "decode_us_per_launch_w8a16":
              {k: round(v * 1e6, 2) for k, v in per.items()}, "prefill_tflops": {}, "prefill_pct_mfma_peak": {}}
     sweep = [s for s in a.sweep.split(",") if s]
     if "w8a16" in sweep:
