@@ -1126,13 +1126,13 @@ static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
   if (d.w.pair) {
     // SwiGLU epilogue: one gate / up strip pair per workgroup, never split
     // (the pair's two sums meet in the workgroup's parking LDS)
+    // 8 waves: each of the pair's strips streams as a 4-wave plain workgroup
+    // would, so the rounds of workgroups over the CUs match the plain launch
     GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
-    const bool small = d.w.pair < device_cus();
     const int pitch = stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK);
-    if (mrows * pitch + 32 <= (small ? kGemvSmallStageBytes : kGemvStageBytes)) {
+    if (mrows * pitch + 32 <= kGemvSmallStageBytes) {
       p.x_pitch = pitch;
-      if (small) return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvSmallWaves>(p, st);
-      return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvWaves>(p, st);
+      return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvSmallWaves>(p, st);
     }
     return launch_ranges<FMT, PolT<A, ACT, false, false>, (U_X < kRangeRing ? U_X : kRangeRing), false, kGemvWaves>(
         p, st);
