@@ -14,17 +14,15 @@
 // pairs and two statistics cross to the host:
 //   1. k_select_slices: slice s of the vocabulary is converted to f32,
 //      penalised and turned into 64-bit keys; for k = 1 the slice keeps its
-//      largest key (a block max), otherwise chunks of C - KC keys behind the
-//      KC best so far (KC = k rounded up to a power of two) are
-//      bitonic-sorted in LDS (C = 512 for k <= 32, 1024 for k <= 64, 4096
-//      above, doubled while the slices would not fit the merge).  The
-//      slice's k best keys, descending, and the (max, sum of exp(x - max))
-//      of its temperature-scaled logits go out;
-//   2. k_select_merge: one workgroup stages the slices' sorted lists in LDS
-//      (at most 18432 keys, 144 KB), merges the statistics, and merges the
-//      lists pairwise in a tree that keeps the k best at each level (every
-//      output element placed by a merge-path binary search, all in
-//      parallel), writing indices and logits in descending order.
+//      largest key (a block max), otherwise chunks of up to 1024 / 2048 /
+//      8192 keys (k <= 32 / 64 / above) join the k best carried so far and a block radix
+//      select (block_topk) keeps the k best.  The slice's k best keys,
+//      descending, and the (max, sum of exp(x - max)) of its
+//      temperature-scaled logits go out;
+//   2. k_select_merge: one workgroup stages the slices' lists in LDS (at
+//      most 16384 keys, 128 KB), merges the statistics and radix-selects
+//      the k best of all of them (a block max for k = 1), writing indices
+//      and logits in descending order.
 //
 // Key of logit v at index i: the f32 bits mapped to an unsigned order
 // (sign set: ~u, else u | 2^31), then the index in the low word:
@@ -39,7 +37,7 @@ namespace dialq {
 
 constexpr int kSelMaxK = 256;          // largest k
 constexpr int kSelMaxSlices = 1024;    // one statistics pair per thread of the merge
-constexpr int kSelMaxKeys = 18432;     // slices x k staged by the merge: 144 KB of LDS
+constexpr int kSelMaxKeys = 16384;     // slices x k staged by the merge: 128 KB of LDS
 
 struct SelectParams {
   const void *logits;
@@ -52,7 +50,7 @@ struct SelectParams {
   int rule;
   int slices;
   int64_t slice_len;
-  int kc;               // carried keys per chunk: k rounded up to a power of two
+  int kc;               // carried keys per chunk (k)
   uint64_t *cand;       // [slices][k] keys, descending
   float *stats;         // [slices][2] (max, sum of exp(x - max)) of the scaled logits
   int k;
@@ -88,23 +86,97 @@ __device__ __forceinline__ uint32_t key_index(uint64_t key, int rule) {
   return rule == 0 ? 0xFFFFFFFFu - lo : lo;
 }
 
-// Descending bitonic sort of n (a power of two) keys in LDS by the whole
-// workgroup (nt threads).
-__device__ __forceinline__ void bitonic_desc(uint64_t *keys, int n, int nt) {
-  for (int size = 2; size <= n; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int t = threadIdx.x; t < n / 2; t += nt) {
-        const int i = 2 * t - (t & (stride - 1)), l = i + stride;
-        const uint64_t a = keys[i], b = keys[l];
-        const bool first_half_desc = (i & size) == 0;
-        if (first_half_desc ? (a < b) : (a > b)) {
-          keys[i] = b;
-          keys[l] = a;
-        }
+// LDS scratch of block_topk.
+struct TopkScratch {
+  int hist[4 * 256];        // digit counts, one table per wave % 4
+  int tot[256];
+  uint64_t sel[kSelMaxK];   // the k keys, unordered
+  uint64_t prefix, mask;
+  int need, done, count;
+};
+
+// The k largest of n distinct keys in LDS, in descending order into out[0..k)
+// (LDS; may alias keys), by the whole workgroup (NT threads).  Radix select
+// on 8-bit digits from the top: each pass counts the digit of the keys that
+// share the prefix chosen so far, and one wave finds the digit whose bucket
+// holds the k-th largest.  It stops as soon as that bucket is needed whole
+// (usually after two or three passes); then exactly k keys have their masked
+// value at or above the prefix.  They are gathered and placed by rank
+// (k <= 256: each thread counts the keys above its own).  Zero keys are
+// padding below every real key; n must hold at least k real keys.
+template <int NT>
+__device__ __forceinline__ void block_topk(const uint64_t *keys, int n, int k, uint64_t *out, TopkScratch &sc) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) {
+    sc.prefix = 0;
+    sc.mask = 0;
+    sc.need = k;
+    sc.done = 0;
+    sc.count = 0;
+  }
+  __syncthreads();
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    if (sc.done) break;  // uniform: read after a barrier
+    const uint64_t prefix = sc.prefix, mask = sc.mask;
+    for (int i = tid; i < 4 * 256; i += NT) sc.hist[i] = 0;
+    __syncthreads();
+    int *h = sc.hist + (wave & 3) * 256;
+    for (int i = tid; i < n; i += NT) {
+      const uint64_t key = keys[i];
+      if ((key & mask) == prefix) atomicAdd(&h[(key >> shift) & 255], 1);
+    }
+    __syncthreads();
+    for (int d = tid; d < 256; d += NT) sc.tot[d] = sc.hist[d] + sc.hist[256 + d] + sc.hist[512 + d] + sc.hist[768 + d];
+    __syncthreads();
+    if (wave == 0) {
+      // lane l holds digits 255 - 4l .. 252 - 4l (lane 0 the largest)
+      int c[4], sum = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = sc.tot[255 - 4 * lane - j];
+        sum += c[j];
       }
-      __syncthreads();
+      int incl = sum;
+      for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
+      }
+      const int excl = incl - sum, need = sc.need;
+      if (excl < need && need <= incl) {  // exactly one lane
+        int acc = excl, dj = 3;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (acc + c[j] >= need) {
+            dj = j;
+            break;
+          }
+          acc += c[j];
+        }
+        const int rem = need - acc;
+        sc.prefix = prefix | ((uint64_t)(255 - 4 * lane - dj) << shift);
+        sc.mask = mask | ((uint64_t)0xFF << shift);
+        sc.need = rem;
+        sc.done = c[dj] == rem;
+      }
+    }
+    __syncthreads();
+  }
+  const uint64_t prefix = sc.prefix, mask = sc.mask;
+  for (int i = tid; i < n; i += NT) {
+    const uint64_t key = keys[i];
+    if ((key & mask) >= prefix) {
+      const int slot = atomicAdd(&sc.count, 1);
+      if (slot < kSelMaxK) sc.sel[slot] = key;
     }
   }
+  __syncthreads();
+  for (int t = tid; t < k; t += NT) {
+    const uint64_t key = sc.sel[t];
+    int r = 0;
+    for (int j = 0; j < k; ++j) r += sc.sel[j] > key;
+    out[r] = key;
+  }
+  __syncthreads();
 }
 
 // Sum (or max) of one value per thread over a 256-thread workgroup.
@@ -153,11 +225,13 @@ __global__ __launch_bounds__(256) void k_select_slices(SelectParams p) {
   __shared__ float vals[C];
   __shared__ float sh[4];
   __shared__ uint64_t shk[4];
+  __shared__ TopkScratch tsc;
   const int tid = threadIdx.x;
   const int kc = p.kc, payload = C - kc;
   const int64_t lo = (int64_t)blockIdx.x * p.slice_len;
   const int64_t hi = (lo + p.slice_len < p.vocab) ? lo + p.slice_len : p.vocab;
   for (int i = tid; i < kc; i += 256) keys[i] = 0;
+  int carried = 0;  // real keys in keys[0..kc)
   float run_m = -INFINITY, run_s = 0.0f;
   const bool stats = p.temperature > 0.0f;
   for (int64_t base = lo; base < hi; base += payload) {
@@ -206,9 +280,15 @@ __global__ __launch_bounds__(256) void k_select_slices(SelectParams p) {
       __syncthreads();
       continue;
     }
-    for (int i = tid; i < payload; i += 256) keys[kc + i] = i < n ? select_key(vals[i], (uint32_t)(base + i), p.rule) : 0;
+    for (int i = tid; i < n; i += 256) keys[kc + i] = select_key(vals[i], (uint32_t)(base + i), p.rule);
     __syncthreads();
-    bitonic_desc(keys, C, 256);
+    // the k best of the carried keys and this chunk's, back to keys[0..kk);
+    // carried slots past the real keys hold zero pads
+    const int kk = p.k < carried + n ? p.k : carried + n;
+    block_topk<256>(keys, kc + n, kk, keys, tsc);
+    for (int i = kk + tid; i < kc; i += 256) keys[i] = 0;
+    carried = kk;
+    __syncthreads();
   }
   uint64_t *out = p.cand + (size_t)blockIdx.x * p.k;
   for (int i = tid; i < p.k; i += 256) out[i] = keys[i];
@@ -233,24 +313,10 @@ __device__ __forceinline__ float block_reduce1024(float v, float *sh) {
   return r;
 }
 
-// Element r (0-based) of the descending merge of two descending lists a, b of
-// k distinct keys each (merge path: i keys come from a, r - i from b).
-__device__ __forceinline__ uint64_t merge_at(const uint64_t *a, const uint64_t *b, int k, int r) {
-  int lo = r > k ? r - k : 0, hi = r < k ? r : k;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1, j = r - mid;
-    if (mid < k && j > 0 && a[mid] > b[j - 1]) lo = mid + 1;
-    else hi = mid;
-  }
-  const int i = lo, j = r - lo;
-  return (i < k && (j >= k || a[i] > b[j])) ? a[i] : b[j];
-}
-
-constexpr int kSelMergeItems = 10;  // per thread and level: (18432 / 2 + 256) / 1024 rounded up
-
 __global__ __launch_bounds__(1024) void k_select_merge(SelectParams p) {
   extern __shared__ __attribute__((aligned(16))) uint64_t lists[];  // [slices][k]
   __shared__ float sh[16];
+  __shared__ TopkScratch tsc;
   const int tid = threadIdx.x;
   const int G = p.slices, k = p.k;
   for (int i = tid; i < G * k; i += 1024) lists[i] = p.cand[i];
@@ -276,31 +342,8 @@ __global__ __launch_bounds__(1024) void k_select_merge(SelectParams p) {
     }
     return;
   }
-  // Pairwise tree merge keeping the k best: at each level list q of the next
-  // level is the top k of lists 2q and 2q+1 (an odd last list moves down
-  // unchanged); every output element is found independently by merge_at,
-  // held in registers over a barrier, then written in place.
-  for (int nl = G; nl > 1; nl = (nl + 1) >> 1) {
-    const int pairs = nl >> 1, items = ((nl + 1) >> 1) * k;
-    uint64_t v[kSelMergeItems];
-#pragma unroll
-    for (int t = 0; t < kSelMergeItems; ++t) {
-      const int it = tid + 1024 * t;
-      v[t] = 0;
-      if (it < items) {
-        const int q = it / k, r = it - q * k;
-        v[t] = q < pairs ? merge_at(lists + (size_t)(2 * q) * k, lists + (size_t)(2 * q + 1) * k, k, r)
-                         : lists[(size_t)(2 * q) * k + r];
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int t = 0; t < kSelMergeItems; ++t) {
-      const int it = tid + 1024 * t;
-      if (it < items) lists[it] = v[t];
-    }
-    __syncthreads();
-  }
+  // the k best of all slices' candidates (zero pads below every real key)
+  block_topk<1024>(lists, G * k, k, lists, tsc);
   if (tid < k) {
     p.out_idx[tid] = key_index(lists[tid], p.rule);
     p.out_val[tid] = key_logit(lists[tid]);
@@ -317,12 +360,13 @@ hipError_t launch_select(const void *logits, int dtype, int64_t vocab, const uin
                          float *out_val, float *out_stats, hipStream_t st) {
   if (k < 1 || k > kSelMaxK || vocab < k || vocab > 0xFFFFFFFFLL || ws_bytes < select_workspace_bytes(vocab))
     return hipErrorInvalidValue;
-  int kc = 1;
-  while (kc < k) kc <<= 1;
-  // slices: their k-key lists must fit the merge's LDS; chunks grow (1024, 2048, 4096 keys) until one chunk covers a slice
+  // chunk keys per slice step: a radix pass costs about the chunk (its
+  // digit counts pile onto few bins), so small k takes short chunks and
+  // many slices, large k long chunks so that slices x k fits the merge's
+  // LDS; k = 1 keeps a running max.
+  const int kc = k;
+  const int C = k <= 32 ? 1024 : (k <= 64 ? 2048 : 8192);
   const int64_t cap = kSelMaxKeys / k < kSelMaxSlices ? kSelMaxKeys / k : kSelMaxSlices;
-  int C = kc <= 32 ? 512 : (kc <= 64 ? 1024 : 4096);
-  while (C < 4096 && (vocab + (C - kc) - 1) / (C - kc) > cap) C <<= 1;
   int64_t g = (vocab + (C - kc) - 1) / (C - kc);
   if (g > cap) g = cap;
   SelectParams p;
@@ -343,10 +387,9 @@ hipError_t launch_select(const void *logits, int dtype, int64_t vocab, const uin
   p.out_idx = out_idx;
   p.out_val = out_val;
   p.out_stats = out_stats;
-  if (C == 512) k_select_slices<512><<<p.slices, 256, 0, st>>>(p);
-  else if (C == 1024) k_select_slices<1024><<<p.slices, 256, 0, st>>>(p);
+  if (C == 1024) k_select_slices<1024><<<p.slices, 256, 0, st>>>(p);
   else if (C == 2048) k_select_slices<2048><<<p.slices, 256, 0, st>>>(p);
-  else k_select_slices<4096><<<p.slices, 256, 0, st>>>(p);
+  else k_select_slices<8192><<<p.slices, 256, 0, st>>>(p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   k_select_merge<<<1, 1024, (size_t)p.slices * k * sizeof(uint64_t), st>>>(p);
