@@ -89,6 +89,23 @@ py::dict gguf_read(const std::string &path) {
   return out;
 }
 
+// Content::tensor_chunks over a file: (the concatenated bytes, [(offset, count)]).
+py::tuple gguf_tensor_chunks(const std::string &path, const std::string &name, size_t chunk) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) throw Error("cannot open " + path);
+  f.seekg(0, std::ios::end);
+  const uint64_t size = (uint64_t)f.tellg();
+  f.seekg(0);
+  const gguf::Content c = gguf::Content::read(f, size);
+  std::string all;
+  py::list pieces;
+  c.tensor_chunks(f, name, chunk, [&](const uint8_t *p, size_t off, size_t n) {
+    all.append((const char *)p, n);
+    pieces.append(py::make_tuple(off, n));
+  });
+  return py::make_tuple(py::bytes(all), pieces);
+}
+
 py::bytes gguf_tensor_bytes(const std::string &path, const std::string &name) {
   std::ifstream f(path, std::ios::binary);
   if (!f) throw Error("cannot open " + path);
@@ -214,6 +231,7 @@ PYBIND11_MODULE(dialq_host, m) {
   });
   m.def("safetensors_paths_from_index", &safetensors::paths_from_index);
   m.def("gguf_tensor_bytes", &gguf_tensor_bytes);
+  m.def("gguf_tensor_chunks", &gguf_tensor_chunks);
   m.def("worker_gguf_prefill_for_dims", &worker_gguf_prefill_for_dims);
   m.def("forward_worker_gguf", &forward_worker_gguf);
   m.def("build_worker_gguf_fp16_prefill_linear", &build_worker_gguf_fp16_prefill_linear);

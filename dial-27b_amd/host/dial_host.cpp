@@ -685,6 +685,24 @@ std::shared_ptr<GgufMatMul> GgufMatMul::from_blocks(Kind kind, const std::vector
   return r;
 }
 
+std::shared_ptr<GgufMatMul> GgufMatMul::from_device_blocks(Kind kind, const Tensor &blocks, int64_t out_dim,
+                                                           int64_t in_dim) {
+  if (!blocks.device().is_rocm()) bail("GGUF device blocks must be on a ROCm device");
+  auto r = std::make_shared<GgufMatMul>();
+  dialq_linear_desc d{(int)kind, DIALQ_F32, out_dim, in_dim, 1.0f, 0};
+  char err[512];
+  void *h = dialq_linear_create(&d, blocks.data(), blocks.nbytes(), nullptr, 0, blocks.device().ordinal, 0, nullptr,
+                                err, sizeof err);
+  if (!h) throw Error(err);
+  hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");  // the repack has read `blocks`
+  r->h_ = std::make_shared<DialqHandle>();
+  r->h_->h = h;
+  r->h_->device = blocks.device().ordinal;
+  r->out_dim_ = out_dim;
+  r->in_dim_ = in_dim;
+  return r;
+}
+
 std::shared_ptr<GgufMatMul> GgufMatMul::quantize(Kind kind, const Tensor &dense, Device device) {
   if (!device.is_rocm()) bail("GGUF QMatMul requires a ROCm device");
   auto r = std::make_shared<GgufMatMul>();
@@ -867,15 +885,21 @@ std::optional<TextLinear> load_worker_gguf_linear(std::optional<int64_t> layer_i
       bail("worker GGUF tensor %s has dtype %s; the ROCm GGUF path takes Q8_0, Q4K and Q6K", name.c_str(),
            gguf::ggml_dtype_name(info.ggml_dtype));
   }
-  std::vector<uint8_t> raw;
+  // The tensor's bytes go to the device in 8 MiB chunks, so the host never
+  // holds more than one chunk (adapter.cpp:198-227 reads the same way).
+  const size_t nbytes = (size_t)info.size_in_bytes();
+  Tensor dev_blocks = Tensor::empty(DType::U8, {(int64_t)nbytes}, src->device);
   {
     std::lock_guard<std::mutex> lk(src->file_mu);
-    raw = src->content.tensor_bytes(src->file, name);
+    DeviceScope ds(src->device);
+    src->content.tensor_chunks(src->file, name, (size_t)8 << 20, [&](const uint8_t *p, size_t off, size_t n) {
+      hip_ok(hipMemcpy((uint8_t *)dev_blocks.data() + off, p, n, hipMemcpyHostToDevice), "hipMemcpy");
+    });
   }
-  std::shared_ptr<GgufMatMul> mm = GgufMatMul::from_blocks(kind, raw, out_dim, in_dim, src->device);
+  std::shared_ptr<GgufMatMul> mm = GgufMatMul::from_device_blocks(kind, dev_blocks, out_dim, in_dim);
   warmup_worker_gguf(*mm, info.ggml_dtype, in_dim, src->device);
   g_gguf_count.fetch_add(1);
-  g_gguf_bytes.fetch_add(raw.size());
+  g_gguf_bytes.fetch_add(nbytes);
   log_info("loaded worker GGUF tensor " + name + " dtype=" + gguf::ggml_dtype_name(info.ggml_dtype));
   return TextLinear::gguf(name, mm);
 }

@@ -191,6 +191,10 @@ class GgufMatMul {
   // row), shape [out, in].
   static std::shared_ptr<GgufMatMul> from_blocks(Kind kind, const std::vector<uint8_t> &blocks, int64_t out_dim,
                                                  int64_t in_dim, Device device);
+  // The same from blocks already on the device (a U8 tensor of the raw
+  // block bytes), repacked there without a host copy.
+  static std::shared_ptr<GgufMatMul> from_device_blocks(Kind kind, const Tensor &blocks, int64_t out_dim,
+                                                        int64_t in_dim);
   // QTensor::quantize of a dense [out, in] tensor (host or device).
   static std::shared_ptr<GgufMatMul> quantize(Kind kind, const Tensor &dense, Device device);
   Tensor forward(const Tensor &x) const;  // output dtype = input dtype

@@ -329,6 +329,30 @@ std::vector<uint8_t> Content::tensor_bytes(std::istream &in, const std::string &
   return out;
 }
 
+size_t Content::tensor_chunks(std::istream &in, const std::string &name, size_t chunk,
+                              const std::function<void(const uint8_t *, size_t, size_t)> &sink) const {
+  auto it = tensor_infos.find(name);
+  if (it == tensor_infos.end()) fail("cannot find tensor info for " + name);
+  if (chunk == 0) fail("chunk size must be positive");
+  const TensorInfo &ti = it->second;
+  const uint64_t n = (uint64_t)ti.size_in_bytes();
+  if (ti.offset > file_size || tensor_data_offset > file_size - ti.offset || n > file_size - tensor_data_offset - ti.offset)
+    fail("truncated GGUF tensor " + name + ": " + std::to_string(n) + " bytes at offset " +
+         std::to_string(tensor_data_offset + ti.offset) + " of a " + std::to_string(file_size) + "-byte file");
+  in.clear();
+  in.seekg((std::streamoff)(tensor_data_offset + ti.offset));
+  std::vector<uint8_t> buf((size_t)(n < chunk ? n : chunk));
+  for (uint64_t off = 0; off < n;) {
+    const size_t count = (size_t)((n - off) < chunk ? (n - off) : chunk);
+    if (!in || !in.read((char *)buf.data(), (std::streamsize)count))
+      fail("truncated GGUF tensor " + name + ": " + std::to_string(n) + " bytes at offset " +
+           std::to_string(tensor_data_offset + ti.offset));
+    sink(buf.data(), (size_t)off, count);
+    off += count;
+  }
+  return (size_t)n;
+}
+
 const Value *Content::get(const std::string &key) const {
   auto it = metadata.find(key);
   return it == metadata.end() ? nullptr : &it->second;

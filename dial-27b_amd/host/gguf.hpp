@@ -21,6 +21,7 @@
 #pragma once
 
 #include <cstdint>
+#include <functional>
 #include <istream>
 #include <map>
 #include <string>
@@ -106,6 +107,12 @@ struct Content {
   static Content read(std::istream &in, uint64_t file_size);
   // The raw bytes of tensor `name` (the range Content::tensor reads).
   std::vector<uint8_t> tensor_bytes(std::istream &in, const std::string &name) const;
+  // The same bytes in chunks of at most `chunk` bytes, each handed to
+  // sink(data, offset, count) in order: the host holds one chunk at a time
+  // (the reference's GGML adapter streams assigned tensors in 8 MiB chunks,
+  // backends/qwen38_ggml/adapter.cpp:198-227).  Returns the tensor's size.
+  size_t tensor_chunks(std::istream &in, const std::string &name, size_t chunk,
+                       const std::function<void(const uint8_t *, size_t, size_t)> &sink) const;
   const Value *get(const std::string &key) const;
 };
 

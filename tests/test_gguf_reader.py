@@ -77,6 +77,22 @@ def test_reads_header_metadata_and_tensor_infos(tmp_path, version):
         assert ti[name][2] % 32 == 0 and blob[off:off + len(raw)] == raw
 
 
+def test_tensor_chunks_stream_the_same_bytes(tmp_path):
+    """Content::tensor_chunks (the loader's bounded-memory path) hands the
+    tensor over in order, each piece at most the chunk size."""
+    p = tmp_path / "c.gguf"
+    meta, tensors, start = _tiny(p)
+    for name, ggml, dims, raw in tensors:
+        for chunk in (1, 100, 4096, 1 << 23):
+            got, pieces = H.gguf_tensor_chunks(str(p), name, chunk)
+            assert got == raw
+            assert all(n <= chunk for _, n in pieces)
+            assert [o for o, _ in pieces] == list(range(0, len(raw), chunk))
+    _tiny(p, tensors=[("x.weight", "Q8_0", [2, 32], bytes(68))], truncate=10)
+    with pytest.raises(H.DialError, match="truncated GGUF tensor x.weight"):
+        H.gguf_tensor_chunks(str(p), "x.weight", 16)
+
+
 def test_alignment_and_nul_terminated_strings(tmp_path):
     p = tmp_path / "a.gguf"
     meta, tensors, start = _tiny(p, alignment=256, nul=True)
