@@ -6,9 +6,11 @@
 //   The N x K weight is cut into 16-row strips and CHUNK-wide k chunks.
 //   Tile (strip s, chunk c) is TILE bytes, contiguous, tiles ordered
 //   strip-major: tiles[(s * k_chunks + c) * TILE].  Inside a tile, lane l of
-//   a 64-wide wavefront owns row r = l % 16 and k-group g = l / 16, and its
-//   bytes sit at offset l * LANE_BYTES, so one wave reads a tile with one
-//   fully coalesced 16-byte (or 32-byte) load per lane.  That lane -> (row,
+//   a 64-wide wavefront owns row r = l % 16 and k-group g = l / 16.  Its
+//   bytes sit in 1 KB planes: byte j of lane l at (j / 16) * 1024 + 16 l +
+//   j % 16 (tile_byte), so each 16-byte load instruction of a wave reads one
+//   contiguous KB (a 32-byte lane at offset 32 l would spread each
+//   instruction over 2 KB: 24 % slower FP8_BLOCK decode).  That lane -> (row,
 //   k-group) map is the operand layout of v_mfma_*_16x16x32 (bf16/f16, B
 //   operand) and of v_mfma_scale_f32_16x16x128_f8f6f4, so tiles go straight
 //   from HBM into MFMA registers without an LDS round trip.
@@ -17,10 +19,10 @@
 //     W8A16, FP8_ROW  CHUNK 64,  16 B: k = 16g + j                 (j < 16)
 //     Q8_0            CHUNK 64,  16 B: bytes 0-7 : block 0, k = 8g + j
 //                                       bytes 8-15: block 1, k = 32 + 8g + j
-//     FP8_BLOCK       CHUNK 128, 32 B: k = 32g + j                 (j < 32)
+//     FP8_BLOCK       CHUNK 128, 32 B (two planes): k = 32g + j  (j < 32)
 //     NVFP4, MXFP4    CHUNK 128, 16 B: k = 32g + j, two codes per byte,
 //                                       low nibble first (raw byte order)
-//     Q4_K            CHUNK 256, 32 B: bytes 8i..8i+7 = qs[32i + 8g + j]
+//     Q4_K            CHUNK 256, 32 B (two planes): bytes 8i..8i+7 = qs[32i + 8g + j]
 //                                       (i < 4): low nibbles are sub-block 2i,
 //                                       high nibbles sub-block 2i+1
 //     Q6_K            CHUNK 256, 48 B in three 1 KB planes (plane p holds
@@ -88,6 +90,9 @@ __host__ __device__ inline FormatGeom format_geom(int fmt) {
       return {0, 0, 0, 0, 0};
   }
 }
+
+// Offset of byte j of lane l inside a tile (the plane layout above).
+__host__ __device__ inline int tile_byte(int lane, int j) { return (j >> 4) * 1024 + lane * 16 + (j & 15); }
 
 // ---- scalar conversions (device) ------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {

@@ -71,10 +71,10 @@ __device__ __forceinline__ RawTile gemm_tile(const WeightView &w, rsrc_t rt, rsr
     t.s0 = bload2(ra, valid ? tidx * 288 + 256 + r * 2 : kOOB);
     return t;
   }
-  const uint32_t off = valid ? tidx * (64 * T::LANE) + lane * T::LANE : kOOB;
+  const uint32_t off = valid ? tidx * (64 * T::LANE) + lane * 16 : kOOB;  // plane 0
   t.a = bload16(rt, off);
   t.b = (u32x4){0, 0, 0, 0};
-  if constexpr (T::LANE == 32) t.b = bload16(rt, valid ? off + 16 : kOOB);
+  if constexpr (T::LANE == 32) t.b = bload16(rt, valid ? off + 1024 : kOOB);  // plane 1
   if constexpr (FMT == DIALQ_FORMAT_Q8_0) t.s0 = bload4(ra, valid ? tidx * 64 + r * 4 : kOOB);
   else if constexpr (FMT == DIALQ_FORMAT_Q4_K) t.hdr = bload16(ra, valid ? tidx * 256 + r * 16 : kOOB);
   else if constexpr (FMT == DIALQ_FORMAT_NVFP4) t.s0 = bload2(ra, valid ? tidx * 128 + r * 8 + 2 * g : kOOB);
@@ -784,8 +784,9 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
     auto bload = [&](int c, int j, int q, int i) -> u32x4 {
       const int strip = s0 + 2 * q + sub;
       const bool valid = c < c1 && strip < slim;
+      // slot 16(2j + h) + r; its 16-byte half i lives in plane i
       const uint32_t off = valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * TILE +
-                                       (uint32_t)(((2 * j + h) * 16 + r) * (16 * BW) + 16 * i)
+                                       (uint32_t)(1024 * i + ((2 * j + h) * 16 + r) * 16)
                                  : kOOB;
       return bload16(rt, off);
     };

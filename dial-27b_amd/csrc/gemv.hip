@@ -130,10 +130,10 @@ __device__ __forceinline__ void tile_fill(RawTile &t, const WeightView &w, const
     t.s0 = sload2(cx.ra, valid ? tidx * 288 + 256 + r * 2 : kOOB);
     return;
   }
-  const uint32_t off = valid ? tidx * (64 * T::LANE) + lane * T::LANE : kOOB;
+  const uint32_t off = valid ? tidx * (64 * T::LANE) + lane * 16 : kOOB;  // plane 0
   t.a = sload16(cx.rt, off);
   t.b = (u32x4){0, 0, 0, 0};
-  if constexpr (T::LANE == 32) t.b = sload16(cx.rt, valid ? off + 16 : kOOB);
+  if constexpr (T::LANE == 32) t.b = sload16(cx.rt, valid ? off + 1024 : kOOB);  // plane 1
   if constexpr (FMT == DIALQ_FORMAT_Q8_0) t.s0 = sload4(cx.ra, valid ? tidx * 64 + r * 4 : kOOB);
   else if constexpr (FMT == DIALQ_FORMAT_Q4_K) t.hdr = sload16(cx.ra, valid ? tidx * 256 + r * 16 : kOOB);
   else if constexpr (FMT == DIALQ_FORMAT_NVFP4) t.s0 = sload2(cx.ra, valid ? tidx * 128 + r * 8 + 2 * g : kOOB);

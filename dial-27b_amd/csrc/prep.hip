@@ -305,7 +305,8 @@ __device__ __forceinline__ int64_t raw_index_tile(const RepackGeom &g, int64_t i
   int b = (int)(i % g.tile_bytes);
   int64_t s = t / g.k_chunks, c = t % g.k_chunks;
   if (g.fmt == DIALQ_FORMAT_Q6_K) return raw_index_q6k_tile(g, s, c, b);
-  int lane = b / g.lane_bytes, j = b % g.lane_bytes;
+  // inverse of tile_byte: plane b / 1024, lane (b / 16) % 64
+  int lane = (b >> 4) & 63, j = (b >> 10) * 16 + (b & 15);
   int r = lane & 15, kg = lane >> 4;
   int64_t n = s * 16 + r;
   if (n >= g.N) return -1;
@@ -460,7 +461,7 @@ __global__ void k_dequant(DequantArgs a) {
       }
       case DIALQ_FORMAT_FP8_BLOCK: {
         int kg = kk / 32, j = kk % 32;
-        v = e4m3_to_f32(tile[(kg * 16 + r) * 32 + j]) * a.block_scale[(n / 128) * a.nbk + k / 128];
+        v = e4m3_to_f32(tile[tile_byte(kg * 16 + r, j)]) * a.block_scale[(n / 128) * a.nbk + k / 128];
         break;
       }
       case DIALQ_FORMAT_Q8_0: {
@@ -487,7 +488,7 @@ __global__ void k_dequant(DequantArgs a) {
       case DIALQ_FORMAT_Q4_K: {
         int sub = kk / 32, val = kk % 32;  // sub-block, value within it
         int i4 = sub / 2, hi = sub & 1, kg = val / 8, j = val % 8;
-        uint8_t byte = tile[(kg * 16 + r) * 32 + i4 * 8 + j];
+        uint8_t byte = tile[tile_byte(kg * 16 + r, i4 * 8 + j)];
         uint32_t q = hi ? (byte >> 4) : (byte & 15u);
         const uint8_t *hdr = a.aux + (s * a.k_chunks + c) * 256 + r * 16;
         float d = f16_bits_to_f32((uint32_t)hdr[0] | ((uint32_t)hdr[1] << 8));

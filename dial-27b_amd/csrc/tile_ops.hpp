@@ -432,11 +432,11 @@ struct RawTile {
 template <int FMT>
 __device__ __forceinline__ RawTile load_tile(const uint8_t *tiles, int64_t tile_idx, int lane) {
   constexpr int LANE = FmtTraits<FMT>::LANE;
-  const uint8_t *p = tiles + tile_idx * (64 * LANE) + lane * LANE;
+  const uint8_t *p = tiles + tile_idx * (64 * LANE) + lane * 16;  // plane 0 (and plane 1 at +1 KB)
   RawTile r;
   r.a = __builtin_nontemporal_load((const u32x4 *)p);
   if constexpr (LANE == 32)
-    r.b = __builtin_nontemporal_load((const u32x4 *)(p + 16));
+    r.b = __builtin_nontemporal_load((const u32x4 *)(p + 1024));
   else
     r.b = (u32x4){0, 0, 0, 0};
   return r;
