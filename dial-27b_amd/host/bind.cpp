@@ -236,6 +236,25 @@ PYBIND11_MODULE(dialq_host, m) {
   m.def("forward_worker_gguf", &forward_worker_gguf);
   m.def("build_worker_gguf_fp16_prefill_linear", &build_worker_gguf_fp16_prefill_linear);
   m.def("last_warning", &last_warning);
+  py::class_<OutputHeadConfig>(m, "OutputHeadConfig")
+      .def(py::init([](int64_t hidden_size, int64_t vocab_size, int64_t num_hidden_layers, double rms_norm_eps) {
+             return OutputHeadConfig{hidden_size, vocab_size, num_hidden_layers, rms_norm_eps};
+           }),
+           py::arg("hidden_size"), py::arg("vocab_size"), py::arg("num_hidden_layers"), py::arg("rms_norm_eps") = 1e-6);
+  m.def("load_worker_gguf_output_head", &load_worker_gguf_output_head, py::arg("cfg"), py::arg("owns_final_layer"));
+  m.def("worker_gguf_output_head_enabled", &worker_gguf_output_head_enabled);
+  m.def("worker_gguf_sample_token_enabled", &worker_gguf_sample_token_enabled);
+  // None, a logits Tensor, or the sampled token as an int.
+  m.def(
+      "maybe_forward_worker_gguf_output_head",
+      [](const Tensor &x, std::optional<int64_t> final_request_block_idx,
+         std::optional<SamplingRequest> sampling) -> py::object {
+        auto r = maybe_forward_worker_gguf_output_head(x, final_request_block_idx, sampling ? &*sampling : nullptr);
+        if (!r) return py::none();
+        if (r->token) return py::int_(*r->token);
+        return py::cast(*r->logits);
+      },
+      py::arg("x"), py::arg("final_request_block_idx"), py::arg("sampling") = py::none());
 
   py::class_<SamplingRequest>(m, "SamplingRequest")
       .def(py::init([](uint64_t seed, uint64_t sample_index, double temperature, std::optional<uint64_t> top_k,

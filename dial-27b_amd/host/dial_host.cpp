@@ -16,6 +16,7 @@
 
 #include "dialq.h"
 #include "gguf.hpp"
+#include "sampling.hpp"
 
 namespace dial {
 
@@ -76,6 +77,23 @@ float f16_to_f32(uint16_t h) {
   float f;
   std::memcpy(&f, &bits, 4);
   return f;
+}
+// f32 -> f16, round to nearest even (overflow to inf, NaN kept quiet).
+uint16_t f32_to_f16_rne(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // >= 65520 rounds to inf
+  if (ax < 0x38800000u) {  // below 2^-14: subnormal steps of 2^-24
+    float v;
+    std::memcpy(&v, &ax, 4);
+    return (uint16_t)(sign | (uint32_t)std::nearbyint(v * 16777216.0f));
+  }
+  uint32_t r = ((((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13));
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+  return (uint16_t)(sign | r);
 }
 float bf16_to_f32(uint16_t h) {
   const uint32_t bits = (uint32_t)h << 16;
@@ -860,6 +878,31 @@ std::optional<std::tuple<size_t, size_t, size_t, size_t>> worker_gguf_summary() 
                          g_gguf_prefill_bytes.load());
 }
 
+// Streams a GGUF tensor to the device in 8 MiB chunks (the host holds one
+// chunk, as adapter.cpp:198-227 reads) and repacks it as a quantized matmul.
+std::shared_ptr<GgufMatMul> upload_gguf_matmul(WorkerGgufSource &src, const std::string &name,
+                                               const gguf::TensorInfo &info, int64_t out_dim, int64_t in_dim) {
+  GgufMatMul::Kind kind;
+  switch (info.ggml_dtype) {
+    case gguf::GgmlDType::Q8_0: kind = GgufMatMul::Q8_0; break;
+    case gguf::GgmlDType::Q4K: kind = GgufMatMul::Q4_K; break;
+    case gguf::GgmlDType::Q6K: kind = GgufMatMul::Q6_K; break;
+    default:
+      bail("worker GGUF tensor %s has dtype %s; the ROCm GGUF path takes Q8_0, Q4K and Q6K", name.c_str(),
+           gguf::ggml_dtype_name(info.ggml_dtype));
+  }
+  const size_t nbytes = (size_t)info.size_in_bytes();
+  Tensor dev_blocks = Tensor::empty(DType::U8, {(int64_t)nbytes}, src.device);
+  {
+    std::lock_guard<std::mutex> lk(src.file_mu);
+    DeviceScope ds(src.device);
+    src.content.tensor_chunks(src.file, name, (size_t)8 << 20, [&](const uint8_t *p, size_t off, size_t n) {
+      hip_ok(hipMemcpy((uint8_t *)dev_blocks.data() + off, p, n, hipMemcpyHostToDevice), "hipMemcpy");
+    });
+  }
+  return GgufMatMul::from_device_blocks(kind, dev_blocks, out_dim, in_dim);
+}
+
 std::optional<TextLinear> load_worker_gguf_linear(std::optional<int64_t> layer_idx, const std::string &tensor_suffix,
                                                   int64_t in_dim, int64_t out_dim) {
   std::shared_ptr<WorkerGgufSource> src = gguf_source();
@@ -876,32 +919,209 @@ std::optional<TextLinear> load_worker_gguf_linear(std::optional<int64_t> layer_i
     bail("worker GGUF tensor %s shape %s], expected [%lld, %lld]", name.c_str(), d.c_str(), (long long)out_dim,
          (long long)in_dim);
   }
-  GgufMatMul::Kind kind;
-  switch (info.ggml_dtype) {
-    case gguf::GgmlDType::Q8_0: kind = GgufMatMul::Q8_0; break;
-    case gguf::GgmlDType::Q4K: kind = GgufMatMul::Q4_K; break;
-    case gguf::GgmlDType::Q6K: kind = GgufMatMul::Q6_K; break;
-    default:
-      bail("worker GGUF tensor %s has dtype %s; the ROCm GGUF path takes Q8_0, Q4K and Q6K", name.c_str(),
-           gguf::ggml_dtype_name(info.ggml_dtype));
-  }
-  // The tensor's bytes go to the device in 8 MiB chunks, so the host never
-  // holds more than one chunk (adapter.cpp:198-227 reads the same way).
-  const size_t nbytes = (size_t)info.size_in_bytes();
-  Tensor dev_blocks = Tensor::empty(DType::U8, {(int64_t)nbytes}, src->device);
-  {
-    std::lock_guard<std::mutex> lk(src->file_mu);
-    DeviceScope ds(src->device);
-    src->content.tensor_chunks(src->file, name, (size_t)8 << 20, [&](const uint8_t *p, size_t off, size_t n) {
-      hip_ok(hipMemcpy((uint8_t *)dev_blocks.data() + off, p, n, hipMemcpyHostToDevice), "hipMemcpy");
-    });
-  }
-  std::shared_ptr<GgufMatMul> mm = GgufMatMul::from_device_blocks(kind, dev_blocks, out_dim, in_dim);
+  std::shared_ptr<GgufMatMul> mm = upload_gguf_matmul(*src, name, info, out_dim, in_dim);
   warmup_worker_gguf(*mm, info.ggml_dtype, in_dim, src->device);
   g_gguf_count.fetch_add(1);
-  g_gguf_bytes.fetch_add(nbytes);
+  g_gguf_bytes.fetch_add((size_t)info.size_in_bytes());
   log_info("loaded worker GGUF tensor " + name + " dtype=" + gguf::ggml_dtype_name(info.ggml_dtype));
   return TextLinear::gguf(name, mm);
+}
+
+// ---- worker GGUF output head (worker_gguf.rs:197-383) -------------------------
+namespace {
+struct OutputHead {
+  std::vector<float> norm;  // output_norm.weight, F16 values (gguf_tensor_to_f16)
+  double eps = 1e-6;
+  std::shared_ptr<GgufMatMul> output;
+  int64_t final_block_idx = 0;
+  Device device;
+};
+std::shared_mutex g_head_mu;
+std::shared_ptr<OutputHead> g_head;
+std::atomic<bool> g_head_route_logged{false};
+
+std::shared_ptr<OutputHead> output_head() {
+  std::shared_lock<std::shared_mutex> lk(g_head_mu);
+  return g_head;
+}
+
+bool warmup_disabled() {
+  const char *e = getenv("DIAL_WORKER_GGUF_WARMUP");
+  if (!e) return false;
+  const std::string v = e;
+  return v == "0" || v == "false" || v == "FALSE" || v == "no" || v == "NO";
+}
+
+// forward_output_head (:333-345): the last position of [1, seq, hidden] (or
+// the [1, hidden] row), candle_nn::RmsNorm -- f32 sum of squares, x * rsqrt(
+// mean + eps) * w, rounded to the activation dtype -- then the lm_head.  The
+// one hidden row is normalised on the host (a few KB each way per token).
+Tensor forward_output_head(const OutputHead &head, const Tensor &x) {
+  const std::vector<int64_t> &d = x.dims();
+  int64_t row_off;
+  if (d.size() == 3 && d[0] == 1 && d[1] > 0) row_off = (d[1] - 1) * d[2];
+  else if (d.size() == 2 && d[0] == 1) row_off = 0;
+  else bail("worker GGUF output head expects [1, seq, hidden] or [1, hidden], got %s", x.dims_debug().c_str());
+  const int64_t hidden = d.back();
+  if (hidden != (int64_t)head.norm.size())
+    bail("worker GGUF output head: hidden size %lld, output_norm.weight has %lld", (long long)hidden,
+         (long long)head.norm.size());
+  if (x.dtype() != DType::F16 && x.dtype() != DType::BF16 && x.dtype() != DType::F32)
+    bail("worker GGUF output head: unsupported activation dtype %s", dtype_name(x.dtype()));
+  const size_t es = dtype_size(x.dtype());
+  std::vector<uint8_t> row((size_t)hidden * es);
+  const uint8_t *src = (const uint8_t *)x.data() + (size_t)row_off * es;
+  if (x.device().is_rocm()) {
+    DeviceScope ds(x.device());
+    hip_ok(hipMemcpy(row.data(), src, row.size(), hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  } else {
+    std::memcpy(row.data(), src, row.size());
+  }
+  std::vector<float> v((size_t)hidden);
+  for (int64_t i = 0; i < hidden; ++i) {
+    uint16_t h;
+    switch (x.dtype()) {
+      case DType::F32: std::memcpy(&v[i], row.data() + 4 * i, 4); break;
+      case DType::F16: std::memcpy(&h, row.data() + 2 * i, 2); v[i] = f16_to_f32(h); break;
+      default: std::memcpy(&h, row.data() + 2 * i, 2); v[i] = bf16_to_f32(h); break;
+    }
+  }
+  float ss = 0.0f;
+  for (float a : v) ss += a * a;
+  const float scale = 1.0f / std::sqrt(ss / (float)hidden + (float)head.eps);
+  for (int64_t i = 0; i < hidden; ++i) {
+    const float y = v[i] * scale * head.norm[i];
+    switch (x.dtype()) {
+      case DType::F32: std::memcpy(row.data() + 4 * i, &y, 4); break;
+      case DType::F16: { const uint16_t h = f32_to_f16_rne(y); std::memcpy(row.data() + 2 * i, &h, 2); break; }
+      default: {
+        uint32_t b;
+        std::memcpy(&b, &y, 4);
+        const uint16_t h = std::isnan(y) ? (uint16_t)0x7fc0u : (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+        std::memcpy(row.data() + 2 * i, &h, 2);
+        break;
+      }
+    }
+  }
+  Tensor normalized = Tensor::from_host(row.data(), x.dtype(), {1, hidden}).to_device(head.device);
+  return forward_worker_gguf(*head.output, normalized);
+}
+}  // namespace
+
+void load_worker_gguf_output_head(const OutputHeadConfig &cfg, bool owns_final_layer) {
+  {
+    std::unique_lock<std::shared_mutex> lk(g_head_mu);
+    g_head.reset();
+  }
+  if (!worker_gguf_output_head_requested()) return;
+  if (!owns_final_layer) {
+    log_info("worker GGUF output head not loaded: this Worker does not own the final layer");
+    return;
+  }
+  std::shared_ptr<WorkerGgufSource> src = gguf_source();
+  if (!src) bail("worker GGUF source is not configured");
+  const auto dims_str = [](const std::vector<int64_t> &dims) {
+    std::string s = "[";
+    for (size_t i = 0; i < dims.size(); ++i) s += (i ? ", " : "") + std::to_string(dims[i]);
+    return s + "]";
+  };
+  const std::string norm_name = "output_norm.weight";
+  auto ni = src->content.tensor_infos.find(norm_name);
+  if (ni == src->content.tensor_infos.end())
+    bail("worker GGUF %s has no tensor %s", src->path.c_str(), norm_name.c_str());
+  if (ni->second.dims != std::vector<int64_t>{cfg.hidden_size})
+    bail("worker GGUF tensor %s shape %s, expected [%lld]", norm_name.c_str(), dims_str(ni->second.dims).c_str(),
+         (long long)cfg.hidden_size);
+  std::string output_name;
+  if (src->content.tensor_infos.count("output.weight")) {
+    output_name = "output.weight";
+  } else if (src->content.tensor_infos.count("token_embd.weight")) {
+    log_info("worker GGUF output.weight missing; using tied token_embd.weight");
+    output_name = "token_embd.weight";
+  } else {
+    bail("worker GGUF %s has neither output.weight nor token_embd.weight", src->path.c_str());
+  }
+  const gguf::TensorInfo &oi = src->content.tensor_infos.at(output_name);
+  if (oi.dims != std::vector<int64_t>{cfg.vocab_size, cfg.hidden_size})
+    bail("worker GGUF tensor %s shape %s, expected [%lld, %lld]", output_name.c_str(), dims_str(oi.dims).c_str(),
+         (long long)cfg.vocab_size, (long long)cfg.hidden_size);
+
+  auto head = std::make_shared<OutputHead>();
+  const gguf::GgmlDType norm_dtype = ni->second.ggml_dtype;
+  std::vector<uint8_t> nb;
+  {
+    std::lock_guard<std::mutex> lk(src->file_mu);
+    nb = src->content.tensor_bytes(src->file, norm_name);
+  }
+  head->norm.resize((size_t)cfg.hidden_size);
+  for (int64_t i = 0; i < cfg.hidden_size; ++i) {
+    float f;
+    uint16_t h;
+    switch (norm_dtype) {
+      case gguf::GgmlDType::F32: std::memcpy(&f, nb.data() + 4 * i, 4); break;
+      case gguf::GgmlDType::F16: std::memcpy(&h, nb.data() + 2 * i, 2); f = f16_to_f32(h); break;
+      case gguf::GgmlDType::BF16: std::memcpy(&h, nb.data() + 2 * i, 2); f = bf16_to_f32(h); break;
+      default:
+        bail("worker GGUF tensor %s has dtype %s; expected F32, F16 or BF16", norm_name.c_str(),
+             gguf::ggml_dtype_name(norm_dtype));
+    }
+    head->norm[i] = f16_to_f32(f32_to_f16_rne(f));
+  }
+  head->eps = cfg.rms_norm_eps;
+  head->output = upload_gguf_matmul(*src, output_name, oi, cfg.vocab_size, cfg.hidden_size);
+  head->final_block_idx = cfg.num_hidden_layers > 0 ? cfg.num_hidden_layers - 1 : 0;
+  head->device = src->device;
+  warmup_worker_gguf(*head->output, oi.ggml_dtype, cfg.hidden_size, src->device);
+  if (!warmup_disabled()) {
+    std::vector<uint16_t> z((size_t)cfg.hidden_size, 0);
+    Tensor hidden = Tensor::from_host(z.data(), DType::F16, {1, 1, cfg.hidden_size}).to_device(src->device);
+    (void)forward_output_head(*head, hidden);
+    DeviceScope ds(src->device);
+    hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    log_info("worker GGUF output head warmup complete");
+  }
+  {
+    std::unique_lock<std::shared_mutex> lk(g_head_mu);
+    g_head = head;
+  }
+  char msg[512];
+  snprintf(msg, sizeof msg,
+           "worker GGUF output head loaded: norm=%s norm_dtype=%s output=%s dtype=%s shape=[%lld, %lld] "
+           "quantized_memory=%.1f MiB return_dtype=F16",
+           norm_name.c_str(), gguf::ggml_dtype_name(norm_dtype), output_name.c_str(),
+           gguf::ggml_dtype_name(oi.ggml_dtype), (long long)cfg.vocab_size, (long long)cfg.hidden_size,
+           (double)oi.size_in_bytes() / 1048576.0);
+  log_info(msg);
+}
+
+bool worker_gguf_output_head_enabled() { return (bool)output_head(); }
+bool worker_gguf_sample_token_enabled() { return worker_gguf_output_head_enabled() && g_gguf_sample_token.load(); }
+
+std::optional<OutputHeadResult> maybe_forward_worker_gguf_output_head(const Tensor &x,
+                                                                      std::optional<int64_t> final_request_block_idx,
+                                                                      const SamplingRequest *sampling) {
+  std::shared_ptr<OutputHead> head = output_head();
+  if (!head) return std::nullopt;
+  if (final_request_block_idx != head->final_block_idx) return std::nullopt;
+  OutputHeadResult r;
+  Tensor logits = forward_output_head(*head, x);
+  if (!g_head_route_logged.exchange(true))
+    log_info("worker GGUF output-head route selected: final_block=" + std::to_string(head->final_block_idx) +
+             " hidden_shape=" + x.dims_debug() + " logits_shape=" + logits.dims_debug() +
+             " logits_dtype=" + dtype_name(logits.dtype()));
+  if (worker_gguf_sample_token_enabled()) {
+    if (!sampling)
+      bail("GGUF remote sampling is enabled but the Master did not send sampling parameters; rebuild and restart "
+           "both endpoints");
+    try {
+      r.token = sample_remote_logits(logits, *sampling);
+    } catch (const Error &e) {
+      bail("remote sampling failed: %s", e.what());
+    }
+    return r;
+  }
+  r.logits = std::move(logits);
+  return r;
 }
 
 // worker_gguf_prefill_for_dims (worker_gguf.rs:399-406): dims [.., seq, hidden]

@@ -255,4 +255,30 @@ Tensor forward_worker_gguf(const GgufMatMul &matmul, const Tensor &x);
 // gate_up), as one dense linear.
 Linear build_worker_gguf_fp16_prefill_linear(const std::string &name, const std::vector<TextLinear> &sources);
 
+// ---- worker GGUF output head (worker_gguf.rs:197-383) ------------------------
+struct SamplingRequest;  // sampling.hpp
+struct OutputHeadConfig {
+  int64_t hidden_size = 0, vocab_size = 0, num_hidden_layers = 0;
+  double rms_norm_eps = 1e-6;
+};
+// load_worker_gguf_output_head (worker_gguf.rs:197-310): when the head was
+// requested and this worker owns the final layer, loads output_norm.weight
+// (as F16, candle's gguf_tensor_to_f16) and output.weight -- or the tied
+// token_embd.weight -- as a quantized lm_head (Q8_0 / Q4K / Q6K, streamed to
+// the device in chunks), with the reference's shape checks and messages.
+void load_worker_gguf_output_head(const OutputHeadConfig &cfg, bool owns_final_layer);
+bool worker_gguf_output_head_enabled();
+bool worker_gguf_sample_token_enabled();
+// maybe_forward_worker_gguf_output_head (:342-383): nullopt without a head
+// or for another block; else the last position's RMS-normalised hidden
+// state times the lm_head -- F16 logits [1, vocab] -- or, with
+// --worker-gguf-sample-token, the token sample_remote_logits draws.
+struct OutputHeadResult {
+  std::optional<Tensor> logits;
+  std::optional<uint32_t> token;
+};
+std::optional<OutputHeadResult> maybe_forward_worker_gguf_output_head(const Tensor &x,
+                                                                      std::optional<int64_t> final_request_block_idx,
+                                                                      const SamplingRequest *sampling);
+
 }  // namespace dial

@@ -288,6 +288,17 @@ def matmul_f64(x, w):
     return y
 
 
+def rms_norm(x, w, eps):
+    """candle_nn::RmsNorm as the GGUF output head applies it
+    (qwen3_vl/worker_gguf.rs:267-268, 341): x * w / sqrt(mean(x^2) + eps)
+    over the last axis, in float64.  Pinned against the closed form for a
+    constant row and against torch.nn.functional.rms_norm
+    (tests/test_oracle_formats.py)."""
+    x = np.asarray(x, np.float64)
+    ms = np.mean(x * x, axis=-1, keepdims=True)
+    return x / np.sqrt(ms + eps) * np.asarray(w, np.float64)
+
+
 def swiglu(gate_up):
     """Mlp::mlp_mid_from_gate_up (qwen3_vl/text.rs:816-820): the fused gate_up
     output's first half is the gate, its second half the up projection;

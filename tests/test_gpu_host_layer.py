@@ -273,3 +273,68 @@ def test_linear_no_bias_from_safetensors_checkpoint(tmp_path, torch_dev):
         assert np.abs(got - want).max() <= 2e-3 * np.abs(want).max()
     finally:
         H.configure_quant_linear(H.Qwen38QuantLinear.Dense, ROCM, H.DType.F16)
+
+
+def _head_ref(O, x_last, w16, deq, eps):
+    # candle_nn::RmsNorm in f32 rounded to F16, then the quantized lm_head
+    normed = O.round_f16(O.rms_norm(x_last.astype(np.float64), w16, eps).astype(np.float32))
+    return O.matmul_f64(normed, deq)
+
+
+def test_worker_gguf_output_head_matches_oracle(tmp_path, torch_dev):
+    # worker_gguf.rs:754-787 (output_head_uses_last_hidden_and_quantized_
+    # projection: Q4_K (2, 256) of (((i + 17) % 37) - 18) / 19, unit F16
+    # norm, input (1, 3, 256) of ((i % 31) - 15) / 16, final block 35) read
+    # from a GGUF file, then a tied token_embd.weight head with a learned norm
+    # whose sampled-token route (:366-381) returns the argmax at temperature 0
+    import oracle as O
+    from gguf_writer import write_gguf
+    meta = [("general.architecture", "STRING", "qwen3vl"), ("qwen3vl.block_count", "U32", 36)]
+    v = ((((np.arange(512) + 17) % 37).astype(np.float32) - 18.0) / 19.0).reshape(2, 256)
+    q4 = O.q4_k_quantize(v)
+    path = tmp_path / "head-q4k.gguf"
+    write_gguf(str(path), meta, [("output_norm.weight", "F32", [256], np.ones(256, np.float32).tobytes()),
+                                 ("output.weight", "Q4K", [2, 256], q4.tobytes())])
+    x = ((np.arange(768) % 31).astype(np.float32) - 15.0) / 16.0
+    x16 = x.astype(np.float16).reshape(1, 3, 256)
+    try:
+        H.configure_worker_gguf_from_args(str(path), False, True, False, True, ROCM, H.DType.F16, 36)
+        H.load_worker_gguf_output_head(H.OutputHeadConfig(256, 2, 36, 1e-6), True)
+        assert H.worker_gguf_output_head_enabled() and not H.worker_gguf_sample_token_enabled()
+        xt = _t(x16).to_device(ROCM)
+        assert H.maybe_forward_worker_gguf_output_head(xt, 34) is None
+        assert H.maybe_forward_worker_gguf_output_head(xt, None) is None
+        got = H.maybe_forward_worker_gguf_output_head(xt, 35)
+        assert got.dtype == H.DType.F16 and got.dims == [1, 2]
+        ref = _head_ref(O, x16[0, 2:3].astype(np.float32), np.ones(256), O.q4_k_dequant(q4, 2, 256), 1e-6)
+        assert O.rel_l2(got.numpy().astype(np.float32), O.round_f16(ref.astype(np.float32))) <= 1e-3
+        # the [1, hidden] form is the same row
+        row = H.maybe_forward_worker_gguf_output_head(_t(x16[0, 2:3].copy()).to_device(ROCM), 35)
+        assert np.array_equal(row.numpy().view(np.uint16), got.numpy().view(np.uint16))
+        with pytest.raises(H.DialError, match=r"expects \[1, seq, hidden\] or \[1, hidden\], got \[2, 256\]"):
+            H.maybe_forward_worker_gguf_output_head(_t(x16[0, :2].copy()).to_device(ROCM), 35)
+
+        rng = np.random.default_rng(9)
+        hid, vocab = 512, 1000
+        emb = O.q8_0_quantize(rng.normal(0, 0.05, (vocab, hid)).astype(np.float32))
+        norm = rng.normal(1.0, 0.2, hid).astype(np.float32)
+        path2 = tmp_path / "head-tied-q8.gguf"
+        write_gguf(str(path2), meta, [("output_norm.weight", "F32", [hid], norm.tobytes()),
+                                      ("token_embd.weight", "Q8_0", [vocab, hid], emb.tobytes())])
+        H.configure_worker_gguf_from_args(str(path2), False, True, True, True, ROCM, H.DType.F16, 36)
+        H.load_worker_gguf_output_head(H.OutputHeadConfig(hid, vocab, 36, 1e-5), True)
+        assert H.worker_gguf_sample_token_enabled()
+        xs = O.round_f16(rng.normal(0, 1, (1, 4, hid)).astype(np.float32))
+        xt = _t(xs.astype(np.float16)).to_device(ROCM)
+        with pytest.raises(H.DialError, match="did not send sampling parameters"):
+            H.maybe_forward_worker_gguf_output_head(xt, 35)
+        ref = _head_ref(O, xs[0, 3:4], O.round_f16(norm), O.q8_0_dequant(emb, vocab, hid), 1e-5)
+        token = H.maybe_forward_worker_gguf_output_head(xt, 35, H.SamplingRequest(seed=1, temperature=0.0))
+        assert isinstance(token, int)
+        top2 = np.sort(ref[0])[-2:]
+        assert top2[1] - top2[0] > 1e-2  # a clear winner, so rounding cannot flip it
+        assert token == int(np.argmax(ref[0]))
+    finally:
+        H.configure_worker_gguf_from_args(None, False, False, False, True, ROCM, H.DType.F16, 1)
+        H.load_worker_gguf_output_head(H.OutputHeadConfig(1, 1, 1), True)
+        assert not H.worker_gguf_output_head_enabled()

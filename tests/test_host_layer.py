@@ -87,3 +87,47 @@ def test_compressed_tensors_zero_global_is_rejected():
     vb.insert("layer.weight_global_scale", H.Tensor.from_numpy(np.array([0.0], np.float32)))
     with pytest.raises(H.DialError, match="weight_global_scale for layer is zero"):
         H.linear_no_bias(16, 1, vb.pp("layer"))
+
+
+def test_worker_gguf_output_head_load_errors(tmp_path):
+    # worker_gguf.rs:197-265: the gates and the shape / presence checks of
+    # load_worker_gguf_output_head, all raised before any device work
+    from gguf_writer import write_gguf
+    rocm = H.Device.rocm(0)
+    cfg = H.OutputHeadConfig(hidden_size=32, vocab_size=4, num_hidden_layers=2)
+    meta = [("general.architecture", "STRING", "qwen3vl"), ("qwen3vl.block_count", "U32", 2)]
+    ones = np.ones(32, np.float32).tobytes()
+    q8 = bytes(4 * 34)
+
+    def configure(tensors, head=True):
+        path = tmp_path / f"head{len(list(tmp_path.iterdir()))}.gguf"
+        write_gguf(str(path), meta, tensors)
+        H.configure_worker_gguf_from_args(str(path), False, head, False, True, rocm, H.DType.F16, 2)
+
+    try:
+        configure([("output_norm.weight", "F32", [32], ones)], head=False)
+        H.load_worker_gguf_output_head(cfg, True)  # not requested: nothing to do
+        assert not H.worker_gguf_output_head_enabled()
+        assert H.maybe_forward_worker_gguf_output_head(H.Tensor.from_numpy(np.zeros((1, 32), np.float32)), 1) is None
+        configure([("output_norm.weight", "F32", [32], ones)])
+        H.load_worker_gguf_output_head(cfg, False)  # another worker owns the final layer
+        assert not H.worker_gguf_output_head_enabled()
+        configure([("output.weight", "Q8_0", [4, 32], q8)])
+        with pytest.raises(H.DialError, match="has no tensor output_norm.weight"):
+            H.load_worker_gguf_output_head(cfg, True)
+        configure([("output_norm.weight", "F32", [16], bytes(64))])
+        with pytest.raises(H.DialError, match=r"output_norm.weight shape \[16\], expected \[32\]"):
+            H.load_worker_gguf_output_head(cfg, True)
+        configure([("output_norm.weight", "F32", [32], ones)])
+        with pytest.raises(H.DialError, match="has neither output.weight nor token_embd.weight"):
+            H.load_worker_gguf_output_head(cfg, True)
+        configure([("output_norm.weight", "F32", [32], ones), ("token_embd.weight", "Q8_0", [5, 32], bytes(5 * 34))])
+        with pytest.raises(H.DialError, match=r"token_embd.weight shape \[5, 32\], expected \[4, 32\]"):
+            H.load_worker_gguf_output_head(cfg, True)
+        assert not H.worker_gguf_output_head_enabled()
+        path = tmp_path / "nohead.gguf"
+        write_gguf(str(path), meta, [])
+        with pytest.raises(H.DialError, match="requires --worker-gguf-output-head"):
+            H.configure_worker_gguf_from_args(str(path), False, False, True, True, rocm, H.DType.F16, 2)
+    finally:
+        H.configure_worker_gguf_from_args(None, False, False, False, True, rocm, H.DType.F16, 1)

@@ -256,6 +256,22 @@ def test_matmul_oracle_matches_numpy(O):
     assert y.shape == (3, 7)
 
 
+def test_rms_norm_oracle(O):
+    """A constant row c gives w * c / sqrt(c^2 + eps) (a sum in place of the
+    mean, or a missing square root, breaks it); random rows match torch's
+    own rms_norm in float64, and the weight multiplies per column."""
+    import torch
+    w = np.linspace(-2.0, 3.0, 16)
+    for c, eps in ((3.0, 1e-6), (-0.5, 0.25), (0.0, 1e-6)):
+        y = O.rms_norm(np.full((1, 16), c), w, eps)
+        assert np.allclose(y, w * c / np.sqrt(c * c + eps), rtol=1e-15, atol=0)
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 2, (5, 64))
+    wr = rng.normal(1, 0.3, 64)
+    want = torch.nn.functional.rms_norm(torch.from_numpy(x), (64,), torch.from_numpy(wr), eps=1e-5).numpy()
+    assert np.allclose(O.rms_norm(x, wr, 1e-5), want, rtol=1e-13, atol=1e-13)
+
+
 def test_swiglu_oracle_known_answers(O):
     """silu(g) = g * sigmoid(g): known values, the odd-part identity
     silu(g) - silu(-g) = g (a sign slip in the exponent breaks it), torch's
