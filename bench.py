@@ -54,8 +54,8 @@ METRIC = "quant GEMV weight GB/s (% HBM peak) + prefill GEMM TFLOP/s, 27B shapes
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=300)
-    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--copies", type=int, default=3, help="layer copies rotated per step")
     ap.add_argument("--prefill-iters", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
