@@ -1,30 +1,28 @@
 """Benchmark of the quantized-linear hot path on one MI355X.
 
-Workload: one 27B-class dense decoder layer's linears as DIAL's W8A16
-worker runs them -- hidden 5120; fused qkv [8192, 5120] (q 6144 + k 1024 +
-v 1024 rows), o [5120, 6144], fused gate_up [34816, 5120], down
-[5120, 17408]; 340,787,200 weights per layer.  Weights are N(0, 0.02),
-quantized on the GPU by the library's own quantizers; activations are bf16
-N(0, 1).
+Workload: one 27B-class dense decoder layer's linears -- hidden 5120, q
+[6144, 5120], k and v [1024, 5120], o [5120, 6144], gate and up
+[17408, 5120], down [5120, 17408]; 340,787,200 weights per layer.  Weights
+are N(0, 0.02), quantized on the GPU by the library's own quantizers;
+activations are bf16 N(0, 1).
 
-A step is one decode pass (M = 1) over the layer's four linears in W8A16
+A step is one decode pass (M = 1) over the layer's seven linears in W8A16
 (int8 per row + bf16 scale), captured once per layer copy in a HIP graph
 and replayed (the serving loop's launch path; no host work per linear).
 Layer copies rotate so the weight working set (COPIES x 341 MB) exceeds the
 256 MB Infinity Cache and the figure measures HBM.  `value` = algorithmic
 weight bytes streamed / wall time of the timed steps, in GB/s.  Extra keys
-report the same decode with f16 activations, with gate_up's SwiGLU
-epilogue, and over the GGUF worker's seven split projections; the decode
-for Q4_K (split projections, as GGUF files store them) / FP8-128 / MXFP4;
-the prefill GEMM TFLOP/s (W8A16 and Q4_K at M = 2048, FP8-128 and MXFP4
-native at M = 1024; with and without the SwiGLU epilogue), the quantized
-lm_head decode GEMV (vocab 248320 x 5120) and the device token selection
-after it, the roofline of the dominant kernel and the CPU baseline.
+report the same decode for Q4_K / FP8-128 / MXFP4, the prefill GEMM TFLOP/s
+(W8A16 and Q4_K at M = 2048, FP8-128 and MXFP4 native at M = 1024; also over
+the fused qkv / o / gate_up / down projections DIAL's layers call, with and
+without gate_up's SwiGLU epilogue), the quantized lm_head decode GEMV (vocab
+248320 x 5120) and the device token selection after it, the roofline of the
+dominant kernel and the CPU baseline.
 
-`--profile` runs only the dominant kernel (W8A16 gate_up GEMV, eager
-launches over rotating copies) plus a 256 MiB device-to-device copy used to
-scale the HBM byte counters; `--profile-lm-head` the same for the lm_head
-GEMV; `--profile-prefill` runs only the prefill GEMMs of one
+`--profile` runs only the dominant kernel (W8A16 gate GEMV, eager launches
+over rotating copies) plus a 256 MiB device-to-device copy used to scale the
+HBM byte counters; `--profile-lm-head` the same for the lm_head GEMV;
+`--profile-prefill` runs only the prefill GEMMs of one
 layer per format, `--profile-swiglu` the fused gate_up with and without its
 SwiGLU epilogue, `--profile-select` the token selection.  They are the
 programs the committed rocprofv3 summaries run.
@@ -77,8 +75,8 @@ def parse():
     return ap.parse_args()
 
 
-DOM = ("gate_up", 34816, 5120)  # the layer's largest linear (178 MB at W8A16)
-DOM_COPIES = 3                  # 3 x 178 MB rotated: beyond the 256 MB Infinity Cache
+DOM = ("gate", 17408, 5120)   # the layer's largest linear (gate/up/down tie on bytes)
+DOM_COPIES = 6                # 6 x 89 MB rotated: beyond the 256 MB Infinity Cache
 
 
 def capture(torch, fn):
@@ -91,9 +89,8 @@ def capture(torch, fn):
 
 def read_traffic():
     """HBM bytes per launch of the dominant kernel from the committed PMC
-    summary (profiles/gemv_w8a16_gate_up_34816x5120_traffic.txt), if present."""
-    name, n, k = DOM
-    path = os.path.join(ROOT, "profiles", f"gemv_w8a16_{name}_{n}x{k}_traffic.txt")
+    summary (profiles/gemv_w8a16_gate_17408x5120_traffic.txt), if present."""
+    path = os.path.join(ROOT, "profiles", "gemv_w8a16_gate_17408x5120_traffic.txt")
     try:
         vals = {}
         for line in open(path):
@@ -190,9 +187,9 @@ def time_launches(dq, torch, lins, k, n, dev, reps=60):
     return e0.elapsed_time(e1) / reps * 1e-3  # seconds per launch
 
 
-def time_per_linear(dq, torch, layers, dev, shapes=LAYER_27B_FUSED):
+def time_per_linear(dq, torch, layers, dev):
     out = {}
-    for li, (name, n, k) in enumerate(shapes):
+    for li, (name, n, k) in enumerate(LAYER_27B):
         out[name] = time_launches(dq, torch, [l[li] for l in layers], k, n, dev)
     return out
 
@@ -369,7 +366,7 @@ def cpu_baseline(seconds):
     dt = (time.perf_counter() - t0) / reps
     gbs = (n * k + 2 * n) / dt / 1e9
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"W8A16 decode GEMV [17408x5120] M=1 (the gate half of gate_up), {reps} reps, "
+            "sample": f"W8A16 decode GEMV [17408x5120] M=1 (the layer's gate linear), {reps} reps, "
                       f"{threads} OpenMP threads, dequantize-on-the-fly f32 dot per row"}
 
 
@@ -401,23 +398,16 @@ def main():
     fmt_of = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}
 
     # ---- headline: W8A16 decode over the 27B layer -----------------------
-    # The layer as DIAL's W8A16 worker runs it: fused qkv_proj and
-    # gate_up_proj (qwen3_vl/text.rs:1428-1455, 640-667), four linears.
-    F = LAYER_27B_FUSED
-    layers = build_layers(dq, torch, dq.W8A16, a.copies, dev, shapes=F)
-    secs = time_decode(dq, torch, layers, a.steps, a.warmup, dev, shapes=F)
-    lbytes = layer_bytes(dq, dq.W8A16, F)
+    layers = build_layers(dq, torch, dq.W8A16, a.copies, dev)
+    secs = time_decode(dq, torch, layers, a.steps, a.warmup, dev)
+    lbytes = layer_bytes(dq, dq.W8A16)
     value = lbytes * a.steps / secs / 1e9
-    per = time_per_linear(dq, torch, layers, dev, F)
-    fsteps = max(a.steps // 3, 10)
+    per = time_per_linear(dq, torch, layers, dev)
     # the same decode with f16 activations (the GGUF worker's runtime dtype)
-    s16 = time_decode(dq, torch, layers, fsteps, 10, dev, shapes=F, xdtype=torch.float16)
-    value_f16 = lbytes * fsteps / s16 / 1e9
-    # ... and with gate_up's SwiGLU epilogue, which writes silu(gate) * up
-    # (the down projection's input) instead of the [M, 34816] gate_up output
-    fs2 = time_decode(dq, torch, layers, fsteps, 10, dev, shapes=F, swiglu=("gate_up",))
-    value_swiglu = lbytes * fsteps / fs2 / 1e9
-    # dominant kernel: the gate_up GEMV (the largest linear), timed over
+    fsteps16 = max(a.steps // 3, 10)
+    s16 = time_decode(dq, torch, layers, fsteps16, 10, dev, xdtype=torch.float16)
+    value_f16 = layer_bytes(dq, dq.W8A16) * fsteps16 / s16 / 1e9
+    # dominant kernel: the gate GEMV (the largest linear), timed over
     # DOM_COPIES rotating copies so no launch finds its weight in the cache
     dom, dn, dk = DOM
     gd = torch.Generator(device=dev).manual_seed(11)
@@ -434,31 +424,37 @@ def main():
     traffic = read_traffic()
     print(f"# w8a16 decode: {value:.1f} GB/s over the layer; per-launch us: "
           + ", ".join(f"{k}={v * 1e6:.1f}" for k, v in per.items()), file=sys.stderr, flush=True)
-    print(f"# w8a16 decode with f16 activations: {value_f16:.1f} GB/s; with the SwiGLU epilogue: "
-          f"{value_swiglu:.1f} GB/s", file=sys.stderr, flush=True)
+
+    print(f"# w8a16 decode with f16 activations: {value_f16:.1f} GB/s", file=sys.stderr, flush=True)
     extra = {"decode_gbs": {"w8a16": round(value, 1)}, "decode_gbs_f16_activations": {"w8a16": round(value_f16, 1)},
-             "decode_gbs_fused_swiglu": {"w8a16": round(value_swiglu, 1)},
              "decode_us_per_launch_w8a16":
              {k: round(v * 1e6, 2) for k, v in per.items()}, "prefill_tflops": {}, "prefill_pct_mfma_peak": {}}
     sweep = [s for s in a.sweep.split(",") if s]
     if "w8a16" in sweep:
-        tf, s2 = time_prefill(dq, torch, layers[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, shapes=F)
+        tf, s2 = time_prefill(dq, torch, layers[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
         extra["prefill_tflops"]["w8a16_m2048"] = round(tf, 1)
         extra["prefill_pct_mfma_peak"]["w8a16_m2048"] = round(100.0 * tf / MFMA_PEAK_TFLOPS["bf16"], 1)
-        tf2, _ = time_prefill(dq, torch, layers[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, shapes=F,
-                              swiglu=("gate_up",))
-        extra["prefill_tflops_fused_swiglu"] = {"w8a16_m2048": round(tf2, 1)}
         print(f"# w8a16 prefill M=2048: {tf:.1f} TFLOP/s ({s2 * 1e3:.2f} ms/layer)", file=sys.stderr, flush=True)
     del layers
     torch.cuda.empty_cache()
-    # the split projections of the GGUF worker (q, k, v, gate, up loaded as
-    # separate blk.N tensors, text.rs:1373-1425): seven linears, same bytes
-    sl = build_layers(dq, torch, dq.W8A16, a.copies, dev, seed=3, shapes=LAYER_27B)
-    ss = time_decode(dq, torch, sl, fsteps, 10, dev, shapes=LAYER_27B)
-    extra["decode_gbs_split_projections"] = {"w8a16": round(layer_bytes(dq, dq.W8A16, LAYER_27B) * fsteps / ss / 1e9, 1)}
-    print(f"# w8a16 decode, split q/k/v/gate/up: {extra['decode_gbs_split_projections']['w8a16']} GB/s",
-          file=sys.stderr, flush=True)
-    del sl
+    # the same layer with fused qkv / gate_up projections (four linears)
+    fl = build_layers(dq, torch, dq.W8A16, a.copies, dev, seed=3, shapes=LAYER_27B_FUSED)
+    fsteps = max(a.steps // 3, 10)
+    fs = time_decode(dq, torch, fl, fsteps, 10, dev, shapes=LAYER_27B_FUSED)
+    extra["decode_gbs_fused_qkv_gate_up"] = {"w8a16": round(layer_bytes(dq, dq.W8A16, LAYER_27B_FUSED) * fsteps / fs / 1e9, 1)}
+    # ... and with gate_up's SwiGLU epilogue, which writes silu(gate) * up
+    # (the down projection's input) instead of the [M, 34816] gate_up output
+    fs2 = time_decode(dq, torch, fl, fsteps, 10, dev, shapes=LAYER_27B_FUSED, swiglu=("gate_up",))
+    extra["decode_gbs_fused_swiglu"] = {"w8a16": round(layer_bytes(dq, dq.W8A16, LAYER_27B_FUSED) * fsteps / fs2 / 1e9, 1)}
+    print(f"# w8a16 decode, fused qkv / gate_up: {extra['decode_gbs_fused_qkv_gate_up']['w8a16']} GB/s; "
+          f"with the SwiGLU epilogue: {extra['decode_gbs_fused_swiglu']['w8a16']} GB/s", file=sys.stderr, flush=True)
+    if "w8a16" in sweep:
+        tf, s2 = time_prefill(dq, torch, fl[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, shapes=LAYER_27B_FUSED)
+        extra.setdefault("prefill_tflops_fused_qkv_gate_up", {})["w8a16_m2048"] = round(tf, 1)
+        tf2, _ = time_prefill(dq, torch, fl[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, shapes=LAYER_27B_FUSED,
+                              swiglu=("gate_up",))
+        extra.setdefault("prefill_tflops_fused_swiglu", {})["w8a16_m2048"] = round(tf2, 1)
+    del fl
     torch.cuda.empty_cache()
     # quantized lm_head GEMV (vocab 248320 x hidden 5120): one copy is 1.27 GB
     # (W8A16) / 0.68 GB (MXFP4), far past the 256 MB last-level cache
@@ -483,23 +479,27 @@ def main():
         if name == "w8a16":
             continue
         fmt = fmt_of[name]
-        # Q4_K is the GGUF worker's format, whose layers load split projections
-        shapes = LAYER_27B if fmt == dq.Q4_K else F
-        ls = build_layers(dq, torch, fmt, a.copies if fmt != dq.MXFP4 and fmt != dq.Q4_K else a.copies + 2, dev,
-                          shapes=shapes)
-        sd = time_decode(dq, torch, ls, fsteps, 10, dev, shapes=shapes)
-        gbs = layer_bytes(dq, fmt, shapes) * fsteps / sd / 1e9
+        ls = build_layers(dq, torch, fmt, a.copies if fmt != dq.MXFP4 and fmt != dq.Q4_K else a.copies + 2, dev)
+        sd = time_decode(dq, torch, ls, max(a.steps // 3, 10), 10, dev)
+        gbs = layer_bytes(dq, fmt) * max(a.steps // 3, 10) / sd / 1e9
         extra["decode_gbs"][name] = round(gbs, 1)
         if fmt in (dq.FP8_BLOCK, dq.MXFP4):
-            tf, s2 = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE, shapes=shapes)
+            tf, s2 = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE)
             extra["prefill_tflops"][name + "_native_m1024"] = round(tf, 1)
             peak = MFMA_PEAK_TFLOPS["fp8" if fmt == dq.FP8_BLOCK else "fp4"]
             extra["prefill_pct_mfma_peak"][name + "_native_m1024"] = round(100.0 * tf / peak, 1)
-            tf2, _ = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE,
-                                  shapes=shapes, swiglu=("gate_up",))
-            extra.setdefault("prefill_tflops_fused_swiglu", {})[name + "_native_m1024"] = round(tf2, 1)
+            # the fused projections DIAL's layers call (qkv, o, gate_up, down)
+            del ls
+            torch.cuda.empty_cache()
+            ls = build_layers(dq, torch, fmt, 1, dev, seed=5, shapes=LAYER_27B_FUSED)
+            tff, _ = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE,
+                                  shapes=LAYER_27B_FUSED)
+            extra.setdefault("prefill_tflops_fused_qkv_gate_up", {})[name + "_native_m1024"] = round(tff, 1)
+            tff2, _ = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE,
+                                   shapes=LAYER_27B_FUSED, swiglu=("gate_up",))
+            extra.setdefault("prefill_tflops_fused_swiglu", {})[name + "_native_m1024"] = round(tff2, 1)
         else:
-            tf, s2 = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, shapes=shapes)
+            tf, s2 = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
             extra["prefill_tflops"][name + "_m2048"] = round(tf, 1)
             extra["prefill_pct_mfma_peak"][name + "_m2048"] = round(100.0 * tf / MFMA_PEAK_TFLOPS["bf16"], 1)
         print(f"# {name}: decode {gbs:.1f} GB/s, prefill {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)
@@ -521,10 +521,9 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "27B-class dense layer linears as DIAL's W8A16 worker runs them (hidden 5120; "
-                        "fused qkv 8192x5120, o 5120x6144, fused gate_up 34816x5120, down 5120x17408), "
-                        "W8A16 decode GEMV, M=1",
-            "weights_per_layer": sum(n * k for _, n, k in LAYER_27B_FUSED),
+            "workload": "27B-class dense layer linears (hidden 5120; q 6144x5120, k/v 1024x5120, "
+                        "o 5120x6144, gate/up 17408x5120, down 5120x17408), W8A16 decode GEMV, M=1",
+            "weights_per_layer": sum(n * k for _, n, k in LAYER_27B),
             "weight_bytes_per_step": lbytes,
             "layer_copies_rotated": a.copies,
             "rows": 1,
