@@ -241,6 +241,13 @@ PYBIND11_MODULE(dialq_host, m) {
              return OutputHeadConfig{hidden_size, vocab_size, num_hidden_layers, rms_norm_eps};
            }),
            py::arg("hidden_size"), py::arg("vocab_size"), py::arg("num_hidden_layers"), py::arg("rms_norm_eps") = 1e-6);
+  m.def("f32_to_f16_bits", [](py::array_t<float, py::array::c_style | py::array::forcecast> a) {
+    py::array_t<uint16_t> out(a.size());
+    const float *src = a.data();
+    uint16_t *dst = out.mutable_data();
+    for (py::ssize_t i = 0; i < a.size(); ++i) dst[i] = f32_to_f16_bits(src[i]);
+    return out;
+  });
   m.def("load_worker_gguf_output_head", &load_worker_gguf_output_head, py::arg("cfg"), py::arg("owns_final_layer"));
   m.def("worker_gguf_output_head_enabled", &worker_gguf_output_head_enabled);
   m.def("worker_gguf_sample_token_enabled", &worker_gguf_sample_token_enabled);

@@ -176,6 +176,8 @@ struct DeviceScope {
 
 }  // namespace
 
+uint16_t f32_to_f16_bits(float f) { return f32_to_f16_rne(f); }
+
 // ---- basics ---------------------------------------------------------------
 const char *dtype_name(DType t) {
   switch (t) {

@@ -257,6 +257,9 @@ Linear build_worker_gguf_fp16_prefill_linear(const std::string &name, const std:
 
 // ---- worker GGUF output head (worker_gguf.rs:197-383) ------------------------
 struct SamplingRequest;  // sampling.hpp
+// f32 -> f16 bits, round to nearest even (half::f16::from_f32), as the output
+// head converts output_norm.weight.
+uint16_t f32_to_f16_bits(float f);
 struct OutputHeadConfig {
   int64_t hidden_size = 0, vocab_size = 0, num_hidden_layers = 0;
   double rms_norm_eps = 1e-6;

@@ -131,3 +131,21 @@ def test_worker_gguf_output_head_load_errors(tmp_path):
             H.configure_worker_gguf_from_args(str(path), False, False, True, True, rocm, H.DType.F16, 2)
     finally:
         H.configure_worker_gguf_from_args(None, False, False, False, True, rocm, H.DType.F16, 1)
+
+
+def test_f32_to_f16_rounding_matches_numpy():
+    # the F16 conversion of output_norm.weight (gguf_tensor_to_f16,
+    # worker_gguf.rs:681-696 checks 1..4): round to nearest even, against
+    # numpy's float16 cast on ties, subnormals, overflow, signed zeros, inf
+    # and every 13-bit tail pattern of a few exponents
+    base = np.array([1.0, 2.0, 3.0, 4.0, 0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e9, -1e9, np.inf, -np.inf,
+                     6.1035156e-05, 6.0e-05, 5.9604645e-08, 2.9802322e-08, 2.98e-08, 8.9e-08, -1.5e-06],
+                    np.float32)
+    bits = (np.arange(1 << 13, dtype=np.uint32)[:, None] | (np.array([103, 112, 127, 140], np.uint32) << 23))
+    tails = bits.ravel().view(np.float32)
+    x = np.concatenate([base, tails, -tails, np.random.default_rng(0).normal(0, 50, 4096).astype(np.float32)])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(H.f32_to_f16_bits(x), want)
+    nan = H.f32_to_f16_bits(np.array([np.nan], np.float32))[0]
+    assert (nan & 0x7c00) == 0x7c00 and (nan & 0x3ff) != 0
