@@ -66,6 +66,21 @@ struct DevBuf {
   DevBuf &operator=(const DevBuf &) = delete;
 };
 
+// One int of pinned, device-mapped host memory that kernels write with
+// system-scope stores and the host reads without synchronising.
+struct HostWord {
+  int *h = nullptr;  // host address
+  int *d = nullptr;  // device address of the same word
+  void alloc() {
+    hip_check(hipHostMalloc((void **)&h, 64, hipHostMallocMapped | hipHostMallocCoherent), "hipHostMalloc");
+    *h = 0;
+    hip_check(hipHostGetDevicePointer((void **)&d, h, 0), "hipHostGetDevicePointer");
+  }
+  ~HostWord() {
+    if (h) (void)hipHostFree(h);
+  }
+};
+
 // Restores the caller's current device on scope exit.
 struct DeviceGuard {
   int prev = -1;
@@ -89,6 +104,8 @@ struct Linear {
   DevBuf gemv_cnt; // per-strip piece counters + work-queue head/exit count (zero between calls)
   DevBuf native_part;  // stream-K partial tiles of the native prefill
   DevBuf native_cnt;   // its per-tile arrival counters (zero between calls)
+  DevBuf xstage;       // 16-byte-aligned copy of an x that arrives misaligned
+  HostWord gave_up;    // set by a decode launch whose bounded wait gave up
   std::mutex scratch_mu;
   float global = 1.0f;
 
@@ -217,8 +234,14 @@ Linear *alloc_linear(const dialq_linear_desc &d, int device) {
   if (d.format == DIALQ_FORMAT_NVFP4) {
     L->global = (d.flags & DIALQ_FLAG_GLOBAL_IS_DIVISOR) ? 1.0f / d.global_scale : d.global_scale;
   }
-  L->gemv_cnt.alloc((size_t)(L->n_strips + 2) * sizeof(int));  // strips, queue head, exit count
-  hip_check(hipMemset(L->gemv_cnt.p, 0, L->gemv_cnt.n), "hipMemset");
+  try {
+    L->gemv_cnt.alloc((size_t)(L->n_strips + 2) * sizeof(int));  // strips, queue head, exit count
+    hip_check(hipMemset(L->gemv_cnt.p, 0, L->gemv_cnt.n), "hipMemset");
+    L->gave_up.alloc();
+  } catch (...) {
+    delete L;
+    throw;
+  }
   return L;
 }
 
@@ -244,26 +267,36 @@ int guarded(char *error, size_t error_size, F &&f) {
   return -1;
 }
 
-void ensure_scratch(Linear *L, size_t bytes) {
-  if (L->scratch.n < bytes) L->scratch.alloc(bytes);
-}
-
-// Stream-K partials and tile counters of the native prefill, owned by the
-// handle like the GEMV workspace (calls on one handle are stream-ordered).
-// They grow on demand, after the stream has drained, never during graph
-// capture: a capture must follow an eager call of at least the same shape.
-void ensure_native_scratch(Linear *L, size_t part_bytes, size_t cnt_count, hipStream_t st) {
-  const size_t cnt_bytes = cnt_count * sizeof(int);
-  if (L->native_part.n >= part_bytes && L->native_cnt.n >= cnt_bytes) return;
+// A handle's scratch buffers (GEMV workspace, native prefill codes and
+// partials, the aligned copy of x) are owned by the handle (calls on one
+// handle are stream-ordered) and grow on demand: after the stream has
+// drained, since earlier launches may still use the old buffer, and never
+// during stream capture, where the allocation would not be replayed -- a
+// capture must follow an eager call of at least the same shape.
+void refuse_growth_in_capture(hipStream_t st, const char *what, size_t bytes) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   hip_check(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
   if (cs != hipStreamCaptureStatusNone)
-    fail("native prefill scratch must grow (%zu partial bytes, %zu tile counters) during stream capture; run "
-         "one eager call of this shape before capturing", part_bytes, cnt_count);
-  hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");  // earlier launches may use the old buffers
-  if (L->native_part.n < part_bytes) L->native_part.alloc(part_bytes);
+    fail("%s must grow to %zu bytes during stream capture; run one eager call of this shape before capturing", what,
+         bytes);
+}
+
+void grow(DevBuf &b, size_t bytes, hipStream_t st, const char *what) {
+  if (b.n >= bytes) return;
+  refuse_growth_in_capture(st, what, bytes);
+  hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+  b.alloc(bytes);
+}
+
+void ensure_scratch(Linear *L, size_t bytes, hipStream_t st) { grow(L->scratch, bytes, st, "activation scratch"); }
+
+// Stream-K partials and tile counters of the native prefill.
+void ensure_native_scratch(Linear *L, size_t part_bytes, size_t cnt_count, hipStream_t st) {
+  const size_t cnt_bytes = cnt_count * sizeof(int);
+  if (L->native_part.n >= part_bytes && L->native_cnt.n >= cnt_bytes) return;
+  grow(L->native_part, part_bytes, st, "native prefill partials");
   if (L->native_cnt.n < cnt_bytes) {
-    L->native_cnt.alloc(cnt_bytes);
+    grow(L->native_cnt, cnt_bytes, st, "native prefill tile counters");
     hip_check(hipMemsetAsync(L->native_cnt.p, 0, cnt_bytes, st), "hipMemsetAsync");
   }
 }
@@ -285,9 +318,9 @@ void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, i
       fail("decode kernel addresses weights with 32-bit offsets: %zu resident bytes exceed 2 GiB; split the "
            "output dimension", L->tiles.n);
     std::lock_guard<std::mutex> lock(L->scratch_mu);
-    size_t need = gemv_workspace_bytes(w, rows);
-    if (L->gemv_ws.n < need) L->gemv_ws.alloc(need);
-    hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, (float *)L->gemv_ws.p, L->gemv_ws.n, (int *)L->gemv_cnt.p, st),
+    grow(L->gemv_ws, gemv_workspace_bytes(w, rows), st, "decode GEMV workspace");
+    hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, (float *)L->gemv_ws.p, L->gemv_ws.n, (int *)L->gemv_cnt.p,
+                          L->gave_up.d, st),
               "GEMV launch");
   } else if (path == DIALQ_PATH_GEMM) {
     hip_check(launch_gemm(w, x, x_dtype, rows, y, y_dtype, st), "GEMM launch");
@@ -300,7 +333,7 @@ void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, i
     std::lock_guard<std::mutex> lock(L->scratch_mu);
     if (fmt == DIALQ_FORMAT_FP8_BLOCK) {
       size_t codes = (size_t)(rows * k_pad), off = (codes + 255) / 256 * 256;
-      ensure_scratch(L, off + (size_t)rows * sizeof(float));
+      ensure_scratch(L, off + (size_t)rows * sizeof(float), st);
       uint8_t *xq = (uint8_t *)L->scratch.p;
       float *xs = (float *)((uint8_t *)L->scratch.p + off);
       hip_check(launch_act_fp8(x, x_dtype, rows, w.K, k_pad, xq, xs, st), "activation quantizer");
@@ -310,7 +343,7 @@ void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, i
                 "native GEMM launch");
     } else {
       size_t codes = (size_t)(rows * k_pad / 2), off = (codes + 255) / 256 * 256;
-      ensure_scratch(L, off + (size_t)(rows * k_pad / 32));
+      ensure_scratch(L, off + (size_t)(rows * k_pad / 32), st);
       uint8_t *xq = (uint8_t *)L->scratch.p;
       uint8_t *xs = (uint8_t *)L->scratch.p + off;
       hip_check(launch_act_mxfp4(x, x_dtype, rows, w.K, k_pad, xq, xs, st), "activation quantizer");
@@ -324,8 +357,22 @@ void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, i
   }
 }
 
-void check_ptr_align(const void *p, const char *what) {
-  if (((uintptr_t)p) & 15u) fail("%s must be 16-byte aligned", what);
+// A decode launch on this handle whose work-queue wait gave up (it wrote
+// an incomplete output and may have left the queue counters non-zero) is
+// reported by the next forward on the handle, which resets the counters.
+void check_gave_up(Linear *L, hipStream_t st) {
+  if (!__atomic_load_n(L->gave_up.h, __ATOMIC_ACQUIRE)) return;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hip_check(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
+  if (cs != hipStreamCaptureStatusNone)
+    fail("a previous decode launch on this handle gave up waiting for its work queue and left an incomplete "
+         "output; the handle cannot be reset during stream capture");
+  hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");  // the launch that gave up has ended
+  hip_check(hipMemset(L->gemv_cnt.p, 0, L->gemv_cnt.n), "hipMemset");
+  __atomic_store_n(L->gave_up.h, 0, __ATOMIC_RELEASE);
+  fail("a previous decode launch on this handle gave up waiting for its work queue after %d polls without "
+       "progress; that call's output is incomplete.  The handle's queue counters are reset and the next call "
+       "runs normally", gemv_wait_limit());
 }
 
 void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void *y, int32_t y_dtype,
@@ -340,6 +387,7 @@ void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void 
   if (!x || !y) fail("x and y must not be NULL");
   DeviceGuard dg(L->device);
   hipStream_t st = (hipStream_t)stream;
+  check_gave_up(L, st);
   const int64_t N = swiglu ? L->desc.out_dim / 2 : L->desc.out_dim, K = L->desc.in_dim;
   size_t xbytes = (size_t)(rows * K) * xs, ybytes = (size_t)(rows * N) * ys;
   DevBuf dx, dy;
@@ -350,16 +398,24 @@ void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void 
     dy.alloc(ybytes);
     xp = dx.p;
     yp = dy.p;
-  } else {
-    check_ptr_align(x, "x");
+  } else if (((uintptr_t)x) & 15u) {
+    // The kernels read x with 16-byte buffer loads and LDS DMA from a
+    // 16-byte-aligned base.  A view at any other offset (a candle narrow /
+    // start_offset, worker_w8a16.rs:419) is copied once into the handle's
+    // aligned staging buffer, on the same stream.
+    std::lock_guard<std::mutex> lock(L->scratch_mu);
+    grow(L->xstage, xbytes, st, "aligned copy of a misaligned x");
+    hip_check(hipMemcpyAsync(L->xstage.p, x, xbytes, hipMemcpyDeviceToDevice, st), "hipMemcpyAsync");
+    xp = L->xstage.p;
   }
+  if (((uintptr_t)yp) % ys) fail("y must be aligned to its element size (%zu bytes)", ys);
   if (local_q8) {
     if (L->desc.format != DIALQ_FORMAT_W8A16 || L->desc.scale_dtype != DIALQ_F32)
       fail("local q8 linear needs a W8A16 weight with f32 scales");
     if (rows != 1) fail("local q8 linear expects decode [1, 1, %lld], got %lld rows", (long long)K, (long long)rows);
     std::lock_guard<std::mutex> lock(L->scratch_mu);
     int64_t k_pad = L->k_chunks * 64;
-    ensure_scratch(L, (size_t)((k_pad + 255) / 256 * 256 + 256));
+    ensure_scratch(L, (size_t)((k_pad + 255) / 256 * 256 + 256), st);
     hip_check(launch_local_q8(L->view(), xp, x_dtype, yp, y_dtype, L->scratch.p, st), "local q8 launch");
   } else {
     run_forward(L, xp, x_dtype, rows, yp, y_dtype, path, st, swiglu);
@@ -517,7 +573,7 @@ uint64_t dialq_linear_device_bytes(const void *linear) {
   const Linear *L = (const Linear *)linear;
   if (!L) return 0;
   return L->tiles.n + L->aux.n + L->row_scale.n + L->block_scale.n + L->scratch.n + L->gemv_ws.n +
-         L->gemv_cnt.n + L->native_part.n + L->native_cnt.n;
+         L->gemv_cnt.n + L->native_part.n + L->native_cnt.n + L->xstage.n;
 }
 
 int dialq_linear_describe(const void *linear, dialq_linear_desc *desc) {
@@ -526,6 +582,8 @@ int dialq_linear_describe(const void *linear, dialq_linear_desc *desc) {
   *desc = L->desc;
   return 0;
 }
+
+void dialq_debug_set_wait_limit(int64_t polls) { set_gemv_wait_limit(polls); }
 
 int dialq_linear_forward(void *linear, const void *x, int32_t x_dtype, int64_t rows, void *y,
                          int32_t y_dtype, void *stream, int device_io, char *error, size_t error_size) {

@@ -28,6 +28,8 @@
 // leaves an f32 partial in the workspace, and the last contributor to arrive
 // (per-strip counter, reset by that contributor) adds the partials in range
 // order -- deterministic.
+#include <atomic>
+
 #include "tile_ops.hpp"
 
 namespace dialq {
@@ -701,7 +703,8 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
 // accumulators in wave order and writes the strip (one piece per strip) or
 // publishes the piece's partial; the last piece of a strip to be published
 // adds all pieces in piece order and writes the strip -- deterministic.  All
-// waits are bounded (kSpinLimit polls), so no wave can hang.
+// waits are bounded (kSpinLimit polls without progress by default), so no
+// wave can hang; a wait that gives up marks the handle (DynParams::err).
 //
 // LDS: [ctl: q[kDynQueue], ng, done[kDynQueue]][staged x][32 zero bytes]
 //      [park[kDynQueue][W][mrows][16] floats]
@@ -726,7 +729,16 @@ struct DynParams {
   float *ws;       // [n_strips][P][mrows][16] piece partials (P > 1)
   size_t ws_bytes;
   int *cnt;        // [n_strips] piece counters, then queue head and exit count
+  int *err;        // host-visible word set to 1 when a bounded wait gives up
+  int spin_limit;  // polls without progress before a wait gives up
 };
+
+// A wave whose bounded wait gave up: the launch's output is incomplete.  The
+// word lives in host memory so that the next forward on the handle can see
+// it without synchronising.
+__device__ __forceinline__ void report_gave_up(const DynParams &p) {
+  if ((threadIdx.x & 63) == 0) __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 __device__ __forceinline__ int lds_load(const int *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -878,7 +890,10 @@ __device__ void control_wave(const DynParams &p, int *q, int *ng, int *done, con
       spin = 0;
     } else {
       __builtin_amdgcn_s_sleep(1);
-      if (++spin > kSpinLimit) break;
+      if (++spin > p.spin_limit) {
+        report_gave_up(p);
+        break;
+      }
     }
   }
   // The last workgroup out resets the queue for the next launch.
@@ -981,11 +996,13 @@ __global__ __launch_bounds__(64 * (kDynWaves + 1)) void k_gemv_dyn(DynParams p) 
     // next unit: wait until the control wave has queued ordinal ord + 1
     int spin = 0;
     while (lds_load(ng) <= ord + 1) {
+      if (++spin > p.spin_limit) break;
       __builtin_amdgcn_s_sleep(1);
-      if (++spin > kSpinLimit) break;
     }
     lds_acquire();
-    const int nxt = (spin > kSpinLimit) ? -1 : lds_load(&q[(ord + 1) % QD]);
+    const bool gave_up = spin > p.spin_limit;
+    if (gave_up) report_gave_up(p);
+    const int nxt = gave_up ? -1 : lds_load(&q[(ord + 1) % QD]);
     int s = 0, c0 = 0, c1 = 0;
     if (nxt >= 0) unit_range(p, nxt, s, c0, c1);
 #pragma unroll
@@ -1169,7 +1186,7 @@ using Q6kRowsPol = Q6kRowsPolicy<ACT, RP, XL, XS>;
 
 template <int FMT, int ACT>
 static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype,
-                                float *ws, size_t ws_bytes, int *cnt, hipStream_t st) {
+                                float *ws, size_t ws_bytes, int *cnt, int *err, hipStream_t st) {
   typedef FmtTraits<FMT> T;
   constexpr int XV = (ACT == DIALQ_F32) ? 8 : 4;  // VGPRs per 8-element activation operand
   constexpr bool KQ = FMT == DIALQ_FORMAT_Q4_K || FMT == DIALQ_FORMAT_Q6_K;
@@ -1177,7 +1194,7 @@ static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, v
   const int rows_per_pass = (KQ && M <= 8) ? 8 : 16;
   for (int64_t mb = 0; mb < M; mb += rows_per_pass) {
     const int64_t rem = M - mb, mrows = rem < 16 ? rem : 16;
-    DynParams p{w, x, y, M, mb, y_dtype, 1, 1, 1, 1, 0, ws, ws_bytes, cnt};
+    DynParams p{w, x, y, M, mb, y_dtype, 1, 1, 1, 1, 0, ws, ws_bytes, cnt, err, gemv_wait_limit()};
     hipError_t e;
     if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
       if (rem <= 4)
@@ -1213,31 +1230,41 @@ size_t gemv_workspace_bytes(const WeightView &w, int64_t M) {
 
 template <int FMT>
 static hipError_t gemv_act(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                           int y_dtype, float *ws, size_t ws_bytes, int *cnt, hipStream_t st) {
+                           int y_dtype, float *ws, size_t ws_bytes, int *cnt, int *err, hipStream_t st) {
   switch (x_dtype) {
-    case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
     // f16 activations feed f16 MFMAs as they are (f16 weight operands);
     // MXFP4's scaled codes need bf16's exponent range (hi / lo parts)
     case DIALQ_F16:
       return gemv_dispatch<FMT, FMT == DIALQ_FORMAT_MXFP4 ? DIALQ_F16 : kActF16N>(w, x, M, y, y_dtype, ws, ws_bytes,
-                                                                                 cnt, st);
-    case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, st);
+                                                                                 cnt, err, st);
+    case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
   }
   return hipErrorInvalidValue;
 }
 
+namespace {
+std::atomic<int> g_wait_limit{kSpinLimit};
+}
+
+int gemv_wait_limit() { return g_wait_limit.load(std::memory_order_relaxed); }
+
+void set_gemv_wait_limit(int64_t polls) {
+  g_wait_limit.store(polls < 0 ? kSpinLimit : (int)(polls < kSpinLimit ? polls : kSpinLimit), std::memory_order_relaxed);
+}
+
 hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                       int y_dtype, float *ws, size_t ws_bytes, int *cnt, hipStream_t st) {
+                       int y_dtype, float *ws, size_t ws_bytes, int *cnt, int *err, hipStream_t st) {
   switch (w.fmt) {
-    case DIALQ_FORMAT_W8A16: return gemv_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
-    case DIALQ_FORMAT_FP8_ROW: return gemv_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
-    case DIALQ_FORMAT_Q8_0: return gemv_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
+    case DIALQ_FORMAT_W8A16: return gemv_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
+    case DIALQ_FORMAT_FP8_ROW: return gemv_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
+    case DIALQ_FORMAT_Q8_0: return gemv_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
     case DIALQ_FORMAT_FP8_BLOCK:
-      return gemv_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
-    case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
-    case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
-    case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
-    case DIALQ_FORMAT_Q6_K: return gemv_act<DIALQ_FORMAT_Q6_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, st);
+      return gemv_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
+    case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
+    case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
+    case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
+    case DIALQ_FORMAT_Q6_K: return gemv_act<DIALQ_FORMAT_Q6_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
   }
   return hipErrorInvalidValue;
 }

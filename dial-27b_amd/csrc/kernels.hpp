@@ -52,11 +52,18 @@ hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int6
 
 // Decode GEMV: y[M,N] = x[M,K] W^T for any M (16 rows per pass).
 // ws: gemv_workspace_bytes(w, M) of scratch; cnt: n_strips + 2 ints that are
-// zero before the call and are left zero after it.  The resident tiles must
-// be smaller than 2 GiB (32-bit buffer offsets).
+// zero before the call and are left zero after it.  err: a host-visible int
+// (device address) that a launch sets to 1 when one of the work queue's
+// bounded waits gives up -- its output is then incomplete and cnt may be
+// left non-zero.  The resident tiles must be smaller than 2 GiB (32-bit
+// buffer offsets).
 size_t gemv_workspace_bytes(const WeightView &w, int64_t M);
 hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                       int y_dtype, float *ws, size_t ws_bytes, int *cnt, hipStream_t st);
+                       int y_dtype, float *ws, size_t ws_bytes, int *cnt, int *err, hipStream_t st);
+// Polls without progress before a bounded wait of the work queue gives up
+// (process-wide; < 0 restores the default).
+void set_gemv_wait_limit(int64_t polls);
+int gemv_wait_limit();
 // Prefill GEMM with weight-only dequantization (bf16 / f16 MFMA operands).
 hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
                        int y_dtype, hipStream_t st);

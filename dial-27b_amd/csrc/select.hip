@@ -252,14 +252,19 @@ __global__ __launch_bounds__(256) void k_select_slices(SelectParams p) {
       float m = -INFINITY;
       for (int i = tid; i < n; i += 256) m = fmaxf(m, vals[i] / p.temperature);
       m = block_reduce256<true>(m, sh);
-      float sum = 0.0f;
-      for (int i = tid; i < n; i += 256) sum += expf(vals[i] / p.temperature - m);
-      sum = block_reduce256<false>(sum, sh);
-      if (m > run_m) {
-        run_s = run_s * expf(run_m - m) + sum;
-        run_m = m;
-      } else {
-        run_s += sum * expf(m - run_m);
+      // a chunk of -inf logits (a masked vocabulary range) adds exp(-inf) =
+      // 0 to the sum, as softmax_in_place does; exp(v - m) would be
+      // exp(-inf + inf) = NaN here.  m is the same in every thread.
+      if (m != -INFINITY) {
+        float sum = 0.0f;
+        for (int i = tid; i < n; i += 256) sum += expf(vals[i] / p.temperature - m);
+        sum = block_reduce256<false>(sum, sh);
+        if (m > run_m) {
+          run_s = run_s * expf(run_m - m) + sum;
+          run_m = m;
+        } else {
+          run_s += sum * expf(m - run_m);
+        }
       }
     }
     if (p.k == 1) {

@@ -76,6 +76,7 @@ def _load():
         "dialq_logits_select_workspace_bytes": (SZ, [I64, I64]),
         "dialq_logits_select": (C.c_int, [P, I32, I64, P, I64, C.c_float, C.c_float, I32, I64, P, P, P, P, SZ,
                                           I32, P, C.c_int, CH, SZ]),
+        "dialq_debug_set_wait_limit": (None, [I64]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -292,6 +293,12 @@ class Linear:
                                      err, 512)
         _check(rc, err)
         return w, s
+
+
+def set_wait_limit(polls):
+    """Test hook (dialq_debug_set_wait_limit): polls without progress before
+    the decode work queue's waits give up; negative restores the default."""
+    lib.dialq_debug_set_wait_limit(int(polls))
 
 
 def logits_select(logits, k=1, *, rule=SELECT_FIRST_MAX, repeat_ids=(), repeat_penalty=1.0, temperature=0.0,

@@ -758,6 +758,9 @@ std::shared_ptr<WorkerGgufSource> g_gguf_source;
 std::atomic<bool> g_gguf_output_head{false}, g_gguf_sample_token{false};
 std::atomic<size_t> g_gguf_count{0}, g_gguf_bytes{0}, g_gguf_prefill_count{0}, g_gguf_prefill_bytes{0};
 std::atomic<unsigned> g_gguf_warmed{0};
+// Drops the loaded output head and re-arms its route log (defined with the
+// head's state below).
+void reset_output_head();
 
 std::shared_ptr<WorkerGgufSource> gguf_source() {
   std::shared_lock<std::shared_mutex> lk(g_gguf_mu);
@@ -805,6 +808,10 @@ void configure_worker_gguf_from_args(const std::optional<std::string> &path, boo
     std::unique_lock<std::shared_mutex> lk(g_gguf_mu);
     g_gguf_source.reset();
   }
+  // the reference clears the output-head slot and its route-logged flag on
+  // every configure (worker_gguf.rs:78-84), so a reconfigure never keeps a
+  // stale head (and its resident lm_head) routing logits
+  reset_output_head();
   if (!worker_mode) {
     if (path || fp16_prefill || output_head || sample_token)
       log_info("worker GGUF options ignored in master mode; master weights remain unchanged");
@@ -941,6 +948,14 @@ struct OutputHead {
 std::shared_mutex g_head_mu;
 std::shared_ptr<OutputHead> g_head;
 std::atomic<bool> g_head_route_logged{false};
+
+void reset_output_head() {
+  {
+    std::unique_lock<std::shared_mutex> lk(g_head_mu);
+    g_head.reset();
+  }
+  g_head_route_logged.store(false);
+}
 
 std::shared_ptr<OutputHead> output_head() {
   std::shared_lock<std::shared_mutex> lk(g_head_mu);

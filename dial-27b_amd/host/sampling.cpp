@@ -5,6 +5,9 @@
 #include <cmath>
 #include <cstring>
 #include <limits>
+#include <map>
+#include <memory>
+#include <mutex>
 #include <string>
 
 #include "dialq.h"
@@ -186,6 +189,24 @@ uint32_t sample_on_host(const Tensor &logits, const SamplingRequest &req, int mo
   return draw_in_token_order(idx, top, rng);
 }
 
+// The selection's workspace and output buffers, one grow-only pair per
+// device, reused by every sampled token: allocating them per token would
+// add hipMalloc / hipFree round trips (and hipFree's device-wide wait) to
+// each token's 7-75 us selection.
+struct SelectBuffers {
+  std::mutex mu;
+  Tensor ws, out;
+};
+
+SelectBuffers &select_buffers(int device) {
+  static std::mutex m;
+  static std::map<int, std::unique_ptr<SelectBuffers>> all;
+  std::lock_guard<std::mutex> lk(m);
+  std::unique_ptr<SelectBuffers> &b = all[device];
+  if (!b) b = std::make_unique<SelectBuffers>();
+  return *b;
+}
+
 struct DeviceSelection {
   std::vector<uint32_t> idx;
   std::vector<float> val;
@@ -210,15 +231,20 @@ DeviceSelection select_on_device(const Tensor &logits, int64_t vocab, const Samp
     lp = dlog.data();
   }
   const size_t wsb = dialq_logits_select_workspace_bytes(vocab, (int64_t)req.repeat_context.size());
-  Tensor ws = Tensor::empty(DType::U8, {(int64_t)wsb}, Device::rocm(device));
-  Tensor out = Tensor::empty(DType::U8, {(int64_t)(8 * k + 8)}, Device::rocm(device));
+  SelectBuffers &buf = select_buffers(device);
+  std::lock_guard<std::mutex> lk(buf.mu);  // one selection at a time per device owns the buffers
+  if (!buf.ws.defined() || buf.ws.nbytes() < wsb) buf.ws = Tensor::empty(DType::U8, {(int64_t)wsb}, Device::rocm(device));
+  if (!buf.out.defined())
+    buf.out = Tensor::empty(DType::U8, {(int64_t)(8 * DIALQ_SELECT_MAX_K + 8)}, Device::rocm(device));
+  Tensor &ws = buf.ws, &out = buf.out;
   uint32_t *oi = (uint32_t *)out.data();
   float *ov = (float *)((uint8_t *)out.data() + 4 * k), *os = (float *)((uint8_t *)out.data() + 8 * k);
   if (dialq_logits_select(lp, dtype_code(logits.dtype()), vocab, ids, (int64_t)req.repeat_context.size(),
                           req.repeat_penalty, temperature, rule, k, oi, ov, os, ws.data(), wsb, device, nullptr, 1,
                           err, sizeof err) != 0)
     fail(std::string("remote sampling failed: ") + err);
-  const std::vector<uint8_t> hb = out.host_bytes();  // synchronous: waits for the selection
+  // synchronous: waits for the selection (2 KB: the buffer holds 256 candidates)
+  const std::vector<uint8_t> hb = out.host_bytes();
   std::memcpy(r.idx.data(), hb.data(), 4 * (size_t)k);
   std::memcpy(r.val.data(), hb.data() + 4 * k, 4 * (size_t)k);
   std::memcpy(st, hb.data() + 8 * k, 8);

@@ -139,10 +139,21 @@ int dialq_linear_describe(const void *linear, dialq_linear_desc *desc);
  * (worker_w8a16.rs:368-386,402-475), CudaQuantLinear::forward + cuda_fwd
  * (cuda_quant.rs:373-391,406-499) and the GGUF QMatMul::forward call of
  * forward_worker_gguf (worker_gguf.rs:574-611).
- *   x: [rows, K] of x_dtype (F16, BF16 or F32), contiguous
- *   y: [rows, N] of y_dtype (F16, BF16 or F32), written in full
+ *   x: [rows, K] of x_dtype (F16, BF16 or F32), contiguous, at any address
+ *      (a view at any start offset, as candle's contiguous layouts allow,
+ *      worker_w8a16.rs:419); the kernels read from a 16-byte-aligned base,
+ *      so a device x at any other address is first copied, on `stream`,
+ *      into an aligned staging buffer the handle owns and grows (outside
+ *      stream capture, like every per-handle scratch buffer)
+ *   y: [rows, N] of y_dtype (F16, BF16 or F32), written in full; aligned to
+ *      its element size
  *   device_io: 1 = x / y are device pointers (asynchronous on `stream`);
  *              0 = host pointers (copied in and out; synchronous)
+ * Per-handle scratch (the decode workspace, the native prefill's activation
+ * codes and partials, the staged x) grows on the first call of a larger
+ * shape: that call synchronizes `stream` and allocates, and fails with a
+ * message if `stream` is capturing -- capture after one eager call of the
+ * same shape.
  * rows == 0 is a successful no-op.  Returns 0, or -1 with a message. */
 int dialq_linear_forward(void *linear, const void *x, int32_t x_dtype,
                          int64_t rows, void *y, int32_t y_dtype, void *stream,
@@ -228,6 +239,15 @@ int dialq_local_q8_forward(void *linear, const void *x, int32_t x_dtype,
                            int64_t rows, void *y, int32_t y_dtype,
                            void *stream, int device_io, char *error,
                            size_t error_size);
+
+/* Test hook; no counterpart in the reference.  Sets how many polls without
+ * progress the decode kernel's work-queue waits make before giving up
+ * (process-wide; a negative value restores the default of 4194304).  A
+ * launch that gives up still ends normally but leaves an incomplete output:
+ * it marks its handle, and the next forward on that handle returns -1 with
+ * a message and resets the handle's queue counters.  For tests of that
+ * failure path only. */
+void dialq_debug_set_wait_limit(int64_t polls);
 
 #ifdef __cplusplus
 }

@@ -39,15 +39,54 @@ def _oracle_rows(fmt, w, s, rows, n, k):
     raise ValueError(fmt)
 
 
-def _check(fmt, n, k, m, torch_dev, path=dq.PATH_AUTO, tol=1e-3, native=False, seed=0):
+def _check_quantizer_bytes(fmt, dense_rows, w, s, rows):
+    """The device quantizer's exported bytes for the sampled rows against the
+    oracle's quantizer on the same dense values.  FP8-128 scales cover
+    128-row blocks, so its sample is whole blocks (`rows` is then a range of
+    block-aligned rows)."""
+    if fmt == dq.W8A16:
+        q, _, sb = O.w8a16_quantize(dense_rows)
+        assert np.array_equal(w[rows], q) and np.array_equal(np.asarray(s)[rows].view(np.uint16), sb)
+    elif fmt == dq.Q8_0:
+        assert np.array_equal(w[rows], O.q8_0_quantize(dense_rows))
+    elif fmt == dq.Q4_K:
+        assert np.array_equal(w[rows], O.q4_k_quantize(dense_rows))
+    elif fmt == dq.MXFP4:
+        p, sx = O.mxfp4_quantize(dense_rows)
+        assert np.array_equal(w[rows], p) and np.array_equal(np.asarray(s)[rows], sx)
+    elif fmt == dq.FP8_BLOCK:
+        q, sx = O.fp8_block_quantize(dense_rows)
+        assert np.array_equal(w[rows], q)
+        assert np.array_equal(np.asarray(s)[rows[0] // 128:rows[-1] // 128 + 1].view(np.uint32), sx.view(np.uint32))
+    else:
+        raise ValueError(fmt)
+
+
+def _check(fmt, n, k, m, torch_dev, path=dq.PATH_AUTO, tol=1e-3, native=False, seed=0, quant_bytes=True):
     import torch
     g = torch.Generator(device=torch_dev).manual_seed(seed)
     wd = torch.randn(n, k, device=torch_dev, generator=g, dtype=torch.float32) * 0.02
     lin = dq.Linear.quantize(fmt, wd, scale_dtype=dq.BF16)
-    del wd
-    w, s = lin.export()
     rng = np.random.default_rng(seed + m)
     rows = np.sort(rng.choice(n, SAMPLE, replace=False))
+    if quant_bytes:
+        # the dense values of the sampled rows (whole 128-row blocks for
+        # FP8-128: the first and the last block row) stay on the host
+        if fmt == dq.FP8_BLOCK:
+            qrows = np.concatenate([np.arange(b * 128, b * 128 + 128) for b in sorted({0, (n - 1) // 128})])
+            qrows = qrows[qrows < n]
+        else:
+            qrows = rows
+        dense_rows = wd[torch.from_numpy(qrows).to(torch_dev)].cpu().numpy()
+    del wd
+    w, s = lin.export()
+    if quant_bytes:
+        if fmt == dq.FP8_BLOCK:
+            for b in sorted({0, (n - 1) // 128}):
+                sel = (qrows >= b * 128) & (qrows < b * 128 + 128)
+                _check_quantizer_bytes(fmt, dense_rows[sel], w, s, qrows[sel])
+        else:
+            _check_quantizer_bytes(fmt, dense_rows, w, s, qrows)
     deq = _oracle_rows(fmt, w, s, rows, n, k)
     x = O.round_bf16(rng.normal(0, 1, (m, k)).astype(np.float32))
     xt = to_torch(x, dq.BF16, torch_dev)

@@ -72,3 +72,38 @@ def test_graph_replay_native_prefill(fmt, torch_dev):
         assert torch.equal(y_graph.cpu(), ref), (dq.FORMAT_NAMES[fmt], rep)
         lin.forward(x * 2, y_eager, path=dq.PATH_GEMM_NATIVE, stream=stream)
         torch.cuda.synchronize()
+
+
+def test_work_queue_give_up_is_reported_by_the_next_forward(torch_dev):
+    # The decode work-queue kernel (small N whose activations are too large to
+    # stage: 1024 x 8704 at M = 8) bounds every wait.  With the limit forced to
+    # zero from the host its waits give up at once and every wave still ends
+    # normally; the launch marks its handle, the next forward reports it and
+    # resets the queue counters, and the call after that is correct again.
+    import torch
+    from helpers import make_weight, reference_product, to_torch
+    import oracle as O
+    n, k, m = 1024, 8704, 8
+    raw, scales, kw, deq = make_weight(dq.W8A16, n, k, seed=17)
+    lin = dq.Linear.create(dq.W8A16, n, k, raw, scales, **kw)
+    x = O.round_bf16(np.random.default_rng(4).normal(0, 1, (m, k)).astype(np.float32))
+    xt = to_torch(x, dq.BF16, torch_dev)
+    y = torch.empty(m, n, device=torch_dev, dtype=torch.bfloat16)
+    ref = reference_product(x, deq, dq.BF16)
+    lin.forward(xt, y, path=dq.PATH_GEMV)
+    torch.cuda.synchronize()
+    assert O.rel_l2(y.float().cpu().numpy(), ref) <= 1e-3
+    try:
+        dq.set_wait_limit(0)
+        y.fill_(float("nan"))
+        lin.forward(xt, y, path=dq.PATH_GEMV)  # gives up: output incomplete, handle marked
+        torch.cuda.synchronize()
+    finally:
+        dq.set_wait_limit(-1)
+    with pytest.raises(dq.DialqError, match="gave up waiting for its work queue"):
+        lin.forward(xt, y, path=dq.PATH_GEMV)
+    for _ in range(2):
+        y.fill_(float("nan"))
+        lin.forward(xt, y, path=dq.PATH_GEMV)
+        torch.cuda.synchronize()
+        assert O.rel_l2(y.float().cpu().numpy(), ref) <= 1e-3

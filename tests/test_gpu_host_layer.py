@@ -338,3 +338,36 @@ def test_worker_gguf_output_head_matches_oracle(tmp_path, torch_dev):
         H.configure_worker_gguf_from_args(None, False, False, False, True, ROCM, H.DType.F16, 1)
         H.load_worker_gguf_output_head(H.OutputHeadConfig(1, 1, 1), True)
         assert not H.worker_gguf_output_head_enabled()
+
+
+def test_reconfigure_drops_a_loaded_output_head(tmp_path, torch_dev):
+    # configure_worker_gguf_from_args clears the output-head slot and its
+    # route-logged flag on every call (worker_gguf.rs:78-84): after a
+    # reconfigure with output_head = false, in master mode or without a file,
+    # no stale head keeps routing logits, with no load_worker_gguf_output_head
+    # call in between
+    import oracle as O
+    from gguf_writer import write_gguf
+    meta = [("general.architecture", "STRING", "qwen3vl"), ("qwen3vl.block_count", "U32", 36)]
+    v = ((((np.arange(512) + 17) % 37).astype(np.float32) - 18.0) / 19.0).reshape(2, 256)
+    path = tmp_path / "head.gguf"
+    write_gguf(str(path), meta, [("output_norm.weight", "F32", [256], np.ones(256, np.float32).tobytes()),
+                                 ("output.weight", "Q4K", [2, 256], O.q4_k_quantize(v).tobytes())])
+    x16 = (((np.arange(256) % 31).astype(np.float32) - 15.0) / 16.0).astype(np.float16).reshape(1, 1, 256)
+    reconfigure = [
+        (str(path), False, False, False, True),   # same file, output head off
+        (None, False, False, False, False),       # master mode
+        (None, False, False, False, True),        # worker without a GGUF file
+    ]
+    try:
+        for args in reconfigure:
+            H.configure_worker_gguf_from_args(str(path), False, True, False, True, ROCM, H.DType.F16, 36)
+            H.load_worker_gguf_output_head(H.OutputHeadConfig(256, 2, 36, 1e-6), True)
+            assert H.worker_gguf_output_head_enabled()
+            assert H.maybe_forward_worker_gguf_output_head(_t(x16).to_device(ROCM), 35) is not None
+            H.configure_worker_gguf_from_args(*args, ROCM, H.DType.F16, 36)
+            assert not H.worker_gguf_output_head_enabled(), args
+            assert not H.worker_gguf_sample_token_enabled(), args
+            assert H.maybe_forward_worker_gguf_output_head(_t(x16).to_device(ROCM), 35) is None, args
+    finally:
+        H.configure_worker_gguf_from_args(None, False, False, False, True, ROCM, H.DType.F16, 1)

@@ -113,6 +113,22 @@ def test_block_quantizers_bit_exact(fmt, torch_dev):
                               np.asarray(ref_s).reshape(-1).view(np.uint8))
 
 
+@pytest.mark.parametrize("dense_dtype", [dq.F32, dq.F16], ids=["f32", "f16"])
+def test_q4_k_quantizer_closed_form_cases(dense_dtype, torch_dev):
+    # the device quantizer on inputs whose Q4_K bytes follow from arithmetic
+    # alone (tests/q4k_cases.py: exact grids, the min > 0 clamp, half-way
+    # ties of nearest_int, the 6-bit packing at every sub-block position).
+    # The grid values need up to 11 significant bits, which f16 holds (bf16,
+    # with 8, does not).
+    import q4k_cases
+    w, want, names = q4k_cases.cases()
+    assert np.array_equal(exact_inputs(w, dense_dtype), w)
+    lin = dq.Linear.quantize(dq.Q4_K, to_torch(w, dense_dtype, torch_dev))
+    got, _ = lin.export()
+    for r, name in enumerate(names):
+        assert np.array_equal(got[r], want[r]), (name, np.nonzero(got[r] != want[r])[0][:8])
+
+
 # ---- decode GEMV ---------------------------------------------------------------
 @pytest.mark.parametrize("x_dtype", [dq.BF16, dq.F16, dq.F32], ids=["bf16", "f16", "f32"])
 @pytest.mark.parametrize("fmt", ALL_FORMATS, ids=lambda f: dq.FORMAT_NAMES[f])

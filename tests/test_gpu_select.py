@@ -129,3 +129,40 @@ def test_select_rejects_bad_arguments(torch_dev):
         dq.logits_select(x, 11)
     with pytest.raises(dq.DialqError, match="unknown selection rule"):
         dq.logits_select(x, 1, rule=5)
+
+
+# Vocabularies past ~508k cap the slice count (slices x k must fit the
+# merge's 16384 staged keys, at most 1024 slices), so each slice runs several
+# chunks: keys carried between chunks, the running softmax merge and, at
+# 1033220 with k = 16, an empty last slice (1024 slices of 1010 tokens).
+@pytest.mark.parametrize("vocab,k", [(600000, 32), (600000, 64), (600000, 256), (1050000, 1), (1050000, 16),
+                                     (1050000, 128), (1033220, 16)])
+@pytest.mark.parametrize("rule", [dq.SELECT_FIRST_MAX, dq.SELECT_TOTAL_LAST_MAX], ids=["first", "total_last"])
+def test_select_multi_chunk_slices(vocab, k, rule, torch_dev):
+    rng = np.random.default_rng(vocab + k + rule)
+    # bf16 values: plenty of ties across chunk boundaries
+    x = _exact(rng.normal(0, 3, vocab).astype(np.float32), dq.BF16)
+    idx, val, st = _run(x, dq.BF16, k, rule, torch_dev, temperature=0.9)
+    want_i, want_v = RULES[rule](x, k)
+    assert np.array_equal(idx, want_i), (vocab, k)
+    assert np.array_equal(val, want_v)
+    m, s = O.softmax_stats(x, 0.9)
+    assert abs(st[0] - m) <= 1e-6 * abs(m) and abs(st[1] - s) <= 1e-5 * s, (st, m, s)
+
+
+@pytest.mark.parametrize("vocab,k", [(248320, 50), (248320, 1), (1050000, 16)])
+def test_select_masked_range_keeps_statistics_finite(vocab, k, torch_dev):
+    # a -inf range longer than a slice (whole slices and whole chunks of
+    # -inf): those tokens add exp(-inf) = 0 to S, as softmax_in_place's
+    # exp(v - max) does (qwen3_vl.rs:325-345)
+    rng = np.random.default_rng(vocab + k)
+    x = _exact(rng.normal(0, 3, vocab).astype(np.float32), dq.F32)
+    x[10000:30000] = -np.inf
+    x[-5000:] = -np.inf
+    for rule in RULES:
+        idx, val, st = _run(x, dq.F32, k, rule, torch_dev, temperature=0.7)
+        want_i, want_v = RULES[rule](x, k)
+        assert np.array_equal(idx, want_i) and np.array_equal(val, want_v)
+        m, s = O.softmax_stats(x, 0.7)
+        assert np.isfinite(st).all(), st
+        assert abs(st[0] - m) <= 1e-6 * abs(m) and abs(st[1] - s) <= 1e-5 * s, (st, m, s)

@@ -138,6 +138,105 @@ def test_q4_k_quantizer_round_trip(O):
             assert max(scs) == 63
 
 
+def test_q4_k_quantizer_closed_form_cases(O):
+    # Exact affine grids, all-positive sub-blocks, half-way ties and
+    # one-non-zero-sub-block super-blocks, whose bytes follow from arithmetic
+    # (tests/q4k_cases.py), against the oracle's restatement of candle's
+    # BlockQ4K::from_float (worker_gguf.rs:641,657)
+    import q4k_cases
+    w, want, names = q4k_cases.cases()
+    got = O.q4_k_quantize(w)
+    for r, name in enumerate(names):
+        assert np.array_equal(got[r], want[r]), (name, np.nonzero(got[r] != want[r])[0][:8])
+    # the dequantized grids come back exactly (d * sc * l - dmin * m)
+    deq = O.q4_k_dequant(got, len(names), 256)
+    for r, name in enumerate(names):
+        if name == "constant_subblocks":  # max == min sub-blocks keep scale 0: they come back as zeros
+            want_deq = np.where(np.repeat([c == 0 for c in (63, 0, 11, 0, 30, 0, 63, 5)], 32), 0.0, w[r])
+            assert np.array_equal(deq[r], want_deq), name
+        elif name != "half_way_ties":
+            assert np.array_equal(deq[r], w[r]), name
+
+
+def test_q4_k_closed_form_cases_catch_plausible_mistakes(O):
+    # the cases are only worth something if a wrong quantizer fails them:
+    # restate the quantizer with one mistake at a time and check that some
+    # case's bytes change (the mistakes live here, on the CPU, in the test)
+    import q4k_cases
+    w, want, names = q4k_cases.cases()
+
+    def quantize(x, clamp_min=True, rne=False, swap_hi=False, nibble_swap=False):
+        def nearest(v):
+            return int(np.rint(v)) if rne else int(np.floor(abs(v) + 0.5)) * (1 if v >= 0 else -1)
+
+        def qkx1(xs):
+            xs = np.asarray(xs, np.float32)
+            mn, mx = np.float32(xs.min()), np.float32(xs.max())
+            if mx == mn:
+                return np.float32(0), np.float32(0)
+            if clamp_min and mn > 0:
+                mn = np.float32(0)
+            isc = np.float32(15) / np.float32(mx - mn)
+            lv = np.zeros(32, np.int64)
+            scale = np.float32(1) / isc
+            for _ in range(5):
+                new = np.array([min(15, max(0, nearest(np.float32(isc * np.float32(v - mn))))) for v in xs])
+                changed = not np.array_equal(new, lv)
+                lv = new
+                sumlx = np.float32(0)
+                for v, li in zip(xs, lv):
+                    sumlx = np.float32(sumlx + np.float32(np.float32(v - mn) * np.float32(li)))
+                scale = np.float32(sumlx / np.float32(int((lv * lv).sum())))
+                tot = np.float32(0)
+                for v, li in zip(xs, lv):
+                    tot = np.float32(tot + np.float32(v - np.float32(scale * np.float32(li))))
+                mn = np.float32(tot / np.float32(32))
+                if clamp_min and mn > 0:
+                    mn = np.float32(0)
+                isc = np.float32(1) / scale
+                if not changed:
+                    break
+            return scale, np.float32(-mn)
+
+        out = np.zeros(144, np.uint8)
+        fits = [qkx1(x[32 * j:32 * j + 32]) for j in range(8)]
+        ms, mm = np.float32(0), np.float32(0)
+        for f in fits:  # fold from +0 with a strict compare
+            ms = f[0] if f[0] > ms else ms
+            mm = f[1] if f[1] > mm else mm
+        isc = np.float32(63) / ms if ms > 0 else np.float32(0)
+        imn = np.float32(63) / mm if mm > 0 else np.float32(0)
+        # `as u8` of a negative value wraps; a planted mistake can produce one
+        sc = [min(63, nearest(np.float32(isc * f[0]))) & 63 for f in fits]
+        mi = [min(63, nearest(np.float32(imn * f[1]))) & 63 for f in fits]
+        packed = q4k_cases.pack_scales(sc, mi)
+        if swap_hi:  # high bits of sc[4..7] and m[4..7] exchanged
+            packed = q4k_cases.pack_scales(sc[:4] + mi[4:], mi[:4] + sc[4:])
+        d = np.float16(ms / np.float32(63))
+        dmin = np.float16(mm / np.float32(63))
+        codes = []
+        for j in range(8):
+            dd = np.float32(np.float32(d) * np.float32(sc[j]))
+            dm = np.float32(np.float32(dmin) * np.float32(mi[j]))
+            for v in x[32 * j:32 * j + 32]:
+                codes.append(0 if dd == 0 else min(15, max(0, nearest(np.float32(np.float32(v + dm) / dd)))))
+        if nibble_swap:
+            codes = [codes[(p // 64) * 64 + (p % 64 + 32) % 64] for p in range(256)]
+        out[0:2] = np.array([d]).view(np.uint8)
+        out[2:4] = np.array([dmin]).view(np.uint8)
+        out[4:16] = packed
+        out[16:] = q4k_cases.pack_codes(codes)
+        return out
+
+    # the faithful restatement reproduces every case ...
+    for r in range(len(names)):
+        assert np.array_equal(quantize(w[r]), want[r]), names[r]
+    # ... and each planted mistake breaks at least one
+    for mistake in ({"clamp_min": False}, {"rne": True}, {"swap_hi": True}, {"nibble_swap": True}):
+        broken = [names[r] for r in range(len(names)) if not np.array_equal(quantize(w[r], **mistake), want[r])]
+        assert broken, mistake
+
+
 def _q6k_encode(codes, scales, d):
     """One Q6_K block from 256 6-bit codes, 16 i8 scales and an f16 d, placed
     element by element from the block layout description: value e of half
