@@ -99,7 +99,7 @@ struct Linear {
   int device = 0;
   int64_t n_strips = 0, k_chunks = 0, nbk = 0;
   DevBuf tiles, aux, row_scale, block_scale;
-  DevBuf scratch;  // activation codes for native prefill / local q8
+  DevBuf act_scratch;  // activation codes for native prefill / local q8
   DevBuf gemv_ws;  // stream-K partials of the decode GEMV
   DevBuf gemv_cnt; // per-strip piece counters + work-queue head/exit count (zero between calls)
   DevBuf native_part;  // stream-K partial tiles of the native prefill
@@ -288,7 +288,7 @@ void grow(DevBuf &b, size_t bytes, hipStream_t st, const char *what) {
   b.alloc(bytes);
 }
 
-void ensure_scratch(Linear *L, size_t bytes, hipStream_t st) { grow(L->scratch, bytes, st, "activation scratch"); }
+void ensure_scratch(Linear *L, size_t bytes, hipStream_t st) { grow(L->act_scratch, bytes, st, "activation scratch"); }
 
 // Stream-K partials and tile counters of the native prefill.
 void ensure_native_scratch(Linear *L, size_t part_bytes, size_t cnt_count, hipStream_t st) {
@@ -301,11 +301,42 @@ void ensure_native_scratch(Linear *L, size_t part_bytes, size_t cnt_count, hipSt
   }
 }
 
-void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, int y_dtype, int path,
-                 hipStream_t st, bool swiglu = false) {
+// The scratch one forward call takes, by region, for the kernel it picks.
+struct ForwardPlan {
+  int path = DIALQ_PATH_AUTO;  // resolved: GEMV, GEMM or GEMM_NATIVE
+  int64_t k_pad = 0;           // native: padded K of the activation codes
+  size_t gemv_ws = 0;          // decode workspace (stream-K / work-queue partials)
+  size_t gemv_cnt = 0;         // decode counters (ints): n_strips + 2
+  size_t codes = 0;            // native: activation codes, rounded up to 256 bytes
+  size_t xscale = 0;           // native: activation scales
+  size_t part = 0;             // native: split-K partial tiles
+  size_t ncnt = 0;             // native: split-K tile counters (ints)
+};
+
+// Where a call's scratch lives: the handle's own buffers, grown on demand,
+// or the allocation-free entry point's static array.  Counters are zero
+// before the call and are left zero by the kernels.
+struct ForwardBufs {
+  float *gemv_ws = nullptr;
+  size_t gemv_ws_bytes = 0;
+  int *gemv_cnt = nullptr;
+  uint8_t *codes = nullptr;
+  void *xscale = nullptr;
+  float *part = nullptr;
+  size_t part_bytes = 0;
+  int *ncnt = nullptr;
+  size_t ncnt_count = 0;
+};
+
+WeightView forward_view(const Linear *L, bool swiglu) {
   WeightView w = L->view();
   if (swiglu) w.pair = L->desc.out_dim / 32;  // gate / up halves of out_dim / 2 rows, 16 rows per strip
+  return w;
+}
+
+ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int64_t rows, int path) {
   const int fmt = L->desc.format;
+  ForwardPlan pl;
   if (path == DIALQ_PATH_AUTO) {
     if (rows <= 64) path = DIALQ_PATH_GEMV;
     else if ((fmt == DIALQ_FORMAT_FP8_BLOCK || fmt == DIALQ_FORMAT_MXFP4) &&
@@ -313,48 +344,70 @@ void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, i
       path = DIALQ_PATH_GEMM_NATIVE;
     else path = DIALQ_PATH_GEMM;
   }
+  pl.path = path;
   if (path == DIALQ_PATH_GEMV) {
     if (L->tiles.n >= ((size_t)1 << 31))
       fail("decode kernel addresses weights with 32-bit offsets: %zu resident bytes exceed 2 GiB; split the "
            "output dimension", L->tiles.n);
-    std::lock_guard<std::mutex> lock(L->scratch_mu);
-    grow(L->gemv_ws, gemv_workspace_bytes(w, rows), st, "decode GEMV workspace");
-    hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, (float *)L->gemv_ws.p, L->gemv_ws.n, (int *)L->gemv_cnt.p,
-                          L->gave_up.d, st),
-              "GEMV launch");
-  } else if (path == DIALQ_PATH_GEMM) {
-    hip_check(launch_gemm(w, x, x_dtype, rows, y, y_dtype, st), "GEMM launch");
+    pl.gemv_ws = gemv_workspace_bytes(w, x_dtype, rows);
+    pl.gemv_cnt = (size_t)(L->n_strips + 2);
   } else if (path == DIALQ_PATH_GEMM_NATIVE) {
     if (fmt != DIALQ_FORMAT_FP8_BLOCK && fmt != DIALQ_FORMAT_MXFP4)
       fail("native fp8/fp4 prefill needs an FP8 block or MXFP4 weight, got %s", format_name(fmt));
-    const int64_t k_pad = w.k_chunks * 128;
-    size_t part_bytes = 0, cnt_count = 0;
-    native_workspace(rows, w, part_bytes, cnt_count);
-    std::lock_guard<std::mutex> lock(L->scratch_mu);
-    if (fmt == DIALQ_FORMAT_FP8_BLOCK) {
-      size_t codes = (size_t)(rows * k_pad), off = (codes + 255) / 256 * 256;
-      ensure_scratch(L, off + (size_t)rows * sizeof(float), st);
-      uint8_t *xq = (uint8_t *)L->scratch.p;
-      float *xs = (float *)((uint8_t *)L->scratch.p + off);
-      hip_check(launch_act_fp8(x, x_dtype, rows, w.K, k_pad, xq, xs, st), "activation quantizer");
-      ensure_native_scratch(L, part_bytes, cnt_count, st);
-      hip_check(launch_gemm_native(w, xq, xs, rows, k_pad, y, y_dtype, (float *)L->native_part.p,
-                                   L->native_part.n, (int *)L->native_cnt.p, L->native_cnt.n / sizeof(int), st),
-                "native GEMM launch");
-    } else {
-      size_t codes = (size_t)(rows * k_pad / 2), off = (codes + 255) / 256 * 256;
-      ensure_scratch(L, off + (size_t)(rows * k_pad / 32), st);
-      uint8_t *xq = (uint8_t *)L->scratch.p;
-      uint8_t *xs = (uint8_t *)L->scratch.p + off;
-      hip_check(launch_act_mxfp4(x, x_dtype, rows, w.K, k_pad, xq, xs, st), "activation quantizer");
-      ensure_native_scratch(L, part_bytes, cnt_count, st);
-      hip_check(launch_gemm_native(w, xq, xs, rows, k_pad, y, y_dtype, (float *)L->native_part.p,
-                                   L->native_part.n, (int *)L->native_cnt.p, L->native_cnt.n / sizeof(int), st),
-                "native GEMM launch");
-    }
-  } else {
+    pl.k_pad = w.k_chunks * 128;
+    const size_t codes = fmt == DIALQ_FORMAT_FP8_BLOCK ? (size_t)(rows * pl.k_pad) : (size_t)(rows * pl.k_pad / 2);
+    pl.codes = (codes + 255) / 256 * 256;
+    pl.xscale = fmt == DIALQ_FORMAT_FP8_BLOCK ? (size_t)rows * sizeof(float) : (size_t)(rows * pl.k_pad / 32);
+    native_workspace(rows, w, pl.part, pl.ncnt);
+  } else if (path != DIALQ_PATH_GEMM) {
     fail("unknown path %d", path);
   }
+  return pl;
+}
+
+void launch_forward(const Linear *L, const WeightView &w, const ForwardPlan &pl, const ForwardBufs &b, const void *x,
+                    int x_dtype, int64_t rows, void *y, int y_dtype, hipStream_t st) {
+  if (pl.path == DIALQ_PATH_GEMV) {
+    hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, b.gemv_ws, b.gemv_ws_bytes, b.gemv_cnt, L->gave_up.d, st),
+              "GEMV launch");
+  } else if (pl.path == DIALQ_PATH_GEMM) {
+    hip_check(launch_gemm(w, x, x_dtype, rows, y, y_dtype, st), "GEMM launch");
+  } else {
+    if (L->desc.format == DIALQ_FORMAT_FP8_BLOCK)
+      hip_check(launch_act_fp8(x, x_dtype, rows, w.K, pl.k_pad, b.codes, (float *)b.xscale, st),
+                "activation quantizer");
+    else
+      hip_check(launch_act_mxfp4(x, x_dtype, rows, w.K, pl.k_pad, b.codes, (uint8_t *)b.xscale, st),
+                "activation quantizer");
+    hip_check(launch_gemm_native(w, b.codes, b.xscale, rows, pl.k_pad, y, y_dtype, b.part, b.part_bytes, b.ncnt,
+                                 b.ncnt_count, st),
+              "native GEMM launch");
+  }
+}
+
+// Forward with the handle's own scratch (grown on demand).
+void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, int y_dtype, int path,
+                 hipStream_t st, bool swiglu = false) {
+  const WeightView w = forward_view(L, swiglu);
+  const ForwardPlan pl = plan_forward(L, w, x_dtype, rows, path);
+  std::lock_guard<std::mutex> lock(L->scratch_mu);
+  ForwardBufs b;
+  if (pl.path == DIALQ_PATH_GEMV) {
+    grow(L->gemv_ws, pl.gemv_ws, st, "decode GEMV workspace");
+    b.gemv_ws = (float *)L->gemv_ws.p;
+    b.gemv_ws_bytes = L->gemv_ws.n;
+    b.gemv_cnt = (int *)L->gemv_cnt.p;
+  } else if (pl.path == DIALQ_PATH_GEMM_NATIVE) {
+    ensure_scratch(L, pl.codes + pl.xscale, st);
+    ensure_native_scratch(L, pl.part, pl.ncnt, st);
+    b.codes = (uint8_t *)L->act_scratch.p;
+    b.xscale = b.codes + pl.codes;
+    b.part = (float *)L->native_part.p;
+    b.part_bytes = L->native_part.n;
+    b.ncnt = (int *)L->native_cnt.p;
+    b.ncnt_count = L->native_cnt.n / sizeof(int);
+  }
+  launch_forward(L, w, pl, b, x, x_dtype, rows, y, y_dtype, st);
 }
 
 // A decode launch on this handle whose work-queue wait gave up (it wrote
@@ -416,7 +469,7 @@ void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void 
     std::lock_guard<std::mutex> lock(L->scratch_mu);
     int64_t k_pad = L->k_chunks * 64;
     ensure_scratch(L, (size_t)((k_pad + 255) / 256 * 256 + 256), st);
-    hip_check(launch_local_q8(L->view(), xp, x_dtype, yp, y_dtype, L->scratch.p, st), "local q8 launch");
+    hip_check(launch_local_q8(L->view(), xp, x_dtype, yp, y_dtype, L->act_scratch.p, st), "local q8 launch");
   } else {
     run_forward(L, xp, x_dtype, rows, yp, y_dtype, path, st, swiglu);
   }
@@ -572,7 +625,7 @@ uint64_t dialq_linear_resident_bytes(const void *linear) {
 uint64_t dialq_linear_device_bytes(const void *linear) {
   const Linear *L = (const Linear *)linear;
   if (!L) return 0;
-  return L->tiles.n + L->aux.n + L->row_scale.n + L->block_scale.n + L->scratch.n + L->gemv_ws.n +
+  return L->tiles.n + L->aux.n + L->row_scale.n + L->block_scale.n + L->act_scratch.n + L->gemv_ws.n +
          L->gemv_cnt.n + L->native_part.n + L->native_cnt.n + L->xstage.n;
 }
 

@@ -47,6 +47,7 @@ struct GemvParams {
   size_t ws_bytes;
   int x_pitch;     // bytes per staged activation row (0: not staged)
   int *cnt;        // [n_strips] arrival counters (zero between launches)
+  size_t *query;   // host: non-null = record the workspace bytes, launch nothing
 };
 
 constexpr int kGemvWaves = 4;       // waves per workgroup, whole-strip kernel at >= 1 strip per CU
@@ -731,6 +732,7 @@ struct DynParams {
   int *cnt;        // [n_strips] piece counters, then queue head and exit count
   int *err;        // host-visible word set to 1 when a bounded wait gives up
   int spin_limit;  // polls without progress before a wait gives up
+  size_t *query;   // host: non-null = record the workspace bytes, launch nothing
 };
 
 // A wave whose bounded wait gave up: the launch's output is incomplete.  The
@@ -1105,7 +1107,12 @@ static hipError_t launch_ranges(GemvParams &p, hipStream_t st) {
   const int64_t nseg = p.spw > 0 ? p.spw : per / p.w.k_chunks + 2;
   const size_t park = (size_t)nseg * WV * mrows * 16 * sizeof(float);
   if (park > (size_t)kGemvParkBytes) return hipErrorInvalidConfiguration;
-  if (p.spw == 0 && (size_t)p.G * 2 * mrows * 16 * sizeof(float) > p.ws_bytes) return hipErrorInvalidValue;
+  const size_t need = p.spw == 0 ? (size_t)p.G * 2 * mrows * 16 * sizeof(float) : 0;
+  if (p.query) {
+    if (need > *p.query) *p.query = need;
+    return hipSuccess;
+  }
+  if (need > p.ws_bytes) return hipErrorInvalidValue;
   const size_t xsums = (XL && Pol::XSUB > 0)
                            ? (size_t)mrows * (p.w.k_chunks * FmtTraits<FMT>::CHUNK / (Pol::XSUB > 0 ? Pol::XSUB : 1)) * 4
                            : 0;
@@ -1123,6 +1130,10 @@ static hipError_t launch_dyn(DynParams &p, int64_t mrows, hipStream_t st) {
   p.G = kGemvWgPerCu * device_cus();
   if (p.G > p.NU) p.G = p.NU;
   const size_t need = p.P > 1 ? (size_t)p.w.n_strips * p.P * mrows * 16 * sizeof(float) : 0;
+  if (p.query) {
+    if (need > *p.query) *p.query = need;
+    return hipSuccess;
+  }
   if (need > p.ws_bytes) return hipErrorInvalidValue;
   const size_t lds = kDynCtlBytes + (XL ? (size_t)mrows * p.x_pitch + 32 : 0) +
                      (size_t)kDynQueue * kDynWaves * mrows * 16 * sizeof(float);
@@ -1145,7 +1156,7 @@ static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
     // (the pair's two sums meet in the workgroup's parking LDS)
     // 8 waves: each of the pair's strips streams as a 4-wave plain workgroup
     // would, so the rounds of workgroups over the CUs match the plain launch
-    GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
+    GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt, d.query};
     const int pitch = stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK);
     if (mrows * pitch + 32 <= kGemvSmallStageBytes) {
       p.x_pitch = pitch;
@@ -1155,7 +1166,7 @@ static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
         p, st);
   }
   if (d.w.n_strips >= device_cus()) {
-    GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
+    GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt, d.query};
     p.x_pitch = xl ? stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) : 0;
     if (xl) return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvWaves>(p, st);
     return launch_ranges<FMT, PolT<A, ACT, false, false>, (U_X < kRangeRing ? U_X : kRangeRing), false, kGemvWaves>(
@@ -1168,7 +1179,7 @@ static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
     // K = 5120: 5.3 us for 256..2048 rows where the work queue took 6.8-9.4
     // (3072 rows: 5.7 against 12.0); K = 17408 at 1024-2048 rows 25-35 %
     // faster.
-    GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt};
+    GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt, d.query};
     p.x_pitch = stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK);
     return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvSmallWaves>(p, st);
   }
@@ -1186,7 +1197,7 @@ using Q6kRowsPol = Q6kRowsPolicy<ACT, RP, XL, XS>;
 
 template <int FMT, int ACT>
 static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype,
-                                float *ws, size_t ws_bytes, int *cnt, int *err, hipStream_t st) {
+                                float *ws, size_t ws_bytes, int *cnt, int *err, size_t *query, hipStream_t st) {
   typedef FmtTraits<FMT> T;
   constexpr int XV = (ACT == DIALQ_F32) ? 8 : 4;  // VGPRs per 8-element activation operand
   constexpr bool KQ = FMT == DIALQ_FORMAT_Q4_K || FMT == DIALQ_FORMAT_Q6_K;
@@ -1194,7 +1205,7 @@ static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, v
   const int rows_per_pass = (KQ && M <= 8) ? 8 : 16;
   for (int64_t mb = 0; mb < M; mb += rows_per_pass) {
     const int64_t rem = M - mb, mrows = rem < 16 ? rem : 16;
-    DynParams p{w, x, y, M, mb, y_dtype, 1, 1, 1, 1, 0, ws, ws_bytes, cnt, err, gemv_wait_limit()};
+    DynParams p{w, x, y, M, mb, y_dtype, 1, 1, 1, 1, 0, ws, ws_bytes, cnt, err, gemv_wait_limit(), query};
     hipError_t e;
     if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
       if (rem <= 4)
@@ -1218,27 +1229,19 @@ static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, v
   return hipSuccess;
 }
 
-size_t gemv_workspace_bytes(const WeightView &w, int64_t M) {
-  // work queue: pieces per strip are at most ceil(k_chunks / (kDynWaves * 2))
-  // (ring depth >= 2); equal tile ranges: two partial slots per workgroup
-  const int64_t mrows = M < 16 ? M : 16;
-  const int64_t pmax = (w.k_chunks + kDynWaves * 2 - 1) / (kDynWaves * 2);
-  const size_t dyn = (size_t)w.n_strips * pmax * mrows * 16 * sizeof(float);
-  const size_t ranges = (size_t)gemv_grid(w, mrows) * 2 * mrows * 16 * sizeof(float);
-  return dyn > ranges ? dyn : ranges;
-}
 
 template <int FMT>
 static hipError_t gemv_act(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                           int y_dtype, float *ws, size_t ws_bytes, int *cnt, int *err, hipStream_t st) {
+                           int y_dtype, float *ws, size_t ws_bytes, int *cnt, int *err, size_t *query,
+                           hipStream_t st) {
   switch (x_dtype) {
-    case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
+    case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
     // f16 activations feed f16 MFMAs as they are (f16 weight operands);
     // MXFP4's scaled codes need bf16's exponent range (hi / lo parts)
     case DIALQ_F16:
       return gemv_dispatch<FMT, FMT == DIALQ_FORMAT_MXFP4 ? DIALQ_F16 : kActF16N>(w, x, M, y, y_dtype, ws, ws_bytes,
-                                                                                 cnt, err, st);
-    case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
+                                                                                 cnt, err, query, st);
+    case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
   }
   return hipErrorInvalidValue;
 }
@@ -1253,20 +1256,36 @@ void set_gemv_wait_limit(int64_t polls) {
   g_wait_limit.store(polls < 0 ? kSpinLimit : (int)(polls < kSpinLimit ? polls : kSpinLimit), std::memory_order_relaxed);
 }
 
-hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                       int y_dtype, float *ws, size_t ws_bytes, int *cnt, int *err, hipStream_t st) {
+static hipError_t gemv_fmt(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype,
+                           float *ws, size_t ws_bytes, int *cnt, int *err, size_t *query, hipStream_t st) {
   switch (w.fmt) {
-    case DIALQ_FORMAT_W8A16: return gemv_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
-    case DIALQ_FORMAT_FP8_ROW: return gemv_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
-    case DIALQ_FORMAT_Q8_0: return gemv_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
+    case DIALQ_FORMAT_W8A16: return gemv_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
+    case DIALQ_FORMAT_FP8_ROW: return gemv_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
+    case DIALQ_FORMAT_Q8_0: return gemv_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
     case DIALQ_FORMAT_FP8_BLOCK:
-      return gemv_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
-    case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
-    case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
-    case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
-    case DIALQ_FORMAT_Q6_K: return gemv_act<DIALQ_FORMAT_Q6_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, st);
+      return gemv_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
+    case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
+    case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
+    case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
+    case DIALQ_FORMAT_Q6_K: return gemv_act<DIALQ_FORMAT_Q6_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype, float *ws,
+                       size_t ws_bytes, int *cnt, int *err, hipStream_t st) {
+  return gemv_fmt(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, nullptr, st);
+}
+
+// The launch plan of launch_gemv, run without launching: the largest
+// workspace any of its row-group launches takes (stream-K partials of equal
+// tile ranges, or the work queue's piece partials; whole strips take none).
+size_t gemv_workspace_bytes(const WeightView &w, int x_dtype, int64_t M) {
+  size_t need = 0;
+  if (M <= 0) return 0;
+  if (gemv_fmt(w, nullptr, x_dtype, M, nullptr, DIALQ_BF16, nullptr, 0, nullptr, nullptr, &need, nullptr) != hipSuccess)
+    return 0;
+  return need;
 }
 
 }  // namespace dialq

@@ -51,13 +51,14 @@ hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int6
                             uint8_t *packed, uint8_t *scales, hipStream_t st);
 
 // Decode GEMV: y[M,N] = x[M,K] W^T for any M (16 rows per pass).
-// ws: gemv_workspace_bytes(w, M) of scratch; cnt: n_strips + 2 ints that are
+// ws: gemv_workspace_bytes(w, x_dtype, M) of scratch (exactly what the
+// launches pick, often 0); cnt: n_strips + 2 ints that are
 // zero before the call and are left zero after it.  err: a host-visible int
 // (device address) that a launch sets to 1 when one of the work queue's
 // bounded waits gives up -- its output is then incomplete and cnt may be
 // left non-zero.  The resident tiles must be smaller than 2 GiB (32-bit
 // buffer offsets).
-size_t gemv_workspace_bytes(const WeightView &w, int64_t M);
+size_t gemv_workspace_bytes(const WeightView &w, int x_dtype, int64_t M);
 hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
                        int y_dtype, float *ws, size_t ws_bytes, int *cnt, int *err, hipStream_t st);
 // Polls without progress before a bounded wait of the work queue gives up
