@@ -479,6 +479,114 @@ void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void 
   }
 }
 
+// ---- allocation-free forward ------------------------------------------------
+// dialq_linear_forward_noalloc takes its scratch from this file-scope
+// device array instead of the handle's grown buffers: callers that cannot
+// allocate (code under graph capture, tight serving loops) get the same
+// kernels with no hipMalloc / hipFree on the call path.  Every device that
+// runs the library holds its own copy until the process ends.  Layout:
+//   [0, kNoAllocCntBytes)   counters (decode GEMV per-strip / queue counters,
+//                           or native split-K tile counters); zero between
+//                           calls: zero at load, cleared once per device at
+//                           set-up, and left zero by every call that ends
+//                           normally (the kernels re-arm them)
+//   [kNoAllocCntBytes, ..)  the call's workspace regions, then the aligned
+//                           copy of a misaligned x
+// Calls on one device share the array: calls that overlap in time on one
+// device (different streams, or concurrent host threads) race.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+constexpr size_t kNoAllocCntBytes = 65536;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+__global__ void k_zero_words(uint32_t *p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+std::mutex g_noalloc_mu;
+std::vector<uint8_t *> g_noalloc_ptr;  // per device: the array's device address (null until set up)
+
+// The array's address on the current device `dev`, looked up once per
+// device (hipGetSymbolAddress with that device current); the counter region
+// is cleared on that first use with a fill kernel on `st`.
+uint8_t *noalloc_scratch(int dev, hipStream_t st) {
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if ((int)g_noalloc_ptr.size() <= dev) g_noalloc_ptr.resize((size_t)dev + 1, nullptr);
+  if (!g_noalloc_ptr[dev]) {
+    void *ptr = nullptr;
+    hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    k_zero_words<<<16, 256, 0, st>>>((uint32_t *)ptr, kNoAllocCntBytes / 4);
+    hip_check(hipGetLastError(), "scratch counter clear");
+    g_noalloc_ptr[dev] = (uint8_t *)ptr;
+  }
+  return g_noalloc_ptr[dev];
+}
+
+void forward_noalloc_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void *y, int32_t y_dtype,
+                          int32_t path, void *stream) {
+  if (!L) fail("linear handle is NULL");
+  if (rows < 0) fail("rows must be >= 0, got %lld", (long long)rows);
+  const size_t xs = dtype_size(x_dtype), ys = dtype_size(y_dtype);
+  if (rows == 0) return;
+  if (!x || !y) fail("x and y must not be NULL");
+  if (((uintptr_t)y) % ys) fail("y must be aligned to its element size (%zu bytes)", ys);
+  DeviceGuard dg(L->device);
+  hipStream_t st = (hipStream_t)stream;
+  uint8_t *base = noalloc_scratch(L->device, st);
+  if (__atomic_load_n(L->gave_up.h, __ATOMIC_ACQUIRE)) {
+    // a decode launch on this handle gave up: its counters may be left set
+    // in the shared array as well as the handle's
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hip_check(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
+    if (cs == hipStreamCaptureStatusNone) {
+      hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+      k_zero_words<<<16, 256, 0, st>>>((uint32_t *)base, kNoAllocCntBytes / 4);
+      hip_check(hipGetLastError(), "scratch counter clear");
+    }
+    check_gave_up(L, st);
+  }
+  const int64_t K = L->desc.in_dim;
+  const WeightView w = forward_view(L, false);
+  const ForwardPlan pl = plan_forward(L, w, x_dtype, rows, path);
+  const size_t cnt_ints = pl.path == DIALQ_PATH_GEMV ? pl.gemv_cnt : pl.ncnt;
+  if (cnt_ints * sizeof(int) > kNoAllocCntBytes)
+    fail("dialq_linear_forward_noalloc: this %s weight needs %zu counters; its scratch holds %zu (out_dim up to "
+         "%zu rows for the decode path)", format_name(L->desc.format), cnt_ints, kNoAllocCntBytes / sizeof(int),
+         (kNoAllocCntBytes / sizeof(int) - 2) * 16);
+  // regions after the counters, 256-byte aligned
+  auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+  size_t off = kNoAllocCntBytes;
+  ForwardBufs b;
+  if (pl.path == DIALQ_PATH_GEMV) {
+    b.gemv_cnt = (int *)base;
+    b.gemv_ws = pl.gemv_ws ? (float *)(base + off) : nullptr;
+    b.gemv_ws_bytes = pl.gemv_ws;
+    off += up(pl.gemv_ws);
+  } else if (pl.path == DIALQ_PATH_GEMM_NATIVE) {
+    b.codes = base + off;
+    b.xscale = base + off + pl.codes;
+    off += up(pl.codes + pl.xscale);
+    b.part = pl.part ? (float *)(base + off) : nullptr;
+    b.part_bytes = pl.part;
+    off += up(pl.part);
+    b.ncnt = pl.ncnt ? (int *)base : nullptr;
+    b.ncnt_count = pl.ncnt;
+  }
+  const void *xp = x;
+  const size_t xbytes = (size_t)(rows * K) * xs;
+  const bool stage_x = ((uintptr_t)x) & 15u;
+  const size_t need = off + (stage_x ? up(xbytes) : 0);
+  if (need > kNoAllocScratchBytes)
+    fail("dialq_linear_forward_noalloc: %lld rows of this %s [%lld, %lld] weight need %zu bytes of scratch; the "
+         "allocation-free entry point has %zu (use dialq_linear_forward, or fewer rows per call)",
+         (long long)rows, format_name(L->desc.format), (long long)L->desc.out_dim, (long long)K, need,
+         kNoAllocScratchBytes);
+  if (stage_x) {
+    hip_check(hipMemcpyAsync(base + off, x, xbytes, hipMemcpyDeviceToDevice, st), "hipMemcpyAsync");
+    xp = base + off;
+  }
+  launch_forward(L, w, pl, b, xp, x_dtype, rows, y, y_dtype, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -637,6 +745,13 @@ int dialq_linear_describe(const void *linear, dialq_linear_desc *desc) {
 }
 
 void dialq_debug_set_wait_limit(int64_t polls) { set_gemv_wait_limit(polls); }
+
+int dialq_linear_forward_noalloc(void *linear, const void *x, int32_t x_dtype, int64_t rows, void *y,
+                                 int32_t y_dtype, int32_t path, void *stream, char *error, size_t error_size) {
+  return guarded(error, error_size, [&] {
+    forward_noalloc_impl((Linear *)linear, x, x_dtype, rows, y, y_dtype, path, stream);
+  });
+}
 
 int dialq_linear_forward(void *linear, const void *x, int32_t x_dtype, int64_t rows, void *y,
                          int32_t y_dtype, void *stream, int device_io, char *error, size_t error_size) {

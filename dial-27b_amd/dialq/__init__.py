@@ -77,6 +77,7 @@ def _load():
         "dialq_logits_select": (C.c_int, [P, I32, I64, P, I64, C.c_float, C.c_float, I32, I64, P, P, P, P, SZ,
                                           I32, P, C.c_int, CH, SZ]),
         "dialq_debug_set_wait_limit": (None, [I64]),
+        "dialq_linear_forward_noalloc": (C.c_int, [P, P, I32, I64, P, I32, I32, P, CH, SZ]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -230,6 +231,19 @@ class Linear:
         err = _err()
         rc = lib.dialq_linear_forward_ex(self.h, _ptr(x), xd, rows, _ptr(y), yd, path,
                                          _stream_ptr(stream), int(dev), err, 512)
+        _check(rc, err)
+        return y
+
+    def forward_noalloc(self, x, y, rows=None, *, path=PATH_AUTO, stream=None, x_dtype=None, y_dtype=None):
+        """dialq_linear_forward_noalloc: the same product with the library's
+        static per-device scratch (device tensors only; nothing allocated)."""
+        if rows is None:
+            rows = x.numel() // self.in_dim
+        xd = dtype_code(x) if x_dtype is None else x_dtype
+        yd = dtype_code(y) if y_dtype is None else y_dtype
+        err = _err()
+        rc = lib.dialq_linear_forward_noalloc(self.h, _ptr(x), xd, rows, _ptr(y), yd, path, _stream_ptr(stream),
+                                              err, 512)
         _check(rc, err)
         return y
 

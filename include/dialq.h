@@ -165,6 +165,27 @@ int dialq_linear_forward_ex(void *linear, const void *x, int32_t x_dtype,
                             int32_t path, void *stream, int device_io,
                             char *error, size_t error_size);
 
+/* Allocation-free forward; no counterpart in the reference.  For callers
+ * that cannot allocate device memory during the call: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  The same
+ * kernels as dialq_linear_forward_ex (device pointers only, device_io = 1),
+ * with every scratch buffer -- decode workspace and counters, the native
+ * prefill's activation codes, split-K partials and tile counters, the
+ * aligned copy of a misaligned x -- taken from one static 32 MiB array per
+ * device (held from the first call on that device until the process ends)
+ * instead of the handle's grown buffers.  The call allocates and frees
+ * nothing.  Sizes beyond the array (e.g. native prefill of 1024 rows at
+ * K = 17408 plus split-K partials over 32 MiB, or an out_dim above 262112
+ * rows) return -1 with a message naming the bytes needed.  The array is
+ * shared by every call on a device: calls that overlap on one device (two
+ * streams, two host threads) race; serialize them.  The first call on a
+ * device looks the array up and clears its counters: make it outside
+ * stream capture. */
+int dialq_linear_forward_noalloc(void *linear, const void *x, int32_t x_dtype,
+                                 int64_t rows, void *y, int32_t y_dtype,
+                                 int32_t path, void *stream, char *error,
+                                 size_t error_size);
+
 /* Fused gate_up projection with the SwiGLU epilogue: for a weight whose rows
  * [0, N/2) are the MLP's gate and [N/2, N) its up projection (the
  * MlpGateUpProjection::Fused weight, qwen3_vl/text.rs:424-469),
