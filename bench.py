@@ -23,7 +23,8 @@ dominant kernel and the CPU baseline.
 over rotating copies) plus a 256 MiB device-to-device copy used to scale the
 HBM byte counters; `--profile-lm-head` the same for the lm_head GEMV;
 `--profile-prefill` runs only the prefill GEMMs of one
-layer per format, `--profile-swiglu` the fused gate_up with and without its
+layer per format, `--profile-prefill-gate` only the gate-shape prefill GEMM
+per format (the counter runs), `--profile-swiglu` the fused gate_up with and without its
 SwiGLU epilogue, `--profile-select` the token selection.  They are the
 programs the committed rocprofv3 summaries run.
 """
@@ -55,6 +56,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--copies", type=int, default=3, help="layer copies rotated per step")
+    ap.add_argument("--settle-seconds", type=float, default=2.0,
+                    help="untimed replays of the decode step before the timed region, so that the GPU "
+                         "clocks have left their idle state (reported as settle_s)")
     ap.add_argument("--prefill-iters", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the lm_head decode line")
@@ -72,6 +76,9 @@ def parse():
                     help="only the fused gate_up GEMV / GEMM, plain and with the SwiGLU epilogue (for rocprofv3)")
     ap.add_argument("--profile-select", action="store_true",
                     help="only the token selection over the 27B vocabulary (for rocprofv3)")
+    ap.add_argument("--profile-prefill-gate", action="store_true",
+                    help="only the prefill GEMM of the gate shape 17408x5120 per format, eager (for "
+                         "rocprofv3 counter runs)")
     return ap.parse_args()
 
 
@@ -139,11 +146,13 @@ def decode_pass(dq, lins, xs, ys, stream, shapes=LAYER_27B, swiglu=()):
         run_linear(lin, name, x, y, swiglu, rows=1, path=dq.PATH_GEMV, stream=stream)
 
 
-def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B, swiglu=(), xdtype=None):
+def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B, swiglu=(), xdtype=None, settle=0.0):
     """Wall time of `steps` decode passes, one HIP-graph replay per pass,
     rotating layer copies.  Linears named in `swiglu` (a fused gate_up) run
     with the SwiGLU epilogue; activations and outputs are bf16 unless
-    `xdtype` says otherwise."""
+    `xdtype` says otherwise.  After `warmup` replays, replays continue
+    untimed for `settle` seconds of wall time (clock ramp-up), then exactly
+    `steps` replays are timed."""
     xdtype = xdtype or torch.bfloat16
     xs = [torch.randn(1, k, device=dev).to(xdtype) for _, n, k in shapes]
     ys = [torch.empty(1, out_cols(name, n, swiglu), device=dev, dtype=xdtype) for name, n, k in shapes]
@@ -155,6 +164,13 @@ def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B, swiglu=
     for i in range(warmup):
         graphs[i % len(graphs)].replay()
     torch.cuda.synchronize()
+    t_settle = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t_settle < settle:
+        for _ in range(20):
+            graphs[i % len(graphs)].replay()
+            i += 1
+        torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         graphs[i % len(graphs)].replay()
@@ -345,29 +361,170 @@ def time_select(dq, torch, vocab, dev, reps=50):
     return out
 
 
+def _cpu_host():
+    """What the CPU baseline ran on: model string, core counts, thread setting."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    threads = affinity
+    if env and env.isdigit() and int(env) > 0:
+        threads = min(threads, int(env))
+    return {"cpu_model": model, "nproc_affinity": affinity, "os_cpu_count": os.cpu_count(),
+            "omp_num_threads_env": env, "threads": threads}
+
+
 def cpu_baseline(seconds):
-    """The oracle's multi-threaded CPU GEMV (oracle/cpu_baseline.c) on this
-    host, W8A16 at the gate shape [17408, 5120], M = 1, repeated for a
-    bounded time."""
+    """The CPU baseline (oracle/cpu_baseline.c) on this host's cores, over a
+    bounded sample of the same workload: the W8A16 decode GEMV of the gate
+    linear [17408, 5120] at M = 1 (the headline unit, GB/s of weight bytes),
+    `seconds` split between the portable build and one compiled here with
+    -march=native (the faster is reported), then the Q4_K GEMV of the same
+    shape and the W8A16 prefill GEMM at M = 256 (blocked f32, on-the-fly
+    dequant), native build, for about a third of that each."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O  # the checker library; timed here as the CPU baseline
-    threads = max(1, min(16, os.cpu_count() or 1))
+    host = _cpu_host()
+    threads = host["threads"]
     n, k = 17408, 5120
     rng = np.random.default_rng(0)
     q = rng.integers(-127, 128, (n, k), dtype=np.int8)
     s = np.full(n, 0x3c00, np.uint16)
     x = (rng.normal(size=(1, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
-    O.cpu_w8a16_gemv(x, q, s, threads)
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        O.cpu_w8a16_gemv(x, q, s, threads)
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
-    gbs = (n * k + 2 * n) / dt / 1e9
+
+    def timed(fn, budget):
+        fn()
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget or reps == 0:
+            fn()
+            reps += 1
+        return (time.perf_counter() - t0) / reps, reps
+
+    # both builds of the GEMV, the portable one (x86-64-v3, liboracle.so) and
+    # the -march=native one; the faster is the baseline
+    builds = {}
+    for native in (False, True):
+        dt_, reps_ = timed(lambda: O.cpu_w8a16_gemv(x, q, s, threads, native=native), seconds / 2)
+        builds["native" if native else "portable"] = ((n * k + 2 * n) / dt_ / 1e9, reps_)
+    best = max(builds, key=lambda b: builds[b][0])
+    gbs, reps = builds[best]
+    # random Q4_K super-blocks (the GEMV's cost does not depend on the
+    # values): random codes and 6-bit scales, f16 d = dmin = 2^-10
+    blocks = rng.integers(0, 256, (n, k // 256, 144), dtype=np.uint8)
+    blocks[:, :, 0:4] = np.array([0x00, 0x14, 0x00, 0x14], np.uint8)
+    blocks = blocks.reshape(n, k // 256 * 144)
+    dq4, reps4 = timed(lambda: O.cpu_q4_k_gemv(x, blocks, n, threads, native=True), seconds / 3)
+    xm = (rng.normal(size=(256, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    dgm, repsm = timed(lambda: O.cpu_w8a16_gemm(xm, q, s, threads, native=True), seconds / 3)
+    why = (f"{threads} threads: this host's CPU affinity ({host['nproc_affinity']} CPUs)"
+           + (f" capped by OMP_NUM_THREADS={host['omp_num_threads_env']}" if host["omp_num_threads_env"] else ""))
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"W8A16 decode GEMV [17408x5120] M=1 (the layer's gate linear), {reps} reps, "
-                      f"{threads} OpenMP threads, dequantize-on-the-fly f32 dot per row"}
+                      f"{threads} OpenMP threads, dequantize-on-the-fly f32 dot per row (rows in chunks of 64)",
+            "build": {"portable": "gcc -O3 -march=x86-64-v3 -fopenmp (oracle/lib/liboracle.so)",
+                      "native": "gcc -O3 -march=native -fopenmp, compiled on this host (oracle/Makefile: native)",
+                      "reported": best},
+            "threads_reason": why, **{k_: v for k_, v in host.items() if k_ != "threads"},
+            "legs": {
+                "w8a16_gemv_gate_m1_gbs": round(gbs, 2),
+                "w8a16_gemv_gate_m1_gbs_by_build": {b: round(v[0], 2) for b, v in builds.items()},
+                "q4_k_gemv_gate_m1_gbs": round(n * (k // 256) * 144 / dq4 / 1e9, 2),
+                "q4_k_gemv_reps": reps4,
+                "w8a16_gemm_gate_m256_tflops": round(2.0 * 256 * n * k / dgm / 1e12, 3),
+                "w8a16_gemm_reps": repsm,
+            }}
+
+
+PREFILL_GATE = [("w8a16", 2048, "PATH_GEMM", "bf16"), ("q4_k", 2048, "PATH_GEMM", "bf16"),
+                ("fp8_block", 1024, "PATH_GEMM_NATIVE", "fp8"), ("mxfp4", 1024, "PATH_GEMM_NATIVE", "fp4")]
+
+
+def prefill_gate_linears(dq, torch, dev, name):
+    fmt = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}[name]
+    _, n, k = DOM
+    g = torch.Generator(device=dev).manual_seed(23)
+    return dq.Linear.quantize(fmt, torch.randn(n, k, device=dev, generator=g) * 0.02, scale_dtype=dq.BF16)
+
+
+def profile_prefill_gate_run(dq, torch, dev, launches=5):
+    """Eager launches of the gate-shape prefill per format (the programs of
+    the committed MFMA counter summaries)."""
+    _, n, k = DOM
+    for name, m, path, _ in PREFILL_GATE:
+        lin = prefill_gate_linears(dq, torch, dev, name)
+        x = torch.randn(m, k, device=dev).to(torch.bfloat16)
+        y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        for _ in range(launches):
+            lin.forward(x, y, path=getattr(dq, path))
+        torch.cuda.synchronize()
+        print(f"# profile: {launches} launches of {name} prefill [{n}x{k}] M={m}", flush=True)
+        del lin
+        torch.cuda.empty_cache()
+
+
+def read_mfma_counters():
+    """Per-format MFMA busy fraction and LDS bank-conflict cycles of the gate
+    prefill GEMM from the committed counter summary
+    (profiles/prefill_gate_17408x5120_mfma_counters.md), if present."""
+    path = os.path.join(ROOT, "profiles", "prefill_gate_17408x5120_mfma_counters.md")
+    out = {}
+    try:
+        for line in open(path):
+            if line.startswith("counters:"):
+                _, name, rest = line.split(None, 2)
+                out[name] = {kv.split("=")[0]: float(kv.split("=")[1]) for kv in rest.split()}
+    except (OSError, ValueError, IndexError):
+        return {}
+    return out
+
+
+def time_prefill_gate(dq, torch, dev, reps=10):
+    """The prefill roofline per format: the gate linear 17408x5120 (the
+    layer's largest; gate / up / down tie on flops), `reps` forwards in a
+    captured graph between HIP events on the replay stream.  For the native
+    paths a forward is the activation quantizer plus the GEMM, so the rate
+    is a lower bound for the GEMM kernel."""
+    _, n, k = DOM
+    counters = read_mfma_counters()
+    out = {}
+    for name, m, path, peak_key in PREFILL_GATE:
+        lin = prefill_gate_linears(dq, torch, dev, name)
+        x = torch.randn(m, k, device=dev).to(torch.bfloat16)
+        y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        stream = torch.cuda.current_stream()
+        lin.forward(x, y, path=getattr(dq, path), stream=stream)
+        torch.cuda.synchronize()
+
+        def body(st):
+            for _ in range(reps):
+                lin.forward(x, y, path=getattr(dq, path), stream=st)
+        g = capture(torch, body)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        secs = e0.elapsed_time(e1) * 1e-3 / reps
+        tf = 2.0 * m * n * k / secs / 1e12
+        peak = MFMA_PEAK_TFLOPS[peak_key]
+        out[name] = {"bound": "mfma", "m": m, "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tf / peak, 4), "us_per_forward": round(secs * 1e6, 2),
+                     "flops_per_launch": 2 * m * n * k, **counters.get(name, {})}
+        del lin, g
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -395,11 +552,14 @@ def main():
     if a.profile_select:
         profile_select_run(dq, torch, dev)
         return
+    if a.profile_prefill_gate:
+        profile_prefill_gate_run(dq, torch, dev)
+        return
     fmt_of = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}
 
     # ---- headline: W8A16 decode over the 27B layer -----------------------
     layers = build_layers(dq, torch, dq.W8A16, a.copies, dev)
-    secs = time_decode(dq, torch, layers, a.steps, a.warmup, dev)
+    secs = time_decode(dq, torch, layers, a.steps, a.warmup, dev, settle=a.settle_seconds)
     lbytes = layer_bytes(dq, dq.W8A16)
     value = lbytes * a.steps / secs / 1e9
     per = time_per_linear(dq, torch, layers, dev)
@@ -506,6 +666,11 @@ def main():
         del ls
         torch.cuda.empty_cache()
 
+    roof_prefill = time_prefill_gate(dq, torch, dev) if sweep else None
+    if roof_prefill:
+        print("# prefill roofline (gate 17408x5120): " + ", ".join(
+            f"{k_} {v['achieved']} TFLOP/s ({100 * v['frac']:.1f} %)" for k_, v in roof_prefill.items()),
+            file=sys.stderr, flush=True)
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds)
     line = {
         "metric": METRIC,
@@ -526,6 +691,7 @@ def main():
             "weights_per_layer": sum(n * k for _, n, k in LAYER_27B),
             "weight_bytes_per_step": lbytes,
             "layer_copies_rotated": a.copies,
+            "settle_s": a.settle_seconds,
             "rows": 1,
             "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
         },
@@ -540,6 +706,7 @@ def main():
             "algorithmic_bytes": dbytes,
             "us_per_launch": round(dom_secs * 1e6, 2),
         },
+        "roofline_prefill": roof_prefill,
         "cpu_baseline": cpu,
         **extra,
     }

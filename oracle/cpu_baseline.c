@@ -90,3 +90,72 @@ void cb_q4_k_gemv(const uint16_t *x, int64_t m, int64_t k,
     free(xbuf);
   }
 }
+
+/* Prefill: y[m,n] (f32) = sum_k x[m,k] * dequant(w)[n,k] for M rows, a
+ * blocked f32 GEMM with on-the-fly dequantization.  The bf16 activations are
+ * widened once; each task dequantizes 64 weight rows to f32 (the rayon
+ * chunk size of qwen3_vl/text.rs:315-327) and multiplies them against all
+ * M rows in 4 x 4 register tiles of 8-wide vector accumulators, so every
+ * loaded x and w vector feeds four FMAs. */
+typedef float v8f __attribute__((vector_size(32)));
+
+static inline v8f ld8(const float *p) {
+  v8f v;
+  memcpy(&v, p, sizeof v);
+  return v;
+}
+
+static inline float hsum8(v8f v) {
+  return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+}
+
+void cb_w8a16_gemm(const uint16_t *x, int64_t m, int64_t k, const int8_t *q,
+                   const uint16_t *scale_bf16, int64_t n, float *y,
+                   int threads) {
+  float *xf = (float *)malloc(sizeof(float) * (size_t)(m * k));
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t i = 0; i < m * k; ++i) xf[i] = bf16f(x[i]);
+  const int64_t tasks = (n + ROWS_PER_TASK - 1) / ROWS_PER_TASK;
+#pragma omp parallel num_threads(threads)
+  {
+    float *wf = (float *)malloc(sizeof(float) * (size_t)(ROWS_PER_TASK * k));
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t t = 0; t < tasks; ++t) {
+      const int64_t n0 = t * ROWS_PER_TASK;
+      const int64_t nr = (n0 + ROWS_PER_TASK < n ? ROWS_PER_TASK : n - n0);
+      for (int64_t r = 0; r < nr; ++r) {
+        const int8_t *qr = q + (n0 + r) * k;
+        for (int64_t i = 0; i < k; ++i) wf[r * k + i] = (float)qr[i];
+      }
+      for (int64_t m0 = 0; m0 < m; m0 += 4) {
+        const int mr = (int)(m - m0 < 4 ? m - m0 : 4);
+        for (int64_t j0 = 0; j0 < nr; j0 += 4) {
+          const int jr = (int)(nr - j0 < 4 ? nr - j0 : 4);
+          v8f acc[4][4];
+          memset(acc, 0, sizeof acc);
+          const float *xr[4], *wr[4];
+          for (int a = 0; a < 4; ++a) {
+            xr[a] = xf + (m0 + (a < mr ? a : 0)) * k;
+            wr[a] = wf + (j0 + (a < jr ? a : 0)) * k;
+          }
+          for (int64_t kk = 0; kk + 8 <= k; kk += 8) {
+            const v8f x0 = ld8(xr[0] + kk), x1 = ld8(xr[1] + kk), x2 = ld8(xr[2] + kk), x3 = ld8(xr[3] + kk);
+            const v8f w0 = ld8(wr[0] + kk), w1 = ld8(wr[1] + kk), w2 = ld8(wr[2] + kk), w3 = ld8(wr[3] + kk);
+            acc[0][0] += x0 * w0; acc[0][1] += x0 * w1; acc[0][2] += x0 * w2; acc[0][3] += x0 * w3;
+            acc[1][0] += x1 * w0; acc[1][1] += x1 * w1; acc[1][2] += x1 * w2; acc[1][3] += x1 * w3;
+            acc[2][0] += x2 * w0; acc[2][1] += x2 * w1; acc[2][2] += x2 * w2; acc[2][3] += x2 * w3;
+            acc[3][0] += x3 * w0; acc[3][1] += x3 * w1; acc[3][2] += x3 * w2; acc[3][3] += x3 * w3;
+          }
+          for (int a = 0; a < mr; ++a)
+            for (int b = 0; b < jr; ++b) {
+              float sum = hsum8(acc[a][b]);
+              for (int64_t kk = k & ~(int64_t)7; kk < k; ++kk) sum += xr[a][kk] * wr[b][kk];
+              y[(m0 + a) * n + n0 + j0 + b] = sum * bf16f(scale_bf16[n0 + j0 + b]);
+            }
+        }
+      }
+    }
+    free(wf);
+  }
+  free(xf);
+}

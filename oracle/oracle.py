@@ -73,6 +73,7 @@ def _declare(L):
         "or_local_q8_forward": (None, [_P, _I64, _P, _P, _I64, _P]),
         "cb_w8a16_gemv": (None, [_P, _I64, _I64, _P, _P, _I64, _P, C.c_int]),
         "cb_q4_k_gemv": (None, [_P, _I64, _I64, _P, _I64, _P, C.c_int]),
+        "cb_w8a16_gemm": (None, [_P, _I64, _I64, _P, _P, _I64, _P, C.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -397,20 +398,51 @@ def local_q8_forward(x, q, scale):
 
 
 # ---- CPU baseline (timed by bench.py's cpu_baseline leg) -----------------
-def cpu_w8a16_gemv(x_bf16, q, scale_bf16, threads):
+# `native=True` uses lib/native/libcpu_baseline.so, compiled on the calling
+# host with -march=native (make native); the default is liboracle.so's
+# portable build, which the tests check.
+_native = None
+
+
+def native_lib():
+    global _native
+    if _native is None:
+        # always rebuilt: a copy compiled on another host may use instructions this CPU lacks
+        subprocess.run(["make", "-s", "-B", "-C", _HERE, "native"], check=True)
+        _native = C.CDLL(os.path.join(_HERE, "lib", "native", "libcpu_baseline.so"))
+        for name in ("cb_w8a16_gemv", "cb_q4_k_gemv", "cb_w8a16_gemm"):
+            fn = getattr(_native, name)
+            fn.restype = None
+            fn.argtypes = {"cb_q4_k_gemv": [_P, _I64, _I64, _P, _I64, _P, C.c_int]}.get(
+                name, [_P, _I64, _I64, _P, _P, _I64, _P, C.c_int])
+    return _native
+
+
+def cpu_w8a16_gemv(x_bf16, q, scale_bf16, threads, native=False):
     x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
     m, k = x_bf16.shape
     n = q.shape[0]
     y = np.empty((m, n), np.float32)
-    lib().cb_w8a16_gemv(_p(x_bf16), m, k, _p(q), _p(scale_bf16), n, _p(y), int(threads))
+    (native_lib() if native else lib()).cb_w8a16_gemv(_p(x_bf16), m, k, _p(q), _p(scale_bf16), n, _p(y),
+                                                      int(threads))
     return y
 
 
-def cpu_q4_k_gemv(x_bf16, blocks, n, threads):
+def cpu_q4_k_gemv(x_bf16, blocks, n, threads, native=False):
     x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
     m, k = x_bf16.shape
     y = np.empty((m, n), np.float32)
-    lib().cb_q4_k_gemv(_p(x_bf16), m, k, _p(blocks), n, _p(y), int(threads))
+    (native_lib() if native else lib()).cb_q4_k_gemv(_p(x_bf16), m, k, _p(blocks), n, _p(y), int(threads))
+    return y
+
+
+def cpu_w8a16_gemm(x_bf16, q, scale_bf16, threads, native=False):
+    x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
+    m, k = x_bf16.shape
+    n = q.shape[0]
+    y = np.empty((m, n), np.float32)
+    (native_lib() if native else lib()).cb_w8a16_gemm(_p(x_bf16), m, k, _p(q), _p(scale_bf16), n, _p(y),
+                                                      int(threads))
     return y
 
 
