@@ -371,3 +371,26 @@ def test_reconfigure_drops_a_loaded_output_head(tmp_path, torch_dev):
             assert H.maybe_forward_worker_gguf_output_head(_t(x16).to_device(ROCM), 35) is None, args
     finally:
         H.configure_worker_gguf_from_args(None, False, False, False, True, ROCM, H.DType.F16, 1)
+
+
+@pytest.mark.parametrize("dtype", ["F16", "BF16", "F32"])
+def test_dense_gguf_output_head_is_refused_with_a_message(tmp_path, dtype, torch_dev):
+    # the ROCm GGUF path multiplies Q8_0 / Q4K / Q6K heads (the Q4_K_M and
+    # Q8_0 exports the reference's docs use); a dense lm_head in the file is
+    # refused at load time with a message naming the tensor and its dtype,
+    # never at the first token
+    from gguf_writer import write_gguf
+    meta = [("general.architecture", "STRING", "qwen3vl"), ("qwen3vl.block_count", "U32", 36)]
+    npd = {"F16": np.float16, "F32": np.float32}.get(dtype)
+    raw = (np.zeros((4, 256), npd).tobytes() if npd is not None else np.zeros((4, 256), np.uint16).tobytes())
+    path = tmp_path / f"head-{dtype}.gguf"
+    write_gguf(str(path), meta, [("output_norm.weight", "F32", [256], np.ones(256, np.float32).tobytes()),
+                                 ("output.weight", dtype, [4, 256], raw)])
+    try:
+        H.configure_worker_gguf_from_args(str(path), False, True, False, True, ROCM, H.DType.F16, 36)
+        with pytest.raises(H.DialError, match=f"output.weight has dtype {dtype}; the ROCm GGUF path takes "
+                                              "Q8_0, Q4K and Q6K"):
+            H.load_worker_gguf_output_head(H.OutputHeadConfig(256, 4, 36, 1e-6), True)
+        assert not H.worker_gguf_output_head_enabled()
+    finally:
+        H.configure_worker_gguf_from_args(None, False, False, False, True, ROCM, H.DType.F16, 1)
