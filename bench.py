@@ -7,8 +7,13 @@ are N(0, 0.02), quantized on the GPU by the library's own quantizers;
 activations are bf16 N(0, 1).
 
 A step is one decode pass (M = 1) over the layer's seven linears in W8A16
-(int8 per row + bf16 scale), captured once per layer copy in a HIP graph
-and replayed (the serving loop's launch path; no host work per linear).
+(int8 per row + bf16 scale), as DIAL's split projections call them: q / k / v
+on one activation and gate / up on another run as grouped forwards
+(dialq_linear_forward_group, the replacement of QkvProjection::Split and
+MlpGateUpProjection::Split: one launch each), o and down alone -- four
+launches, captured once per layer copy in a HIP graph and replayed (the
+serving loop's launch path; no host work per linear).  The same seven
+linears as seven separate forwards are reported as decode_gbs_ungrouped.
 Layer copies rotate so the weight working set (COPIES x 341 MB) exceeds the
 256 MB Infinity Cache and the figure measures HBM.  `value` = algorithmic
 weight bytes streamed / wall time of the timed steps, in GB/s.  Extra keys
@@ -19,9 +24,9 @@ without gate_up's SwiGLU epilogue), the quantized lm_head decode GEMV (vocab
 248320 x 5120) and the device token selection after it, the roofline of the
 dominant kernel and the CPU baseline.
 
-`--profile` runs only the dominant kernel (W8A16 gate GEMV, eager launches
-over rotating copies) plus a 256 MiB device-to-device copy used to scale the
-HBM byte counters; `--profile-lm-head` the same for the lm_head GEMV;
+`--profile` runs only the dominant kernel (the grouped W8A16 gate / up
+decode launch, eager, over rotating copies) plus a 256 MiB device-to-device
+copy used to scale the HBM byte counters; `--profile-lm-head` the same for the lm_head GEMV;
 `--profile-prefill` runs only the prefill GEMMs of one
 layer per format, `--profile-prefill-gate` only the gate-shape prefill GEMM
 per format (the counter runs), `--profile-swiglu` the fused gate_up with and without its
@@ -84,6 +89,13 @@ def parse():
 
 DOM = ("gate", 17408, 5120)   # the layer's largest linear (gate/up/down tie on bytes)
 DOM_COPIES = 6                # 6 x 89 MB rotated: beyond the 256 MB Infinity Cache
+# The decode pass as DIAL's split projections call it: q / k / v on one x
+# and gate / up on another, each pair or triple one grouped forward
+# (dialq_linear_forward_group, the replacement of QkvProjection::Split and
+# MlpGateUpProjection::Split), o and down alone -- four launches.
+LAYER_27B_GROUPS = [("qkv", (0, 1, 2)), ("o", (3,)), ("gate_up", (4, 5)), ("down", (6,))]
+DOM_GROUP = ("gate_up", [17408, 17408], 5120)  # the dominant launch of the grouped pass
+DOM_GROUP_COPIES = 3                            # 3 x 178 MB rotated
 
 
 def capture(torch, fn):
@@ -96,8 +108,9 @@ def capture(torch, fn):
 
 def read_traffic():
     """HBM bytes per launch of the dominant kernel from the committed PMC
-    summary (profiles/gemv_w8a16_gate_17408x5120_traffic.txt), if present."""
-    path = os.path.join(ROOT, "profiles", "gemv_w8a16_gate_17408x5120_traffic.txt")
+    summary (profiles/gemv_w8a16_gate_up_group_2x17408x5120_traffic.txt), if
+    present."""
+    path = os.path.join(ROOT, "profiles", "gemv_w8a16_gate_up_group_2x17408x5120_traffic.txt")
     try:
         vals = {}
         for line in open(path):
@@ -141,26 +154,41 @@ def run_linear(lin, name, x, y, swiglu, **kw):
         lin.forward(x, y, **kw)
 
 
-def decode_pass(dq, lins, xs, ys, stream, shapes=LAYER_27B, swiglu=()):
+def decode_pass(dq, lins, xs, ys, stream, shapes=LAYER_27B, swiglu=(), groups=None):
+    if groups is not None:
+        for (gname, idx), x, y in zip(groups, xs, ys):
+            if len(idx) == 1:
+                lins[idx[0]].forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+            else:
+                dq.forward_group([lins[i] for i in idx], x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+        return
     for lin, x, y, (name, _, _) in zip(lins, xs, ys, shapes):
         run_linear(lin, name, x, y, swiglu, rows=1, path=dq.PATH_GEMV, stream=stream)
 
 
-def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B, swiglu=(), xdtype=None, settle=0.0):
+def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B, swiglu=(), xdtype=None, settle=0.0,
+                groups=None):
     """Wall time of `steps` decode passes, one HIP-graph replay per pass,
     rotating layer copies.  Linears named in `swiglu` (a fused gate_up) run
     with the SwiGLU epilogue; activations and outputs are bf16 unless
     `xdtype` says otherwise.  After `warmup` replays, replays continue
     untimed for `settle` seconds of wall time (clock ramp-up), then exactly
-    `steps` replays are timed."""
+    `steps` replays are timed.  With `groups` ([(name, indices of shapes)]),
+    the linears of a group share one x and run as one grouped forward into
+    their concatenated output."""
     xdtype = xdtype or torch.bfloat16
-    xs = [torch.randn(1, k, device=dev).to(xdtype) for _, n, k in shapes]
-    ys = [torch.empty(1, out_cols(name, n, swiglu), device=dev, dtype=xdtype) for name, n, k in shapes]
+    if groups is not None:
+        xs = [torch.randn(1, shapes[idx[0]][2], device=dev).to(xdtype) for _, idx in groups]
+        ys = [torch.empty(1, sum(shapes[i][1] for i in idx), device=dev, dtype=xdtype) for _, idx in groups]
+    else:
+        xs = [torch.randn(1, k, device=dev).to(xdtype) for _, n, k in shapes]
+        ys = [torch.empty(1, out_cols(name, n, swiglu), device=dev, dtype=xdtype) for name, n, k in shapes]
     stream = torch.cuda.current_stream()
     for lins in layers:  # eager first: sizes the GEMV workspaces outside capture
-        decode_pass(dq, lins, xs, ys, stream, shapes, swiglu)
+        decode_pass(dq, lins, xs, ys, stream, shapes, swiglu, groups)
     torch.cuda.synchronize()
-    graphs = [capture(torch, lambda st, l=lins: decode_pass(dq, l, xs, ys, st, shapes, swiglu)) for lins in layers]
+    graphs = [capture(torch, lambda st, l=lins: decode_pass(dq, l, xs, ys, st, shapes, swiglu, groups))
+              for lins in layers]
     for i in range(warmup):
         graphs[i % len(graphs)].replay()
     torch.cuda.synchronize()
@@ -203,6 +231,40 @@ def time_launches(dq, torch, lins, k, n, dev, reps=60):
     return e0.elapsed_time(e1) / reps * 1e-3  # seconds per launch
 
 
+def time_group_launches(dq, torch, groups_of_lins, k, n_total, dev, reps=60):
+    """Average device time of one grouped decode launch: `reps` grouped
+    forwards over the rotating member lists, in a graph between HIP events
+    on the replay stream."""
+    x = torch.randn(1, k, device=dev).to(torch.bfloat16)
+    y = torch.empty(1, n_total, device=dev, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream()
+    for lins in groups_of_lins:
+        dq.forward_group(lins, x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+    torch.cuda.synchronize()
+
+    def body(st):
+        for i in range(reps):
+            dq.forward_group(groups_of_lins[i % len(groups_of_lins)], x, y, rows=1, path=dq.PATH_GEMV, stream=st)
+    g = capture(torch, body)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    g.replay()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e-3
+
+
+def time_per_group(dq, torch, layers, dev):
+    out = {}
+    for gname, idx in LAYER_27B_GROUPS:
+        members = [[l[i] for i in idx] for l in layers]
+        out[gname] = time_group_launches(dq, torch, members, LAYER_27B[idx[0]][2],
+                                         sum(LAYER_27B[i][1] for i in idx), dev)
+    return out
+
+
 def time_per_linear(dq, torch, layers, dev):
     out = {}
     for li, (name, n, k) in enumerate(LAYER_27B):
@@ -211,26 +273,27 @@ def time_per_linear(dq, torch, layers, dev):
 
 
 def profile_run(dq, torch, dev, launches):
-    """Dominant kernel only, eager launches, plus the calibration copy."""
-    name, n, k = DOM
+    """Dominant kernel only -- the grouped gate / up decode launch (two
+    17408x5120 W8A16 members, 178 MB) over rotating copies, eager -- plus
+    the calibration copy."""
+    name, ns, k = DOM_GROUP
     g = torch.Generator(device=dev).manual_seed(7)
-    lins = []
-    for _ in range(DOM_COPIES):
-        w = torch.randn(n, k, device=dev, generator=g, dtype=torch.float32) * 0.02
-        lins.append(dq.Linear.quantize(dq.W8A16, w, scale_dtype=dq.BF16))
-        del w
+    groups = []
+    for _ in range(DOM_GROUP_COPIES):
+        groups.append([dq.Linear.quantize(dq.W8A16, torch.randn(n, k, device=dev, generator=g) * 0.02,
+                                          scale_dtype=dq.BF16) for n in ns])
     x = torch.randn(1, k, device=dev).to(torch.bfloat16)
-    y = torch.empty(1, n, device=dev, dtype=torch.bfloat16)
+    y = torch.empty(1, sum(ns), device=dev, dtype=torch.bfloat16)
     stream = torch.cuda.current_stream()
     for i in range(launches):
-        lins[i % DOM_COPIES].forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+        dq.forward_group(groups[i % DOM_GROUP_COPIES], x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
     torch.cuda.synchronize()
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"# profile: {launches} launches of W8A16 {name} [{n}x{k}] M=1; 3 copies of 256 MiB "
+    print(f"# profile: {launches} grouped launches of W8A16 {name} 2 x [{ns[0]}x{k}] M=1; 3 copies of 256 MiB "
           "(calibration: 268435456 bytes read and written per copy)", flush=True)
 
 
@@ -559,34 +622,45 @@ def main():
 
     # ---- headline: W8A16 decode over the 27B layer -----------------------
     layers = build_layers(dq, torch, dq.W8A16, a.copies, dev)
-    secs = time_decode(dq, torch, layers, a.steps, a.warmup, dev, settle=a.settle_seconds)
+    secs = time_decode(dq, torch, layers, a.steps, a.warmup, dev, settle=a.settle_seconds, groups=LAYER_27B_GROUPS)
     lbytes = layer_bytes(dq, dq.W8A16)
     value = lbytes * a.steps / secs / 1e9
+    per_group = time_per_group(dq, torch, layers, dev)
+    # the same seven linears as seven separate forwards (no grouping)
+    usteps = max(a.steps // 3, 10)
+    su = time_decode(dq, torch, layers, usteps, 10, dev, settle=a.settle_seconds / 4)
+    value_ungrouped = lbytes * usteps / su / 1e9
     per = time_per_linear(dq, torch, layers, dev)
     # the same decode with f16 activations (the GGUF worker's runtime dtype)
     fsteps16 = max(a.steps // 3, 10)
-    s16 = time_decode(dq, torch, layers, fsteps16, 10, dev, xdtype=torch.float16)
+    s16 = time_decode(dq, torch, layers, fsteps16, 10, dev, xdtype=torch.float16, groups=LAYER_27B_GROUPS)
     value_f16 = layer_bytes(dq, dq.W8A16) * fsteps16 / s16 / 1e9
-    # dominant kernel: the gate GEMV (the largest linear), timed over
-    # DOM_COPIES rotating copies so no launch finds its weight in the cache
-    dom, dn, dk = DOM
+    del layers
+    torch.cuda.empty_cache()
+    # dominant kernel: the grouped gate / up launch (the largest of the four),
+    # timed over DOM_GROUP_COPIES rotating copies so no launch finds its
+    # weights in the cache
+    dom, dns, dk = DOM_GROUP
     gd = torch.Generator(device=dev).manual_seed(11)
-    dlins = []
-    for _ in range(DOM_COPIES):
-        w = torch.randn(dn, dk, device=dev, generator=gd, dtype=torch.float32) * 0.02
-        dlins.append(dq.Linear.quantize(dq.W8A16, w, scale_dtype=dq.BF16))
-        del w
-    dom_secs = time_launches(dq, torch, dlins, dk, dn, dev)
-    del dlins
-    # algorithmic bytes per launch: int8 codes + bf16 row scales + x + y
-    dbytes = dq.raw_weight_bytes(dq.W8A16, dn, dk) + 2 * dk + 2 * dn
+    dgroups = [[dq.Linear.quantize(dq.W8A16, torch.randn(n, dk, device=dev, generator=gd) * 0.02,
+                                   scale_dtype=dq.BF16) for n in dns] for _ in range(DOM_GROUP_COPIES)]
+    dom_secs = time_group_launches(dq, torch, dgroups, dk, sum(dns), dev)
+    del dgroups
+    torch.cuda.empty_cache()
+    # algorithmic bytes per launch: int8 codes + bf16 row scales of both
+    # members + x + y
+    dbytes = sum(dq.raw_weight_bytes(dq.W8A16, n, dk) for n in dns) + 2 * dk + 2 * sum(dns)
     achieved = dbytes / dom_secs / 1e9
     traffic = read_traffic()
-    print(f"# w8a16 decode: {value:.1f} GB/s over the layer; per-launch us: "
+    print(f"# w8a16 decode: {value:.1f} GB/s over the layer (4 launches: q/k/v and gate/up grouped); per-launch us: "
+          + ", ".join(f"{k}={v * 1e6:.1f}" for k, v in per_group.items()), file=sys.stderr, flush=True)
+    print(f"# w8a16 decode, seven separate forwards: {value_ungrouped:.1f} GB/s; per-launch us: "
           + ", ".join(f"{k}={v * 1e6:.1f}" for k, v in per.items()), file=sys.stderr, flush=True)
-
     print(f"# w8a16 decode with f16 activations: {value_f16:.1f} GB/s", file=sys.stderr, flush=True)
+    layers = build_layers(dq, torch, dq.W8A16, 1, dev)
     extra = {"decode_gbs": {"w8a16": round(value, 1)}, "decode_gbs_f16_activations": {"w8a16": round(value_f16, 1)},
+             "decode_gbs_ungrouped": {"w8a16": round(value_ungrouped, 1)},
+             "decode_us_per_launch_w8a16_grouped": {k: round(v * 1e6, 2) for k, v in per_group.items()},
              "decode_us_per_launch_w8a16":
              {k: round(v * 1e6, 2) for k, v in per.items()}, "prefill_tflops": {}, "prefill_pct_mfma_peak": {}}
     sweep = [s for s in a.sweep.split(",") if s]
@@ -640,7 +714,7 @@ def main():
             continue
         fmt = fmt_of[name]
         ls = build_layers(dq, torch, fmt, a.copies if fmt != dq.MXFP4 and fmt != dq.Q4_K else a.copies + 2, dev)
-        sd = time_decode(dq, torch, ls, max(a.steps // 3, 10), 10, dev)
+        sd = time_decode(dq, torch, ls, max(a.steps // 3, 10), 10, dev, groups=LAYER_27B_GROUPS)
         gbs = layer_bytes(dq, fmt) * max(a.steps // 3, 10) / sd / 1e9
         extra["decode_gbs"][name] = round(gbs, 1)
         if fmt in (dq.FP8_BLOCK, dq.MXFP4):
@@ -687,7 +761,8 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "27B-class dense layer linears (hidden 5120; q 6144x5120, k/v 1024x5120, "
-                        "o 5120x6144, gate/up 17408x5120, down 5120x17408), W8A16 decode GEMV, M=1",
+                        "o 5120x6144, gate/up 17408x5120, down 5120x17408), W8A16 decode GEMV, M=1; "
+                        "q/k/v and gate/up as grouped forwards (4 launches)",
             "weights_per_layer": sum(n * k for _, n, k in LAYER_27B),
             "weight_bytes_per_step": lbytes,
             "layer_copies_rotated": a.copies,
@@ -697,7 +772,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"k_gemv W8A16 bf16 ({dom} {dn}x{dk}, M=1)",
+            "kernel": f"k_gemv W8A16 bf16, grouped {dom} (2 x {dns[0]}x{dk}, M=1)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

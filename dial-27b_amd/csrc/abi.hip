@@ -385,10 +385,11 @@ void launch_forward(const Linear *L, const WeightView &w, const ForwardPlan &pl,
   }
 }
 
-// Forward with the handle's own scratch (grown on demand).
-void run_forward(Linear *L, const void *x, int x_dtype, int64_t rows, void *y, int y_dtype, int path,
-                 hipStream_t st, bool swiglu = false) {
-  const WeightView w = forward_view(L, swiglu);
+// Forward of the weight view `w` of handle L (its own view, or a member's
+// view into a concatenated output) with the handle's own scratch, grown on
+// demand.
+void run_forward(Linear *L, const WeightView &w, const void *x, int x_dtype, int64_t rows, void *y, int y_dtype,
+                 int path, hipStream_t st) {
   const ForwardPlan pl = plan_forward(L, w, x_dtype, rows, path);
   std::lock_guard<std::mutex> lock(L->scratch_mu);
   ForwardBufs b;
@@ -471,8 +472,93 @@ void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void 
     ensure_scratch(L, (size_t)((k_pad + 255) / 256 * 256 + 256), st);
     hip_check(launch_local_q8(L->view(), xp, x_dtype, yp, y_dtype, L->act_scratch.p, st), "local q8 launch");
   } else {
-    run_forward(L, xp, x_dtype, rows, yp, y_dtype, path, st, swiglu);
+    run_forward(L, forward_view(L, swiglu), xp, x_dtype, rows, yp, y_dtype, path, st);
   }
+  if (!device_io) {
+    hip_check(hipMemcpyAsync(y, yp, ybytes, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
+    hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+  }
+}
+
+// ---- grouped forward ---------------------------------------------------------
+// y = cat([x W_0^T, ..., x W_{n-1}^T], -1) for handles that share x: the
+// decode path runs the strips of up to four same-format members in one
+// launch (one workgroup per strip, x staged once per workgroup as in a
+// single forward); every other case runs one launch per member, each
+// writing its columns of the concatenated output.
+constexpr int kGroupMax = 4;
+
+void forward_group_impl(Linear *const *Ls, int32_t n, const void *x, int32_t x_dtype, int64_t rows, void *y,
+                        int32_t y_dtype, int32_t path, void *stream, int device_io) {
+  if (!Ls || n < 1) fail("a grouped forward needs at least one handle, got %d", (int)n);
+  for (int j = 0; j < n; ++j)
+    if (!Ls[j]) fail("linear handle %d of the group is NULL", j);
+  const int64_t K = Ls[0]->desc.in_dim;
+  int64_t ntot = 0;
+  for (int j = 0; j < n; ++j) {
+    if (Ls[j]->desc.in_dim != K)
+      fail("grouped forward: handle %d has in_dim %lld, handle 0 has %lld (the members share x)", j,
+           (long long)Ls[j]->desc.in_dim, (long long)K);
+    if (Ls[j]->device != Ls[0]->device)
+      fail("grouped forward: handle %d lives on device %d, handle 0 on %d", j, Ls[j]->device, Ls[0]->device);
+    ntot += Ls[j]->desc.out_dim;
+  }
+  if (rows < 0) fail("rows must be >= 0, got %lld", (long long)rows);
+  const size_t xs = dtype_size(x_dtype), ys = dtype_size(y_dtype);
+  if (rows == 0) return;
+  if (!x || !y) fail("x and y must not be NULL");
+  DeviceGuard dg(Ls[0]->device);
+  hipStream_t st = (hipStream_t)stream;
+  for (int j = 0; j < n; ++j) check_gave_up(Ls[j], st);
+  const size_t xbytes = (size_t)(rows * K) * xs, ybytes = (size_t)(rows * ntot) * ys;
+  DevBuf dx, dy;
+  const void *xp = x;
+  void *yp = y;
+  if (!device_io) {
+    stage_in(dx, x, xbytes, true, st);
+    dy.alloc(ybytes);
+    xp = dx.p;
+    yp = dy.p;
+  } else {
+    if (((uintptr_t)yp) % ys) fail("y must be aligned to its element size (%zu bytes)", ys);
+    if (((uintptr_t)x) & 15u) {  // staged once, in the first member's buffer
+      std::lock_guard<std::mutex> lock(Ls[0]->scratch_mu);
+      grow(Ls[0]->xstage, xbytes, st, "aligned copy of a misaligned x");
+      hip_check(hipMemcpyAsync(Ls[0]->xstage.p, x, xbytes, hipMemcpyDeviceToDevice, st), "hipMemcpyAsync");
+      xp = Ls[0]->xstage.p;
+    }
+  }
+  std::vector<WeightView> views((size_t)n);
+  std::vector<void *> outs((size_t)n);
+  std::vector<int> paths((size_t)n);
+  int64_t off = 0;
+  for (int j = 0; j < n; ++j) {
+    views[j] = forward_view(Ls[j], false);
+    views[j].ldy = ntot;
+    outs[j] = (uint8_t *)yp + (size_t)off * ys;
+    off += Ls[j]->desc.out_dim;
+    paths[j] = plan_forward(Ls[j], views[j], x_dtype, rows, path).path;
+  }
+  std::vector<bool> done((size_t)n, false);
+  // runs of up to four consecutive decode members of one format: one launch
+  for (int j = 0; j < n;) {
+    int e = j + 1;
+    while (e < n && e - j < kGroupMax && paths[e] == DIALQ_PATH_GEMV && paths[j] == DIALQ_PATH_GEMV &&
+           Ls[e]->desc.format == Ls[j]->desc.format)
+      ++e;
+    if (e - j >= 2) {
+      for (int i = j; i < e; ++i)
+        if (Ls[i]->tiles.n >= ((size_t)1 << 31)) fail("decode kernel addresses weights with 32-bit offsets");
+      const hipError_t r = launch_gemv_group(&views[j], &outs[j], e - j, xp, x_dtype, rows, y_dtype, st);
+      if (r == hipSuccess)
+        for (int i = j; i < e; ++i) done[i] = true;
+      else if (r != hipErrorNotSupported)
+        hip_check(r, "grouped GEMV launch");
+    }
+    j = e;
+  }
+  for (int j = 0; j < n; ++j)
+    if (!done[j]) run_forward(Ls[j], views[j], xp, x_dtype, rows, outs[j], y_dtype, path, st);
   if (!device_io) {
     hip_check(hipMemcpyAsync(y, yp, ybytes, hipMemcpyDeviceToHost, st), "hipMemcpyAsync");
     hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
@@ -742,6 +828,14 @@ int dialq_linear_describe(const void *linear, dialq_linear_desc *desc) {
   if (!L || !desc) return -1;
   *desc = L->desc;
   return 0;
+}
+
+int dialq_linear_forward_group(void *const *linears, int32_t n, const void *x, int32_t x_dtype, int64_t rows,
+                               void *y, int32_t y_dtype, int32_t path, void *stream, int device_io, char *error,
+                               size_t error_size) {
+  return guarded(error, error_size, [&] {
+    forward_group_impl((Linear *const *)linears, n, x, x_dtype, rows, y, y_dtype, path, stream, device_io);
+  });
 }
 
 void dialq_debug_set_wait_limit(int64_t polls) { set_gemv_wait_limit(polls); }

@@ -339,13 +339,14 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
           if (j >= I) continue;
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (rb + i < p.M) store_out(p.y, (rb + i) * I + j, p.y_dtype, silu_mul(mine[n * 4 + i], up[n * 4 + i]));
+            if (rb + i < p.M) store_out(p.y, (rb + i) * out_ld(w) + j, p.y_dtype, silu_mul(mine[n * 4 + i], up[n * 4 + i]));
         }
       }
     }
     return;
   }
   const bool full = m0 + S::ROWS <= p.M;
+  const int64_t ldy = out_ld(w);
   auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
     typedef decltype(yd) Y;
     constexpr bool CHK = decltype(chk)::value;  // row checks only for the ragged last row tile
@@ -357,10 +358,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms) {
         const int64_t rb = m0 + ms * 16 + g * 4;
-        typename Y::T *py = (typename Y::T *)p.y + rb * w.N + col;
+        typename Y::T *py = (typename Y::T *)p.y + rb * ldy + col;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (!CHK || rb + i < p.M) py[i * w.N] = Y::conv(acc[ms][n][i] * scale);
+          if (!CHK || rb + i < p.M) py[i * ldy] = Y::conv(acc[ms][n][i] * scale);
       }
     }
   };
@@ -536,7 +537,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int64_t row = rb + 8 * (v / 4) + (v % 4);
-            if (row < p.M) store_out(p.y, row * I + j, p.y_dtype, silu_mul(mine[v], up[v]));
+            if (row < p.M) store_out(p.y, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[v], up[v]));
           }
         }
       }
@@ -544,6 +545,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
     return;
   }
   const bool full = m0 + ROWS <= p.M;
+  const int64_t ldy = out_ld(w);
   auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
     typedef decltype(yd) Y;
     constexpr bool CHK = decltype(chk)::value;  // row checks only for the ragged last row tile
@@ -555,11 +557,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int64_t rb = m0 + mt * 32 + 4 * h;
-        typename Y::T *py = (typename Y::T *)p.y + rb * w.N + col;
+        typename Y::T *py = (typename Y::T *)p.y + rb * ldy + col;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int rr = 8 * (v / 4) + (v % 4);
-          if (!CHK || rb + rr < p.M) py[rr * w.N] = Y::conv(acc[mt][q][v] * scale);
+          if (!CHK || rb + rr < p.M) py[rr * ldy] = Y::conv(acc[mt][q][v] * scale);
         }
       }
     }
@@ -1032,7 +1034,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
               const int64_t row = rbase + 8 * (e / 4) + (e % 4);
-              if (row < p.M) store_out(p.y, row * I + j, p.y_dtype, silu_mul(mine[e], up[e]));
+              if (row < p.M) store_out(p.y, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[e], up[e]));
             }
           }
         }
@@ -1040,7 +1042,8 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
       return;
     }
     const bool full = m0 + ROWS <= p.M;
-    auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
+    const int64_t ldy = out_ld(w);
+  auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
       typedef decltype(yd) Y;
       constexpr bool CHK = decltype(chk)::value;  // row checks only for the ragged last row tile
 #pragma unroll
@@ -1050,11 +1053,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const int64_t rbase = m0 + mt * 32 + 4 * h;
-          typename Y::T *py = (typename Y::T *)p.y + rbase * w.N + col;
+          typename Y::T *py = (typename Y::T *)p.y + rbase * ldy + col;
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int rr = 8 * (e / 4) + (e % 4);
-            if (!CHK || rbase + rr < p.M) py[rr * w.N] = Y::conv(sum[(mt * 2 + q) * 16 + e] * rowf[mt][e]);
+            if (!CHK || rbase + rr < p.M) py[rr * ldy] = Y::conv(sum[(mt * 2 + q) * 16 + e] * rowf[mt][e]);
           }
         }
       }

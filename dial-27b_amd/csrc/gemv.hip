@@ -34,8 +34,10 @@
 
 namespace dialq {
 
+constexpr int kGemvMaxGroup = 4;  // handles one grouped launch covers
+
 struct GemvParams {
-  WeightView w;
+  WeightView w;  // the weight (a grouped launch: its first member)
   const void *x;
   void *y;
   int64_t M;       // total rows of x / y
@@ -48,6 +50,13 @@ struct GemvParams {
   int x_pitch;     // bytes per staged activation row (0: not staged)
   int *cnt;        // [n_strips] arrival counters (zero between launches)
   size_t *query;   // host: non-null = record the workspace bytes, launch nothing
+  // Grouped launch (nm > 1, whole strips only): members share x and K;
+  // workgroup b takes strip b - sbase[j] of member j, sbase[j] <= b <
+  // sbase[j + 1], and writes through ym[j].
+  int nm;
+  int sbase[kGemvMaxGroup + 1];
+  WeightView wm[kGemvMaxGroup];
+  void *ym[kGemvMaxGroup];
 };
 
 constexpr int kGemvWaves = 4;       // waves per workgroup, whole-strip kernel at >= 1 strip per CU
@@ -476,10 +485,20 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int W = WV;
   constexpr int BY = ActTraits<Pol::XACT>::BYTES;
-  const WeightView &w = p.w;
+  WeightView w = p.w;
+  void *yout = p.y;
+  int b = blockIdx.x;
+  if (p.nm > 1) {  // grouped launch: this workgroup's member (uniform)
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < kGemvMaxGroup; ++i) j += (i < p.nm && b >= p.sbase[i]) ? 1 : 0;
+    w = p.wm[j];
+    yout = p.ym[j];
+    b -= p.sbase[j];
+  }
+  const int64_t ldy = out_ld(w);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int b = blockIdx.x;
   const int kc = (int)w.k_chunks;
   const int64_t total = w.n_strips * w.k_chunks;
   int lo, hi;
@@ -609,7 +628,7 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
           gs += part[(size_t)ww * slot_floats + e];
           us += part[(size_t)(W + ww) * slot_floats + e];
         }
-        store_out(p.y, (p.m_base + m) * ((int64_t)pair * 16) + ng, p.y_dtype, silu_mul(gs * sg, us * su));
+        store_out(yout, (p.m_base + m) * ldy + ng, p.y_dtype, silu_mul(gs * sg, us * su));
       }
     }
     return;
@@ -635,7 +654,7 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int e = lane + 64 * q, m = e >> 4;
-        if (e < slot_floats && n < w.N) store_out(p.y, (p.m_base + m) * w.N + n, p.y_dtype, v[q] * scale);
+        if (e < slot_floats && n < w.N) store_out(yout, (p.m_base + m) * ldy + n, p.y_dtype, v[q] * scale);
       }
       continue;
     }
@@ -684,7 +703,7 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int e = lane + 64 * q, m = e >> 4;
-      if (e < slot_floats && n < w.N) store_out(p.y, (p.m_base + m) * w.N + n, p.y_dtype, a[q] * scale);
+      if (e < slot_floats && n < w.N) store_out(yout, (p.m_base + m) * ldy + n, p.y_dtype, a[q] * scale);
     }
     if (lane == 0) __hip_atomic_store(&p.cnt[sj], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -733,6 +752,7 @@ struct DynParams {
   int *err;        // host-visible word set to 1 when a bounded wait gives up
   int spin_limit;  // polls without progress before a wait gives up
   size_t *query;   // host: non-null = record the workspace bytes, launch nothing
+  const GemvParams *group;  // host: grouped launch (members, strip bases, outputs), or null
 };
 
 // A wave whose bounded wait gave up: the launch's output is incomplete.  The
@@ -782,7 +802,7 @@ __device__ __forceinline__ void store_strip(const DynParams &p, int s, int slot_
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int e = lane + 64 * q, m = e >> 4;
-    if (e < slot_floats && n < w.N) store_out(p.y, (p.m_base + m) * w.N + n, p.y_dtype, v[q] * scale);
+    if (e < slot_floats && n < w.N) store_out(p.y, (p.m_base + m) * out_ld(w) + n, p.y_dtype, v[q] * scale);
   }
 }
 
@@ -1103,6 +1123,7 @@ static hipError_t launch_ranges(GemvParams &p, hipStream_t st) {
   const int64_t total = p.w.n_strips * p.w.k_chunks;
   p.spw = p.w.pair ? 2 : gemv_spw(p.w, mrows, XL);  // SwiGLU: whole gate / up strip pairs
   p.G = p.spw > 0 ? (int)((p.w.n_strips + p.spw - 1) / p.spw) : gemv_grid(p.w, mrows);
+  if (p.nm > 1) p.G = p.sbase[p.nm];  // grouped: one workgroup per strip of every member
   const int64_t per = p.spw > 0 ? p.spw * p.w.k_chunks : (total + p.G - 1) / p.G;
   const int64_t nseg = p.spw > 0 ? p.spw : per / p.w.k_chunks + 2;
   const size_t park = (size_t)nseg * WV * mrows * 16 * sizeof(float);
@@ -1151,6 +1172,24 @@ static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
   constexpr int BY = ActTraits<ACT>::BYTES;
   const bool xl = mrows * stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) + 32 <= kGemvStageBytes;
   constexpr int UR = U_XL < kRangeRing ? U_XL : kRangeRing;
+  if (d.group) {
+    // Grouped launch: the strips of every member, whole strips with staged
+    // activations only (4 waves per workgroup at one strip per CU or more,
+    // 8 below); other configurations run one launch per member.
+    const int pitch = stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK);
+    const int total = d.group->sbase[d.group->nm];
+    if (d.w.pair || mrows * pitch + 32 > (total >= device_cus() ? kGemvStageBytes : kGemvSmallStageBytes))
+      return hipErrorNotSupported;
+    GemvParams p = *d.group;
+    p.x = d.x;
+    p.M = d.M;
+    p.m_base = d.m_base;
+    p.y_dtype = d.y_dtype;
+    p.x_pitch = pitch;
+    p.query = d.query;
+    if (total >= device_cus()) return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvWaves>(p, st);
+    return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvSmallWaves>(p, st);
+  }
   if (d.w.pair) {
     // SwiGLU epilogue: one gate / up strip pair per workgroup, never split
     // (the pair's two sums meet in the workgroup's parking LDS)
@@ -1197,7 +1236,8 @@ using Q6kRowsPol = Q6kRowsPolicy<ACT, RP, XL, XS>;
 
 template <int FMT, int ACT>
 static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype,
-                                float *ws, size_t ws_bytes, int *cnt, int *err, size_t *query, hipStream_t st) {
+                                float *ws, size_t ws_bytes, int *cnt, int *err, size_t *query, hipStream_t st,
+                                const GemvParams *group = nullptr) {
   typedef FmtTraits<FMT> T;
   constexpr int XV = (ACT == DIALQ_F32) ? 8 : 4;  // VGPRs per 8-element activation operand
   constexpr bool KQ = FMT == DIALQ_FORMAT_Q4_K || FMT == DIALQ_FORMAT_Q6_K;
@@ -1205,7 +1245,7 @@ static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, v
   const int rows_per_pass = (KQ && M <= 8) ? 8 : 16;
   for (int64_t mb = 0; mb < M; mb += rows_per_pass) {
     const int64_t rem = M - mb, mrows = rem < 16 ? rem : 16;
-    DynParams p{w, x, y, M, mb, y_dtype, 1, 1, 1, 1, 0, ws, ws_bytes, cnt, err, gemv_wait_limit(), query};
+    DynParams p{w, x, y, M, mb, y_dtype, 1, 1, 1, 1, 0, ws, ws_bytes, cnt, err, gemv_wait_limit(), query, group};
     hipError_t e;
     if constexpr (FMT == DIALQ_FORMAT_Q4_K) {
       if (rem <= 4)
@@ -1233,15 +1273,15 @@ static hipError_t gemv_dispatch(const WeightView &w, const void *x, int64_t M, v
 template <int FMT>
 static hipError_t gemv_act(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
                            int y_dtype, float *ws, size_t ws_bytes, int *cnt, int *err, size_t *query,
-                           hipStream_t st) {
+                           hipStream_t st, const GemvParams *group) {
   switch (x_dtype) {
-    case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
+    case DIALQ_BF16: return gemv_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st, group);
     // f16 activations feed f16 MFMAs as they are (f16 weight operands);
     // MXFP4's scaled codes need bf16's exponent range (hi / lo parts)
     case DIALQ_F16:
       return gemv_dispatch<FMT, FMT == DIALQ_FORMAT_MXFP4 ? DIALQ_F16 : kActF16N>(w, x, M, y, y_dtype, ws, ws_bytes,
-                                                                                 cnt, err, query, st);
-    case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
+                                                                                 cnt, err, query, st, group);
+    case DIALQ_F32: return gemv_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st, group);
   }
   return hipErrorInvalidValue;
 }
@@ -1257,17 +1297,18 @@ void set_gemv_wait_limit(int64_t polls) {
 }
 
 static hipError_t gemv_fmt(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype,
-                           float *ws, size_t ws_bytes, int *cnt, int *err, size_t *query, hipStream_t st) {
+                           float *ws, size_t ws_bytes, int *cnt, int *err, size_t *query, hipStream_t st,
+                           const GemvParams *group = nullptr) {
   switch (w.fmt) {
-    case DIALQ_FORMAT_W8A16: return gemv_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
-    case DIALQ_FORMAT_FP8_ROW: return gemv_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
-    case DIALQ_FORMAT_Q8_0: return gemv_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
+    case DIALQ_FORMAT_W8A16: return gemv_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st, group);
+    case DIALQ_FORMAT_FP8_ROW: return gemv_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st, group);
+    case DIALQ_FORMAT_Q8_0: return gemv_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st, group);
     case DIALQ_FORMAT_FP8_BLOCK:
-      return gemv_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
-    case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
-    case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
-    case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
-    case DIALQ_FORMAT_Q6_K: return gemv_act<DIALQ_FORMAT_Q6_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st);
+      return gemv_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st, group);
+    case DIALQ_FORMAT_NVFP4: return gemv_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st, group);
+    case DIALQ_FORMAT_MXFP4: return gemv_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st, group);
+    case DIALQ_FORMAT_Q4_K: return gemv_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st, group);
+    case DIALQ_FORMAT_Q6_K: return gemv_act<DIALQ_FORMAT_Q6_K>(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, query, st, group);
   }
   return hipErrorInvalidValue;
 }
@@ -1275,6 +1316,26 @@ static hipError_t gemv_fmt(const WeightView &w, const void *x, int x_dtype, int6
 hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype, float *ws,
                        size_t ws_bytes, int *cnt, int *err, hipStream_t st) {
   return gemv_fmt(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, nullptr, st);
+}
+
+hipError_t launch_gemv_group(const WeightView *ws, void *const *ys, int n, const void *x, int x_dtype, int64_t M,
+                             int y_dtype, hipStream_t st) {
+  if (n < 2 || n > kGemvMaxGroup) return hipErrorNotSupported;
+  GemvParams g{};
+  g.w = ws[0];
+  g.y = ys[0];
+  g.nm = n;
+  g.sbase[0] = 0;
+  for (int j = 0; j < n; ++j) {
+    if (ws[j].fmt != ws[0].fmt || ws[j].K != ws[0].K || ws[j].k_chunks != ws[0].k_chunks || ws[j].pair)
+      return hipErrorNotSupported;
+    g.wm[j] = ws[j];
+    g.ym[j] = ys[j];
+    g.sbase[j + 1] = g.sbase[j] + (int)ws[j].n_strips;
+  }
+  for (int j = n; j < kGemvMaxGroup; ++j) g.sbase[j + 1] = g.sbase[n];
+  // a grouped launch never uses the workspace or the counters
+  return gemv_fmt(ws[0], x, x_dtype, M, ys[0], y_dtype, nullptr, 0, nullptr, nullptr, nullptr, st, &g);
 }
 
 // The launch plan of launch_gemv, run without launching: the largest

@@ -35,7 +35,17 @@ struct WeightView {
   // writes y[m, j] = silu(gate[m, j]) * up[m, j], j < I (the MLP's
   // mlp_mid_from_gate_up, qwen3_vl/text.rs:816-820).
   int64_t pair = 0;
+  // Output row stride in elements; 0 = the natural width (N, or I for the
+  // SwiGLU product).  A member of a grouped forward writes its columns of
+  // the concatenated [M, sum N] output: y points at its first column and
+  // ldy is the sum.
+  int64_t ldy = 0;
 };
+
+// Row stride of the output a product kernel writes.
+__host__ __device__ inline int64_t out_ld(const WeightView &w) {
+  return w.ldy ? w.ldy : (w.pair ? w.pair * 16 : w.N);
+}
 
 hipError_t launch_quantize(int fmt, const void *dense, int dtype, int64_t N, int64_t K, void *raw_w,
                            void *raw_s, hipStream_t st);
@@ -61,6 +71,13 @@ hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int6
 size_t gemv_workspace_bytes(const WeightView &w, int x_dtype, int64_t M);
 hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
                        int y_dtype, float *ws, size_t ws_bytes, int *cnt, int *err, hipStream_t st);
+// One decode launch over the strips of n (2..4) weights that share x (the
+// same format and K): member j writes [M, N_j] through ys[j] with its view's
+// output stride.  Returns hipErrorNotSupported, launching nothing, where the
+// grouped kernel does not apply (activations too large to stage, SwiGLU,
+// mixed formats); the caller then launches per member.
+hipError_t launch_gemv_group(const WeightView *ws, void *const *ys, int n, const void *x, int x_dtype, int64_t M,
+                             int y_dtype, hipStream_t st);
 // Polls without progress before a bounded wait of the work queue gives up
 // (process-wide; < 0 restores the default).
 void set_gemv_wait_limit(int64_t polls);

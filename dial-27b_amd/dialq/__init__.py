@@ -78,6 +78,7 @@ def _load():
                                           I32, P, C.c_int, CH, SZ]),
         "dialq_debug_set_wait_limit": (None, [I64]),
         "dialq_linear_forward_noalloc": (C.c_int, [P, P, I32, I64, P, I32, I32, P, CH, SZ]),
+        "dialq_linear_forward_group": (C.c_int, [P, I32, P, I32, I64, P, I32, I32, P, C.c_int, CH, SZ]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -307,6 +308,23 @@ class Linear:
                                      err, 512)
         _check(rc, err)
         return w, s
+
+
+def forward_group(linears, x, y, rows=None, *, path=PATH_AUTO, stream=None, x_dtype=None, y_dtype=None):
+    """dialq_linear_forward_group: y = cat([x W_j^T for each handle], -1),
+    y of shape [rows, sum of out_dim]."""
+    dev = _is_torch(x)
+    k = linears[0].in_dim
+    if rows is None:
+        rows = (x.numel() if dev else np.asarray(x).size) // k
+    xd = dtype_code(x) if x_dtype is None else x_dtype
+    yd = dtype_code(y) if y_dtype is None else y_dtype
+    hs = (C.c_void_p * len(linears))(*[l.h.value for l in linears])
+    err = _err()
+    rc = lib.dialq_linear_forward_group(hs, len(linears), _ptr(x), xd, rows, _ptr(y), yd, path,
+                                        _stream_ptr(stream), int(dev), err, 512)
+    _check(rc, err)
+    return y
 
 
 def set_wait_limit(polls):

@@ -165,6 +165,24 @@ int dialq_linear_forward_ex(void *linear, const void *x, int32_t x_dtype,
                             int32_t path, void *stream, int device_io,
                             char *error, size_t error_size);
 
+/* Grouped forward over n handles that share their input:
+ *   y = cat([x W_0^T, x W_1^T, ..., x W_{n-1}^T], -1),  y: [rows, sum N_j]
+ * Replaces QkvProjection::Split::forward and MlpGateUpProjection::Split::
+ * forward (qwen3_vl/text.rs:1093-1101, :451-455: q / k / v or gate / up
+ * TextLinear::forward on one x, then Tensor::cat along the last dim), the
+ * projections the GGUF worker builds (text.rs:1387-1425).  All handles must
+ * have the same in_dim and device.  The decode path runs the strips of up
+ * to four consecutive same-format members in one launch (x staged once per
+ * workgroup, one launch's fill and drain instead of one per member); other
+ * cases run one launch per member, each writing its columns of y, with the
+ * same kernels and results as dialq_linear_forward_ex per member.  Other
+ * arguments as dialq_linear_forward_ex (x at any address; y aligned to its
+ * element size; per-handle scratch grows outside stream capture only). */
+int dialq_linear_forward_group(void *const *linears, int32_t n, const void *x,
+                               int32_t x_dtype, int64_t rows, void *y,
+                               int32_t y_dtype, int32_t path, void *stream,
+                               int device_io, char *error, size_t error_size);
+
 /* Allocation-free forward; no counterpart in the reference.  For callers
  * that cannot allocate device memory during the call: code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc.  The same
