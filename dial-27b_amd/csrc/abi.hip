@@ -491,8 +491,11 @@ constexpr int kGroupMax = 4;
 void forward_group_impl(Linear *const *Ls, int32_t n, const void *x, int32_t x_dtype, int64_t rows, void *y,
                         int32_t y_dtype, int32_t path, void *stream, int device_io) {
   if (!Ls || n < 1) fail("a grouped forward needs at least one handle, got %d", (int)n);
-  for (int j = 0; j < n; ++j)
+  for (int j = 0; j < n; ++j) {
     if (!Ls[j]) fail("linear handle %d of the group is NULL", j);
+    for (int i = 0; i < j; ++i)  // members own their scratch; one handle twice would share it
+      if (Ls[i] == Ls[j]) fail("grouped forward: handle %d is the same handle as %d", j, i);
+  }
   const int64_t K = Ls[0]->desc.in_dim;
   int64_t ntot = 0;
   for (int j = 0; j < n; ++j) {
@@ -839,6 +842,8 @@ int dialq_linear_forward_group(void *const *linears, int32_t n, const void *x, i
 }
 
 void dialq_debug_set_wait_limit(int64_t polls) { set_gemv_wait_limit(polls); }
+
+int64_t dialq_debug_grouped_launches(void) { return gemv_grouped_launches(); }
 
 int dialq_linear_forward_noalloc(void *linear, const void *x, int32_t x_dtype, int64_t rows, void *y,
                                  int32_t y_dtype, int32_t path, void *stream, char *error, size_t error_size) {

@@ -1318,6 +1318,12 @@ hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t 
   return gemv_fmt(w, x, x_dtype, M, y, y_dtype, ws, ws_bytes, cnt, err, nullptr, st);
 }
 
+namespace {
+std::atomic<int64_t> g_grouped_launches{0};
+}
+
+int64_t gemv_grouped_launches() { return g_grouped_launches.load(std::memory_order_relaxed); }
+
 hipError_t launch_gemv_group(const WeightView *ws, void *const *ys, int n, const void *x, int x_dtype, int64_t M,
                              int y_dtype, hipStream_t st) {
   if (n < 2 || n > kGemvMaxGroup) return hipErrorNotSupported;
@@ -1335,7 +1341,9 @@ hipError_t launch_gemv_group(const WeightView *ws, void *const *ys, int n, const
   }
   for (int j = n; j < kGemvMaxGroup; ++j) g.sbase[j + 1] = g.sbase[n];
   // a grouped launch never uses the workspace or the counters
-  return gemv_fmt(ws[0], x, x_dtype, M, ys[0], y_dtype, nullptr, 0, nullptr, nullptr, nullptr, st, &g);
+  const hipError_t e = gemv_fmt(ws[0], x, x_dtype, M, ys[0], y_dtype, nullptr, 0, nullptr, nullptr, nullptr, st, &g);
+  if (e == hipSuccess) g_grouped_launches.fetch_add(1, std::memory_order_relaxed);
+  return e;
 }
 
 // The launch plan of launch_gemv, run without launching: the largest

@@ -78,6 +78,9 @@ hipError_t launch_gemv(const WeightView &w, const void *x, int x_dtype, int64_t 
 // mixed formats); the caller then launches per member.
 hipError_t launch_gemv_group(const WeightView *ws, void *const *ys, int n, const void *x, int x_dtype, int64_t M,
                              int y_dtype, hipStream_t st);
+// Grouped decode launches made by this process (a test hook: a group that
+// fell back to one launch per member leaves it unchanged).
+int64_t gemv_grouped_launches();
 // Polls without progress before a bounded wait of the work queue gives up
 // (process-wide; < 0 restores the default).
 void set_gemv_wait_limit(int64_t polls);

@@ -77,6 +77,7 @@ def _load():
         "dialq_logits_select": (C.c_int, [P, I32, I64, P, I64, C.c_float, C.c_float, I32, I64, P, P, P, P, SZ,
                                           I32, P, C.c_int, CH, SZ]),
         "dialq_debug_set_wait_limit": (None, [I64]),
+        "dialq_debug_grouped_launches": (I64, []),
         "dialq_linear_forward_noalloc": (C.c_int, [P, P, I32, I64, P, I32, I32, P, CH, SZ]),
         "dialq_linear_forward_group": (C.c_int, [P, I32, P, I32, I64, P, I32, I32, P, C.c_int, CH, SZ]),
     }
@@ -325,6 +326,11 @@ def forward_group(linears, x, y, rows=None, *, path=PATH_AUTO, stream=None, x_dt
                                         _stream_ptr(stream), int(dev), err, 512)
     _check(rc, err)
     return y
+
+
+def grouped_launches():
+    """Test hook (dialq_debug_grouped_launches): grouped decode launches so far."""
+    return int(lib.dialq_debug_grouped_launches())
 
 
 def set_wait_limit(polls):

@@ -288,6 +288,12 @@ int dialq_local_q8_forward(void *linear, const void *x, int32_t x_dtype,
  * failure path only. */
 void dialq_debug_set_wait_limit(int64_t polls);
 
+/* Test hook; no counterpart in the reference.  The number of grouped decode
+ * launches (dialq_linear_forward_group members run as one kernel) this
+ * process has made, so that tests can tell a grouped launch from the
+ * per-member fallback, whose outputs are the same to rounding. */
+int64_t dialq_debug_grouped_launches(void);
+
 #ifdef __cplusplus
 }
 #endif
