@@ -338,7 +338,11 @@ ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int6
   const int fmt = L->desc.format;
   ForwardPlan pl;
   if (path == DIALQ_PATH_AUTO) {
-    if (rows <= 64) path = DIALQ_PATH_GEMV;
+    // the decode kernel re-streams the weight for every 16 rows; past one
+    // pass the GEMM (32-row tiles split along K where its tiles are few) is
+    // faster: 17408x5120 W8A16 at M = 24 36.5 against 71 us, at M = 64 45.5
+    // against 163
+    if (rows <= 16) path = DIALQ_PATH_GEMV;
     else if ((fmt == DIALQ_FORMAT_FP8_BLOCK || fmt == DIALQ_FORMAT_MXFP4) &&
              !(L->desc.flags & DIALQ_FLAG_WEIGHT_ONLY_PREFILL))
       path = DIALQ_PATH_GEMM_NATIVE;
@@ -359,7 +363,9 @@ ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int6
     pl.codes = (codes + 255) / 256 * 256;
     pl.xscale = fmt == DIALQ_FORMAT_FP8_BLOCK ? (size_t)rows * sizeof(float) : (size_t)(rows * pl.k_pad / 32);
     native_workspace(rows, w, pl.part, pl.ncnt);
-  } else if (path != DIALQ_PATH_GEMM) {
+  } else if (path == DIALQ_PATH_GEMM) {
+    gemm_workspace(rows, w, pl.part, pl.ncnt);  // split-K partials of few-tile launches
+  } else {
     fail("unknown path %d", path);
   }
   return pl;
@@ -371,7 +377,8 @@ void launch_forward(const Linear *L, const WeightView &w, const ForwardPlan &pl,
     hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, b.gemv_ws, b.gemv_ws_bytes, b.gemv_cnt, L->gave_up.d, st),
               "GEMV launch");
   } else if (pl.path == DIALQ_PATH_GEMM) {
-    hip_check(launch_gemm(w, x, x_dtype, rows, y, y_dtype, st), "GEMM launch");
+    hip_check(launch_gemm(w, x, x_dtype, rows, y, y_dtype, b.part, b.part_bytes, b.ncnt, b.ncnt_count, st),
+              "GEMM launch");
   } else {
     if (L->desc.format == DIALQ_FORMAT_FP8_BLOCK)
       hip_check(launch_act_fp8(x, x_dtype, rows, w.K, pl.k_pad, b.codes, (float *)b.xscale, st),
@@ -398,11 +405,14 @@ void run_forward(Linear *L, const WeightView &w, const void *x, int x_dtype, int
     b.gemv_ws = (float *)L->gemv_ws.p;
     b.gemv_ws_bytes = L->gemv_ws.n;
     b.gemv_cnt = (int *)L->gemv_cnt.p;
-  } else if (pl.path == DIALQ_PATH_GEMM_NATIVE) {
-    ensure_scratch(L, pl.codes + pl.xscale, st);
+  } else {
+    if (pl.path == DIALQ_PATH_GEMM_NATIVE) {
+      ensure_scratch(L, pl.codes + pl.xscale, st);
+      b.codes = (uint8_t *)L->act_scratch.p;
+      b.xscale = b.codes + pl.codes;
+    }
+    // split-K partials and tile counters (native prefill, or a GEMM of few tiles)
     ensure_native_scratch(L, pl.part, pl.ncnt, st);
-    b.codes = (uint8_t *)L->act_scratch.p;
-    b.xscale = b.codes + pl.codes;
     b.part = (float *)L->native_part.p;
     b.part_bytes = L->native_part.n;
     b.ncnt = (int *)L->native_cnt.p;
@@ -650,10 +660,12 @@ void forward_noalloc_impl(Linear *L, const void *x, int32_t x_dtype, int64_t row
     b.gemv_ws = pl.gemv_ws ? (float *)(base + off) : nullptr;
     b.gemv_ws_bytes = pl.gemv_ws;
     off += up(pl.gemv_ws);
-  } else if (pl.path == DIALQ_PATH_GEMM_NATIVE) {
-    b.codes = base + off;
-    b.xscale = base + off + pl.codes;
-    off += up(pl.codes + pl.xscale);
+  } else {
+    if (pl.path == DIALQ_PATH_GEMM_NATIVE) {
+      b.codes = base + off;
+      b.xscale = base + off + pl.codes;
+      off += up(pl.codes + pl.xscale);
+    }
     b.part = pl.part ? (float *)(base + off) : nullptr;
     b.part_bytes = pl.part;
     off += up(pl.part);

@@ -28,6 +28,12 @@ struct GemmParams {
   void *y;
   int64_t M;
   int y_dtype;
+  // Split-K (k_gemm32, P > 1): each tile's chunks split into P pieces, one
+  // workgroup each; partial tiles in `part` ([tiles][P][rows x 256]), one
+  // arrival counter per tile in `cnt` (zero between launches).
+  int P = 1;
+  float *part = nullptr;
+  int *cnt = nullptr;
 };
 
 template <int FMT, int ACT>
@@ -164,7 +170,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   typedef GemmShape<FMT, ACT> S;
   typedef FmtTraits<FMT> T;
   constexpr int KS = S::KS, BY = ActTraits<ACT>::BYTES;
-  extern __shared__ uint16_t lds[];  // [2][PARTS][ROWS][STRIDE] bf16
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // [2][PARTS][ROWS][STRIDE] bf16
   const WeightView &w = p.w;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -405,18 +411,34 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   constexpr int PARTS = ActTraits<ACT>::PARTS, BY = ActTraits<ACT>::BYTES;
   constexpr int ROWS = 32 * MT, STRIDE = SK + 8, BUF = PARTS * ROWS * STRIDE;
   constexpr int NQ = 2, PIECES = ROWS * SK / 8 / 256;
-  extern __shared__ uint16_t lds[];  // [2][PARTS][ROWS][STRIDE] bf16
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // [2][PARTS][ROWS][STRIDE] bf16
   const WeightView &w = p.w;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
-  int tm, tn;
+  int tm, tn, piece = 0;
   const int nt = SWI ? (int)((w.pair + 7) / 8) : (int)((w.n_strips + 15) / 16);
-  tile_of(blockIdx.x, gridDim.x, nt, (int)((p.M + ROWS - 1) / ROWS), tm, tn);
+  const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
+  const int P = p.P;
+  if (P == 1) {
+    tile_of(blockIdx.x, gridDim.x, nt, mtiles, tm, tn);
+  } else {
+    // (column tile, piece, row block) over XCD-contiguous ranks, as the
+    // native kernel's split tiles: row blocks streaming the same weight
+    // chunks run on one XCD at once and share them in its L2
+    const int u = xcd_rank(blockIdx.x, gridDim.x);
+    tm = u % mtiles;
+    piece = (u / mtiles) % P;
+    tn = u / (mtiles * P);
+  }
   const int m0 = tm * ROWS;
   int s0 = tn * 16 + wave * 4, slim = (int)w.n_strips, j0 = 0;
   if constexpr (SWI) swiglu_strips<16>(w, tn, wave, s0, slim, j0);
-  const int kc = (int)w.k_chunks, K = (int)w.K;
+  const int K = (int)w.K;
+  // this workgroup's chunks [c0, c1) (all of them unless the tile is split)
+  const int c0 = (int)((int64_t)piece * w.k_chunks / P), c1 = (int)((int64_t)(piece + 1) * w.k_chunks / P);
+  const int kc = c1 - c0;
+  const int kend = (c1 * CHUNK < K) ? c1 * CHUNK : K;  // activations past the piece read as zeros
   const int nstage = (kc + KS - 1) / KS;
   const int64_t total = w.n_strips * w.k_chunks;
   const rsrc_t rt = make_rsrc(w.tiles, (uint32_t)(total * 1024));
@@ -427,16 +449,16 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   auto fetch_a = [&](int st) {
 #pragma unroll
     for (int q = 0; q < PIECES; ++q) {
-      const int piece = tid + q * 256, row = piece / (SK / 8), kk = (piece % (SK / 8)) * 8;
-      const int k = st * SK + kk;
-      apre[q] = xraw_load<ACT>(rx, (st < nstage && k < K) ? (uint32_t)((row * K + k) * BY) : kOOB);
+      const int pc = tid + q * 256, row = pc / (SK / 8), kk = (pc % (SK / 8)) * 8;
+      const int k = c0 * CHUNK + st * SK + kk;
+      apre[q] = xraw_load<ACT>(rx, (st < nstage && k < kend) ? (uint32_t)((row * K + k) * BY) : kOOB);
     }
   };
   auto store_a = [&](int buf) {
     uint16_t *base = lds + buf * BUF;
 #pragma unroll
     for (int q = 0; q < PIECES; ++q) {
-      const int piece = tid + q * 256, row = piece / (SK / 8), kk = (piece % (SK / 8)) * 8;
+      const int pc = tid + q * 256, row = pc / (SK / 8), kk = (pc % (SK / 8)) * 8;
       const XOp<ACT> o = xraw_to_op<ACT>(apre[q]);
       *(u32x4 *)(base + row * STRIDE + kk) = o.hi;
       if constexpr (PARTS == 2) *(u32x4 *)(base + (ROWS + row) * STRIDE + kk) = o.lo;
@@ -445,9 +467,9 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   // weight bytes of (stage st, 16-k step j, column tile q) for this lane
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   auto bload = [&](int st, int j, int q) -> u32x2 {
-    const int c = st * KS + j / 4, strip = s0 + 2 * q + sub;
-    const bool valid = st < nstage && c < kc && strip < slim;
-    const uint32_t off = valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * 1024u +
+    const int c = c0 + st * KS + j / 4, strip = s0 + 2 * q + sub;
+    const bool valid = st < nstage && c < c1 && strip < slim;
+    const uint32_t off = valid ? ((uint32_t)strip * (uint32_t)w.k_chunks + (uint32_t)c) * 1024u +
                                      (uint32_t)(((j % 4) * 16 + r) * 16 + 8 * h)
                                : kOOB;
     return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rt, (int)off, 0, 0));
@@ -517,6 +539,56 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   }
   if (st < nstage) stage(wb[0], st);
 
+  if (P > 1) {
+    // Split tile: each piece publishes its partial (agent-scope relaxed
+    // stores, complete before the count); the last to arrive adds the P
+    // partials in piece order -- the same order whichever piece is last --
+    // then runs the epilogue and re-arms the tile's counter.
+    // the arrival flag sits past the two staging buffers (the SwiGLU
+    // exchange uses their first 8 KB); a static __shared__ variable would
+    // move the dynamic staging area off its 16-byte alignment
+    int &last_piece = *(int *)(lds + 2 * BUF);
+    constexpr int NV = MT * NQ * 16;
+    const int t = tn * mtiles + tm;
+    float *mine = p.part + ((size_t)t * P + piece) * (NV * 256);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          __hip_atomic_store(&mine[((mt * NQ + q) * 16 + v) * 256 + tid], acc[mt][q][v], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) last_piece = __hip_atomic_fetch_add(&p.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1;
+    __syncthreads();
+    if (!last_piece) return;
+    // all P partials (this piece's too, read back from L2) in piece order,
+    // one piece's 64 values in flight per round trip
+    const rsrc_t rp = make_rsrc(p.part + (size_t)t * P * (NV * 256), (uint32_t)((size_t)P * NV * 256 * 4));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[mt][q][v] = 0.0f;
+    for (int u = 0; u < P; ++u) {
+      float pv[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        pv[i] = __uint_as_float(
+            (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, (int)(((u * NV + i) * 256 + tid) * 4), 0, kSC1));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[mt][q][v] += pv[(mt * NQ + q) * 16 + v];
+    }
+    if (tid == 0) __hip_atomic_store(&p.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
   if constexpr (SWI) {
     // y[m, j] = silu(gate) * up, one 32x32 tile per exchange
     const int64_t I = w.pair * 16;
@@ -572,22 +644,83 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   });
 }
 
+// Launch plan of the 32x32 kernel.  Two shapes: 64-row tiles with one 64-k
+// chunk per stage (GEMM32_MT, GEMM32_KS) for prefill, and for 17..96 rows
+// 32-row tiles with two chunks per stage: those launches have few tiles, so
+// each workgroup's weight stream is latency bound, and half the accumulators
+// with twice the weight bytes per stage keep more of it in flight (measured
+// on the 27B shapes at 24..96 rows: 1.2-1.6x faster than 64-row tiles).
+// A launch with few tiles also leaves CUs idle; it splits every tile along K
+// into P pieces (split-K), at least kGemm32MinChunks chunks each.  A piece
+// writes a rows x 256 f32 partial tile and the last one reads them all
+// back, traffic worth spending only while the tiles are far fewer than the
+// CUs: small-row launches split while tiles fill at most half the workgroup
+// slots (<= 8 pieces), prefill launches only below CUs / 2 tiles
+// (<= 4 pieces; the 17408-row gate at 128 rows, 136 tiles, is faster whole).
+// Either bound keeps the partials under 32 MiB.
+constexpr int64_t kGemm32SmallRows = 96;
+constexpr int kGemm32MinChunks = 20;
+struct Gemm32Plan {
+  int mt, ks, P;
+  int64_t tiles;
+  size_t part_bytes() const { return P > 1 ? (size_t)(tiles * P) * 32 * mt * 256 * sizeof(float) : 0; }
+};
+static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w) {
+  Gemm32Plan g;
+  const bool small = M <= kGemm32SmallRows;
+  g.mt = small ? 1 : GEMM32_MT;
+  g.ks = small ? 2 : GEMM32_KS;
+  const int64_t rows = 32 * g.mt, nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
+  g.tiles = nt * ((M + rows - 1) / rows);
+  g.P = 1;
+  const int64_t cus = device_cus(), slots = (int64_t)GEMM32_OCC * cus;
+  if (small ? g.tiles * 2 <= slots : g.tiles * 2 < cus) {
+    int64_t P = slots / g.tiles, cap = w.k_chunks / kGemm32MinChunks;
+    if (cap > (small ? 8 : 4)) cap = small ? 8 : 4;
+    if (P > cap) P = cap;
+    g.P = (int)(P < 1 ? 1 : P);
+  }
+  return g;
+}
+
+static bool gemm32_applies(const WeightView &w) {
+  return (w.fmt == DIALQ_FORMAT_W8A16 || w.fmt == DIALQ_FORMAT_FP8_ROW) &&
+         w.n_strips * w.k_chunks * 1024 <= 0xffffffffLL;
+}
+
+void gemm_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count) {
+  part_bytes = 0;
+  cnt_count = 0;
+  if (!gemm32_applies(w) || M <= 0) return;
+  const Gemm32Plan g = gemm32_plan(M, w);
+  if (g.P > 1) {
+    part_bytes = g.part_bytes();
+    cnt_count = (size_t)g.tiles;
+  }
+}
+
+template <int FMT, int ACT, int MT, int KS>
+static hipError_t gemm32_launch(const GemmParams &p, int64_t grid, hipStream_t st) {
+  constexpr int BUF = ActTraits<ACT>::PARTS * 32 * MT * (KS * 64 + 8);
+  static_assert(2 * BUF * 2 >= 8192, "the SwiGLU exchange reuses the staging LDS");
+  const size_t lds_bytes = 2 * BUF * 2 + 16;  // two staging buffers and the split-K arrival flag
+  if (p.w.pair) k_gemm32<FMT, ACT, MT, KS, GEMM32_OCC, true><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
+  else k_gemm32<FMT, ACT, MT, KS, GEMM32_OCC, false><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
+  return hipGetLastError();
+}
+
 template <int FMT, int ACT>
-static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype,
-                                hipStream_t st) {
+static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype, float *part,
+                                size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st) {
   typedef GemmShape<FMT, ACT> S;
   if ((int64_t)S::ROWS * w.K * ActTraits<ACT>::BYTES > 0xffffffffLL) return hipErrorInvalidValue;
   if constexpr (FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW) {
-    if (w.n_strips * w.k_chunks * 1024 <= 0xffffffffLL) {
-      constexpr int MT = GEMM32_MT, KS = GEMM32_KS, ROWS = 32 * MT;
-      constexpr int BUF = ActTraits<ACT>::PARTS * ROWS * (KS * 64 + 8);
-      static_assert(2 * BUF * 2 >= 8192, "the SwiGLU exchange reuses the staging LDS");
-      const int64_t nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
-      dim3 grid((unsigned)(nt * ((M + ROWS - 1) / ROWS)));
-      GemmParams p{w, x, y, M, y_dtype};
-      if (w.pair) k_gemm32<FMT, ACT, MT, KS, GEMM32_OCC, true><<<grid, 256, 2 * BUF * 2, st>>>(p);
-      else k_gemm32<FMT, ACT, MT, KS, GEMM32_OCC, false><<<grid, 256, 2 * BUF * 2, st>>>(p);
-      return hipGetLastError();
+    if (gemm32_applies(w)) {
+      const Gemm32Plan g = gemm32_plan(M, w);
+      if (g.P > 1 && ((size_t)g.tiles > cnt_count || g.part_bytes() > part_bytes)) return hipErrorInvalidValue;
+      const GemmParams p{w, x, y, M, y_dtype, g.P, part, cnt};
+      if (g.mt == 1) return gemm32_launch<FMT, ACT, 1, 2>(p, g.tiles * g.P, st);
+      return gemm32_launch<FMT, ACT, GEMM32_MT, GEMM32_KS>(p, g.tiles * g.P, st);
     }
   }
   static_assert(S::LDS_BYTES >= 8192, "the SwiGLU exchange reuses the staging LDS");
@@ -600,32 +733,35 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
 }
 
 template <int FMT>
-static hipError_t gemm_act(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                           int y_dtype, hipStream_t st) {
+static hipError_t gemm_act(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype,
+                           float *part, size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st) {
   switch (x_dtype) {
-    case DIALQ_BF16: return gemm_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, st);
+    case DIALQ_BF16: return gemm_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
     // f16 activations go to f16 MFMAs as they are, against f16 weight
     // operands; MXFP4's scaled codes need bf16's exponent range (hi / lo parts)
     case DIALQ_F16:
-      return gemm_dispatch<FMT, FMT == DIALQ_FORMAT_MXFP4 ? DIALQ_F16 : kActF16N>(w, x, M, y, y_dtype, st);
-    case DIALQ_F32: return gemm_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, st);
+      return gemm_dispatch<FMT, FMT == DIALQ_FORMAT_MXFP4 ? DIALQ_F16 : kActF16N>(w, x, M, y, y_dtype, part,
+                                                                                 part_bytes, cnt, cnt_count, st);
+    case DIALQ_F32: return gemm_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
   }
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y,
-                       int y_dtype, hipStream_t st) {
+hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype, float *part,
+                       size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st) {
+#define DIALQ_GEMM_FMT(F) \
+  case F: return gemm_act<F>(w, x, x_dtype, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
   switch (w.fmt) {
-    case DIALQ_FORMAT_W8A16: return gemm_act<DIALQ_FORMAT_W8A16>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_FP8_ROW: return gemm_act<DIALQ_FORMAT_FP8_ROW>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_Q8_0: return gemm_act<DIALQ_FORMAT_Q8_0>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_FP8_BLOCK:
-      return gemm_act<DIALQ_FORMAT_FP8_BLOCK>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_NVFP4: return gemm_act<DIALQ_FORMAT_NVFP4>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_MXFP4: return gemm_act<DIALQ_FORMAT_MXFP4>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_Q4_K: return gemm_act<DIALQ_FORMAT_Q4_K>(w, x, x_dtype, M, y, y_dtype, st);
-    case DIALQ_FORMAT_Q6_K: return gemm_act<DIALQ_FORMAT_Q6_K>(w, x, x_dtype, M, y, y_dtype, st);
+    DIALQ_GEMM_FMT(DIALQ_FORMAT_W8A16)
+    DIALQ_GEMM_FMT(DIALQ_FORMAT_FP8_ROW)
+    DIALQ_GEMM_FMT(DIALQ_FORMAT_Q8_0)
+    DIALQ_GEMM_FMT(DIALQ_FORMAT_FP8_BLOCK)
+    DIALQ_GEMM_FMT(DIALQ_FORMAT_NVFP4)
+    DIALQ_GEMM_FMT(DIALQ_FORMAT_MXFP4)
+    DIALQ_GEMM_FMT(DIALQ_FORMAT_Q4_K)
+    DIALQ_GEMM_FMT(DIALQ_FORMAT_Q6_K)
   }
+#undef DIALQ_GEMM_FMT
   return hipErrorInvalidValue;
 }
 

@@ -77,7 +77,11 @@ typedef struct dialq_linear_desc {
 
 /* Kernel selection for dialq_linear_forward_ex. */
 enum dialq_path {
-  DIALQ_PATH_AUTO = 0,        /* GEMV for rows <= 64, GEMM above */
+  DIALQ_PATH_AUTO = 0,        /* GEMV for rows <= 16; above, GEMM_NATIVE for
+                                 FP8_BLOCK / MXFP4 (unless
+                                 DIALQ_FLAG_WEIGHT_ONLY_PREFILL), GEMM for
+                                 the other formats (W8A16 / FP8_ROW split
+                                 along K while their tiles are few) */
   DIALQ_PATH_GEMV = 1,        /* decode kernel, any rows (loops over row groups) */
   DIALQ_PATH_GEMM = 2,        /* weight-only MFMA GEMM (bf16/f16 operands) */
   DIALQ_PATH_GEMM_NATIVE = 3  /* FP8_BLOCK / MXFP4: activations quantized per

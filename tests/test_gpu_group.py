@@ -65,7 +65,7 @@ def test_group_equals_separate(fmts, rows, torch_dev):
     ns = [384, 64, 64][:len(fmts)] if len(fmts) == 3 else [320, 320]
     lins, deqs = _members(fmts, ns, k, seed=11 * rows)
     x = O.round_bf16(np.random.default_rng(rows).normal(0, 1, (rows, k)).astype(np.float32))
-    grouped = rows <= 64 and len(set(fmts)) == 1  # one grouped decode launch
+    grouped = rows <= 16 and len(set(fmts)) == 1  # decode path: one grouped launch
     for x_dtype in (dq.BF16, dq.F16, dq.F32):
         xt = to_torch(x, x_dtype, torch_dev)
         want = _separate(lins, xt, dq.BF16, dq.PATH_AUTO, torch_dev)
@@ -77,8 +77,8 @@ def test_group_equals_separate(fmts, rows, torch_dev):
         assert (dq.grouped_launches() > before) == grouped, (rows, fmts)
         _agree(got, want, not grouped, (x_dtype, rows))
     # and against the weight-only oracle, where the product is weight-only
-    # (MXFP4 above 64 rows takes the native path, which quantizes x too)
-    if not (rows > 64 and dq.MXFP4 in fmts):
+    # (MXFP4 above 16 rows takes the native path, which quantizes x too)
+    if not (rows > 16 and dq.MXFP4 in fmts):
         ref = np.concatenate([reference_product(x, d, dq.BF16) for d in deqs], axis=1)
         assert O.rel_l2(got.float().cpu().numpy(), ref) <= 1e-3
 
