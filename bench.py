@@ -18,7 +18,8 @@ Layer copies rotate so the weight working set (COPIES x 341 MB) exceeds the
 256 MB Infinity Cache and the figure measures HBM.  `value` = algorithmic
 weight bytes streamed / wall time of the timed steps, in GB/s.  Extra keys
 report the same decode for Q4_K / FP8-128 / MXFP4, the prefill GEMM TFLOP/s
-(W8A16 and Q4_K at M = 2048, FP8-128 and MXFP4 native at M = 1024; also over
+(W8A16 and Q4_K at M = 2048 -- Q4_K also with f16 activations, the dtype
+of DIAL's GGUF worker --, FP8-128 and MXFP4 native at M = 1024; also over
 the fused qkv / o / gate_up / down projections DIAL's layers call, with and
 without gate_up's SwiGLU epilogue), the quantized lm_head decode GEMV (vocab
 248320 x 5120) and the device token selection after it, the roofline of the
@@ -45,7 +46,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "dial-27b_amd"))
 
 HBM_PEAK_GBS = 8000.0
-MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "fp4": 10100.0}
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0, "fp4": 10100.0}
 LAYER_27B = [("q", 6144, 5120), ("k", 1024, 5120), ("v", 1024, 5120), ("o", 5120, 6144),
              ("gate", 17408, 5120), ("up", 17408, 5120), ("down", 5120, 17408)]
 # The same weights as the fused projections DIAL's Qwen3-VL layers run
@@ -369,14 +370,14 @@ def profile_prefill_run(dq, torch, dev, iters=5):
         torch.cuda.empty_cache()
 
 
-def time_prefill(dq, torch, lins, m, iters, dev, path, shapes=LAYER_27B, swiglu=()):
+def time_prefill(dq, torch, lins, m, iters, dev, path, shapes=LAYER_27B, swiglu=(), act="bfloat16"):
     """Device time of one prefill pass over the layer's seven linears
     (activation quantization included for the native paths), captured in a
     HIP graph like the decode step and replayed `iters` times between HIP
     events on the replay stream."""
     stream = torch.cuda.current_stream()
-    xs = [torch.randn(m, k, device=dev).to(torch.bfloat16) for _, n, k in shapes]
-    ys = [torch.empty(m, out_cols(name, n, swiglu), device=dev, dtype=torch.bfloat16) for name, n, k in shapes]
+    xs = [torch.randn(m, k, device=dev).to(getattr(torch, act)) for _, n, k in shapes]
+    ys = [torch.empty(m, out_cols(name, n, swiglu), device=dev, dtype=getattr(torch, act)) for name, n, k in shapes]
 
     def body(st):
         for lin, x, y, (name, _, _) in zip(lins, xs, ys, shapes):
@@ -508,12 +509,18 @@ def cpu_baseline(seconds):
             }}
 
 
-PREFILL_GATE = [("w8a16", 2048, "PATH_GEMM", "bf16"), ("q4_k", 2048, "PATH_GEMM", "bf16"),
-                ("fp8_block", 1024, "PATH_GEMM_NATIVE", "fp8"), ("mxfp4", 1024, "PATH_GEMM_NATIVE", "fp4")]
+# (key, rows, path, peak, activation dtype).  q4_k_f16act: Q4_K with the f16
+# activations of DIAL's GGUF worker, whose prefill multiplies f16-dequantized
+# weights (qwen3_vl/worker_gguf.rs:426-455).
+PREFILL_GATE = [("w8a16", 2048, "PATH_GEMM", "bf16", "bfloat16"), ("q4_k", 2048, "PATH_GEMM", "bf16", "bfloat16"),
+                ("q4_k_f16act", 2048, "PATH_GEMM", "f16", "float16"),
+                ("fp8_block", 1024, "PATH_GEMM_NATIVE", "fp8", "bfloat16"),
+                ("mxfp4", 1024, "PATH_GEMM_NATIVE", "fp4", "bfloat16")]
 
 
 def prefill_gate_linears(dq, torch, dev, name):
-    fmt = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}[name]
+    fmt = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "q4_k_f16act": dq.Q4_K, "fp8_block": dq.FP8_BLOCK,
+           "mxfp4": dq.MXFP4}[name]
     _, n, k = DOM
     g = torch.Generator(device=dev).manual_seed(23)
     return dq.Linear.quantize(fmt, torch.randn(n, k, device=dev, generator=g) * 0.02, scale_dtype=dq.BF16)
@@ -523,10 +530,10 @@ def profile_prefill_gate_run(dq, torch, dev, launches=5):
     """Eager launches of the gate-shape prefill per format (the programs of
     the committed MFMA counter summaries)."""
     _, n, k = DOM
-    for name, m, path, _ in PREFILL_GATE:
+    for name, m, path, _, act in PREFILL_GATE:
         lin = prefill_gate_linears(dq, torch, dev, name)
-        x = torch.randn(m, k, device=dev).to(torch.bfloat16)
-        y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        x = torch.randn(m, k, device=dev).to(getattr(torch, act))
+        y = torch.empty(m, n, device=dev, dtype=getattr(torch, act))
         for _ in range(launches):
             lin.forward(x, y, path=getattr(dq, path))
         torch.cuda.synchronize()
@@ -560,10 +567,10 @@ def time_prefill_gate(dq, torch, dev, reps=10):
     _, n, k = DOM
     counters = read_mfma_counters()
     out = {}
-    for name, m, path, peak_key in PREFILL_GATE:
+    for name, m, path, peak_key, act in PREFILL_GATE:
         lin = prefill_gate_linears(dq, torch, dev, name)
-        x = torch.randn(m, k, device=dev).to(torch.bfloat16)
-        y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        x = torch.randn(m, k, device=dev).to(getattr(torch, act))
+        y = torch.empty(m, n, device=dev, dtype=getattr(torch, act))
         stream = torch.cuda.current_stream()
         lin.forward(x, y, path=getattr(dq, path), stream=stream)
         torch.cuda.synchronize()
@@ -736,6 +743,10 @@ def main():
             tf, s2 = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
             extra["prefill_tflops"][name + "_m2048"] = round(tf, 1)
             extra["prefill_pct_mfma_peak"][name + "_m2048"] = round(100.0 * tf / MFMA_PEAK_TFLOPS["bf16"], 1)
+            if fmt == dq.Q4_K:  # the GGUF worker's f16 activations
+                tfh, _ = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, act="float16")
+                extra["prefill_tflops"][name + "_f16act_m2048"] = round(tfh, 1)
+                extra["prefill_pct_mfma_peak"][name + "_f16act_m2048"] = round(100.0 * tfh / MFMA_PEAK_TFLOPS["f16"], 1)
         print(f"# {name}: decode {gbs:.1f} GB/s, prefill {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)
         del ls
         torch.cuda.empty_cache()

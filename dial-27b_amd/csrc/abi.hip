@@ -364,7 +364,7 @@ ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int6
     pl.xscale = fmt == DIALQ_FORMAT_FP8_BLOCK ? (size_t)rows * sizeof(float) : (size_t)(rows * pl.k_pad / 32);
     native_workspace(rows, w, pl.part, pl.ncnt);
   } else if (path == DIALQ_PATH_GEMM) {
-    gemm_workspace(rows, w, pl.part, pl.ncnt);  // split-K partials of few-tile launches
+    gemm_workspace(rows, w, x_dtype, pl.part, pl.ncnt);  // split-K partials of few-tile launches
   } else {
     fail("unknown path %d", path);
   }

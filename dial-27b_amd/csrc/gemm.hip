@@ -103,6 +103,12 @@ constexpr int kXcds = 8, kPanel = 4;
 #ifndef GEMM32_KS
 #define GEMM32_KS 1  // 64-k chunks per pipeline stage in the 32x32 kernel
 #endif
+#ifndef GEMMQ4K_MT
+#define GEMMQ4K_MT 4  // 32-row MFMA tiles per workgroup in the Q4_K prefill kernel
+#endif
+#ifndef GEMMQ4K_OCC
+#define GEMMQ4K_OCC 2  // workgroups per CU the Q4_K prefill kernel is built for
+#endif
 #ifndef GEMM32_OCC
 #define GEMM32_OCC 3  // workgroups per CU the 32x32 kernel is built for
 #endif
@@ -405,6 +411,73 @@ __device__ __forceinline__ f32x16 mfma32_op(u32x4 a, u32x4 b, f32x16 c) {
   else return mfma32(a, b, c);
 }
 
+// Tile of a 32x32-kernel workgroup: (row block tm, column tile tn) and, when
+// the launch splits tiles along K (P > 1), its piece.  Split launches walk
+// (row block, piece, column tile) over XCD-contiguous ranks, as the native
+// kernel's split tiles: the row blocks and pieces of one column tile run on
+// one XCD at once and share its weight and activation lines in that L2.
+__device__ __forceinline__ void split_tile_of(int nt, int mtiles, int P, int &tm, int &tn, int &piece) {
+  piece = 0;
+  if (P == 1) {
+    tile_of(blockIdx.x, gridDim.x, nt, mtiles, tm, tn);
+    return;
+  }
+  const int u = xcd_rank(blockIdx.x, gridDim.x);
+  tm = u % mtiles;
+  piece = (u / mtiles) % P;
+  tn = u / (mtiles * P);
+}
+
+// Split-K fixup of a 32x32-kernel tile t: each of its P pieces publishes
+// its partial (agent-scope relaxed stores, complete before the count); the
+// last to arrive adds the P partials in piece order -- the same order
+// whichever piece is last, so the result is deterministic -- into `acc`,
+// re-arms the tile's counter and returns true; the others return false.
+// `flag`: an LDS int the staging buffers do not overlap.
+template <int MT, int NQ>
+__device__ __forceinline__ bool split_fixup(const GemmParams &p, f32x16 (&acc)[MT][NQ], int t, int piece, int *flag) {
+  constexpr int NV = MT * NQ * 16;
+  const int tid = threadIdx.x, P = p.P;
+  float *mine = p.part + ((size_t)t * P + piece) * (NV * 256);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        __hip_atomic_store(&mine[((mt * NQ + q) * 16 + v) * 256 + tid], acc[mt][q][v], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) *flag = __hip_atomic_fetch_add(&p.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1;
+  __syncthreads();
+  if (!*flag) return false;
+  // all P partials (this piece's too, read back from L2) in piece order,
+  // one piece's values in flight per round trip
+  const rsrc_t rp = make_rsrc(p.part + (size_t)t * P * (NV * 256), (uint32_t)((size_t)P * NV * 256 * 4));
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mt][q][v] = 0.0f;
+  for (int u = 0; u < P; ++u) {
+    float pv[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      pv[i] = __uint_as_float(
+          (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, (int)(((u * NV + i) * 256 + tid) * 4), 0, kSC1));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[mt][q][v] += pv[(mt * NQ + q) * 16 + v];
+  }
+  if (tid == 0) __hip_atomic_store(&p.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
 template <int FMT, int ACT, int MT, int KS, int OCC, bool SWI>
 __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   constexpr int CHUNK = 64, SK = KS * CHUNK, STEPS = SK / 16;
@@ -416,21 +489,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
-  int tm, tn, piece = 0;
+  int tm, tn, piece;
   const int nt = SWI ? (int)((w.pair + 7) / 8) : (int)((w.n_strips + 15) / 16);
   const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
   const int P = p.P;
-  if (P == 1) {
-    tile_of(blockIdx.x, gridDim.x, nt, mtiles, tm, tn);
-  } else {
-    // (column tile, piece, row block) over XCD-contiguous ranks, as the
-    // native kernel's split tiles: row blocks streaming the same weight
-    // chunks run on one XCD at once and share them in its L2
-    const int u = xcd_rank(blockIdx.x, gridDim.x);
-    tm = u % mtiles;
-    piece = (u / mtiles) % P;
-    tn = u / (mtiles * P);
-  }
+  split_tile_of(nt, mtiles, P, tm, tn, piece);
   const int m0 = tm * ROWS;
   int s0 = tn * 16 + wave * 4, slim = (int)w.n_strips, j0 = 0;
   if constexpr (SWI) swiglu_strips<16>(w, tn, wave, s0, slim, j0);
@@ -539,55 +602,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   }
   if (st < nstage) stage(wb[0], st);
 
-  if (P > 1) {
-    // Split tile: each piece publishes its partial (agent-scope relaxed
-    // stores, complete before the count); the last to arrive adds the P
-    // partials in piece order -- the same order whichever piece is last --
-    // then runs the epilogue and re-arms the tile's counter.
-    // the arrival flag sits past the two staging buffers (the SwiGLU
-    // exchange uses their first 8 KB); a static __shared__ variable would
-    // move the dynamic staging area off its 16-byte alignment
-    int &last_piece = *(int *)(lds + 2 * BUF);
-    constexpr int NV = MT * NQ * 16;
-    const int t = tn * mtiles + tm;
-    float *mine = p.part + ((size_t)t * P + piece) * (NV * 256);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int q = 0; q < NQ; ++q)
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          __hip_atomic_store(&mine[((mt * NQ + q) * 16 + v) * 256 + tid], acc[mt][q][v], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) last_piece = __hip_atomic_fetch_add(&p.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1;
-    __syncthreads();
-    if (!last_piece) return;
-    // all P partials (this piece's too, read back from L2) in piece order,
-    // one piece's 64 values in flight per round trip
-    const rsrc_t rp = make_rsrc(p.part + (size_t)t * P * (NV * 256), (uint32_t)((size_t)P * NV * 256 * 4));
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int q = 0; q < NQ; ++q)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[mt][q][v] = 0.0f;
-    for (int u = 0; u < P; ++u) {
-      float pv[NV];
-#pragma unroll
-      for (int i = 0; i < NV; ++i)
-        pv[i] = __uint_as_float(
-            (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, (int)(((u * NV + i) * 256 + tid) * 4), 0, kSC1));
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int q = 0; q < NQ; ++q)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[mt][q][v] += pv[(mt * NQ + q) * 16 + v];
-    }
-    if (tid == 0) __hip_atomic_store(&p.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (P > 1 && !split_fixup<MT, NQ>(p, acc, tn * mtiles + tm, piece, (int *)(lds + 2 * BUF))) return;
 
   if constexpr (SWI) {
     // y[m, j] = silu(gate) * up, one 32x32 tile per exchange
@@ -644,6 +659,271 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   });
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K prefill on v_mfma_f32_32x32x16 with dequantized weight operands.
+// The weight-only k_gemm keeps Q4_K exact (codes offset by 128, one extra
+// MFMA per 32-k slice for the min term, the sub-block scales applied to f32
+// partials), which leaves it bound by VALU and half its MFMAs on x * 1.
+// Prefill instead takes each weight as the value DIAL's GGUF prefill
+// multiplies by: d*sc*q - dmin*m in f32, rounded to f16 -- the weight
+// build_worker_gguf_fp16_prefill_linear dequantizes once
+// (qwen3_vl/worker_gguf.rs:426-455, candle's Q4K to_float) -- against f16
+// activations (the GGUF worker's dtype), one MFMA per 16-k step.  bf16
+// activations take the f32 weight as a bf16 hi + lo pair (two MFMAs, 2^-17
+// relative), since one bf16 rounding of the weight alone (2^-9) would
+// dominate the product's error.
+//
+// Layout as k_gemm32: a 256-thread workgroup computes a (32*MT) x 256 tile;
+// wave v owns 32-column MFMA tiles q = 0, 1 (strips s0 + 2q, s0 + 2q + 1;
+// lane l: column l % 32, k group h = l / 32).  A stage is one quarter i of
+// a 256-k chunk: k = 64i + 8g + j (low nibbles, sub-block 2i) and
+// 64i + 32 + 8g + j (high nibbles, sub-block 2i + 1) sit in byte 8i + j of
+// tile lane r + 16g, so the stage's 16-k steps 0..3 read lane groups
+// g = h, 2 + h, h, 2 + h, low nibbles for steps 0-1 and high for 2-3: two
+// 8-byte loads per column tile, plus the row's 16-byte block header.
+// ---------------------------------------------------------------------------
+template <int ACT>
+__device__ __forceinline__ void q4k_operand(uint32_t d0, uint32_t d1, bool high, float s1, float s2, u32x4 &hi,
+                                            u32x4 &lo) {
+  // the high nibbles are taken in place (16q) against s1 / 16 (exact)
+  const uint32_t m = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+  const float sc = high ? s1 * 0.0625f : s1;
+  const uint32_t x[2] = {d0 & m, d1 & m};
+  float wv[8];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    wv[4 * i] = __builtin_fmaf(sc, (float)(x[i] & 0xffu), -s2);
+    wv[4 * i + 1] = __builtin_fmaf(sc, (float)((x[i] >> 8) & 0xffu), -s2);
+    wv[4 * i + 2] = __builtin_fmaf(sc, (float)((x[i] >> 16) & 0xffu), -s2);
+    wv[4 * i + 3] = __builtin_fmaf(sc, (float)(x[i] >> 24), -s2);
+  }
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (ACT == kActF16N) {
+      const h2 v = {(_Float16)wv[2 * i], (_Float16)wv[2 * i + 1]};
+      hi[i] = __builtin_bit_cast(uint32_t, v);
+    } else {
+      const b2 v = {(__bf16)wv[2 * i], (__bf16)wv[2 * i + 1]};
+      const uint32_t hb = __builtin_bit_cast(uint32_t, v);
+      const b2 u = {(__bf16)(wv[2 * i] - __uint_as_float(hb << 16)),
+                    (__bf16)(wv[2 * i + 1] - __uint_as_float(hb & 0xffff0000u))};
+      hi[i] = hb;
+      lo[i] = __builtin_bit_cast(uint32_t, u);
+    }
+  }
+}
+
+// d * sc and dmin * m (f32, exact) of sub-blocks 2i and 2i + 1 from a Q4_K
+// block header {d, dmin, scales[12]} (the 6-bit packing of
+// candle's get_scale_min_k4).
+template <int I>
+__device__ __forceinline__ void q4k_scales(u32x4 hd, float (&s1)[2], float (&s2)[2]) {
+  const float d = f16_bits_to_f32(hd[0] & 0xffffu), dmin = f16_bits_to_f32(hd[0] >> 16);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int j = 2 * I + e;
+    uint32_t sc, mn;
+    if (j < 4) {
+      sc = (hd[1] >> (8 * j)) & 63u;
+      mn = (hd[2] >> (8 * j)) & 63u;
+    } else {
+      const int jj = j - 4;
+      const uint32_t b8 = (hd[3] >> (8 * jj)) & 0xffu;
+      sc = (b8 & 0xfu) | (((hd[1] >> (8 * jj + 6)) & 3u) << 4);
+      mn = (b8 >> 4) | (((hd[2] >> (8 * jj + 6)) & 3u) << 4);
+    }
+    s1[e] = d * (float)sc;
+    s2[e] = dmin * (float)mn;
+  }
+}
+
+template <int ACT, int MT, int OCC, bool SWI>
+__global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
+  static_assert(ACT == DIALQ_BF16 || ACT == kActF16N, "bf16 or f16 activations");
+  constexpr bool HL = ACT == DIALQ_BF16;  // weight as bf16 hi + lo
+  constexpr int SK = 64, BY = 2;
+  constexpr int ROWS = 32 * MT, STRIDE = SK + 8, BUF = ROWS * STRIDE;
+  constexpr int NQ = 2, PIECES = ROWS * SK / 8 / 256;
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // [2][ROWS][STRIDE]
+  const WeightView &w = p.w;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
+  int tm, tn, piece;
+  const int nt = SWI ? (int)((w.pair + 7) / 8) : (int)((w.n_strips + 15) / 16);
+  const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
+  const int P = p.P;
+  split_tile_of(nt, mtiles, P, tm, tn, piece);
+  const int m0 = tm * ROWS;
+  int s0 = tn * 16 + wave * 4, slim = (int)w.n_strips, j0 = 0;
+  if constexpr (SWI) swiglu_strips<16>(w, tn, wave, s0, slim, j0);
+  const int K = (int)w.K;
+  // this workgroup's 256-k chunks [c0, c1): four stages each
+  const int c0 = (int)((int64_t)piece * w.k_chunks / P), c1 = (int)((int64_t)(piece + 1) * w.k_chunks / P);
+  const int nstage = 4 * (c1 - c0);
+  const int kend = (c1 * 256 < K) ? c1 * 256 : K;
+  const int64_t total = w.n_strips * w.k_chunks;
+  const rsrc_t rt = make_rsrc(w.tiles, (uint32_t)(total * 2048));
+  const rsrc_t ra = make_rsrc(w.aux, (uint32_t)(total * 256));
+  const int mrows = (int)((p.M - m0) < ROWS ? (p.M - m0) : ROWS);
+  const rsrc_t rx = make_rsrc((const uint8_t *)p.x + (int64_t)m0 * K * BY, (uint32_t)((int64_t)mrows * K * BY));
+
+  XRaw<ACT> apre[PIECES];
+  auto fetch_a = [&](int st) {
+#pragma unroll
+    for (int q = 0; q < PIECES; ++q) {
+      const int pc = tid + q * 256, row = pc / (SK / 8), kk = (pc % (SK / 8)) * 8;
+      const int k = c0 * 256 + st * SK + kk;
+      apre[q] = xraw_load<ACT>(rx, (st < nstage && k < kend) ? (uint32_t)((row * K + k) * BY) : kOOB);
+    }
+  };
+  auto store_a = [&](int buf) {
+    uint16_t *base = lds + buf * BUF;
+#pragma unroll
+    for (int q = 0; q < PIECES; ++q) {
+      const int pc = tid + q * 256, row = pc / (SK / 8), kk = (pc % (SK / 8)) * 8;
+      *(u32x4 *)(base + row * STRIDE + kk) = apre[q].a;
+    }
+  };
+  // stage st's codes (lane groups h and 2 + h) and block header of column
+  // tile q, for this lane's weight row
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  struct Slot {
+    u32x2 c[NQ][2];
+    u32x4 hd[NQ];
+  };
+  auto fetch_b = [&](Slot &sl, int st) {
+    const int c = c0 + st / 4, i = st % 4;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int strip = s0 + 2 * q + sub;
+      const bool valid = st < nstage && strip < slim;
+      const uint32_t tile = (uint32_t)strip * (uint32_t)w.k_chunks + (uint32_t)c;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t off = tile * 2048u + (uint32_t)(i / 2) * 1024u + (uint32_t)(16 * (r + 16 * (2 * e + h)) + 8 * (i % 2));
+        sl.c[q][e] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rt, valid ? (int)off : (int)kOOB, 0, 0));
+      }
+      sl.hd[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               ra, valid ? (int)(tile * 256u + 16u * (uint32_t)r) : (int)kOOB, 0, 0));
+    }
+  };
+
+  f32x16 acc[MT][NQ];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][q][v] = 0.0f;
+
+  Slot wb[2];
+  fetch_b(wb[0], 0);
+  fetch_a(0);
+  store_a(0);
+  fetch_a(1);
+  __builtin_amdgcn_sched_barrier(0);
+  fetch_b(wb[1], 1);
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto stage = [&](Slot &sl, int st, auto quarter) {
+    constexpr int I = decltype(quarter)::value;
+    __syncthreads();  // buffer st&1 written; buffer (st+1)&1 no longer read
+    store_a((st + 1) & 1);
+    fetch_a(st + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    float s1[NQ][2], s2[NQ][2];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) q4k_scales<I>(sl.hd[q], s1[q], s2[q]);
+    u32x2 cw[NQ][2];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      cw[q][0] = sl.c[q][0];
+      cw[q][1] = sl.c[q][1];
+    }
+    fetch_b(sl, st + 2);  // refill with stage st + 2
+    const uint16_t *base = lds + (st & 1) * BUF;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u32x4 bh[NQ], bl[NQ];
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+        q4k_operand<ACT>(cw[q][j & 1][0], cw[q][j & 1][1], j >= 2, s1[q][j >> 1], s2[q][j >> 1], bh[q], bl[q]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int row = mt * 32 + (lane & 31), kk = j * 16 + 8 * h;
+        const u32x4 a = *(const u32x4 *)(base + row * STRIDE + kk);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          acc[mt][q] = mfma32_op<ACT>(a, bh[q], acc[mt][q]);
+          if constexpr (HL) acc[mt][q] = mfma32_op<ACT>(a, bl[q], acc[mt][q]);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int st = 0; st < nstage; st += 4) {
+    stage(wb[0], st, std::integral_constant<int, 0>{});
+    stage(wb[1], st + 1, std::integral_constant<int, 1>{});
+    stage(wb[0], st + 2, std::integral_constant<int, 2>{});
+    stage(wb[1], st + 3, std::integral_constant<int, 3>{});
+  }
+
+  if (P > 1 && !split_fixup<MT, NQ>(p, acc, tn * mtiles + tm, piece, (int *)(lds + 2 * BUF))) return;
+
+  if constexpr (SWI) {
+    const int64_t I = w.pair * 16;
+    float *xch = (float *)lds;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int64_t j = (int64_t)(j0 + 2 * q) * 16 + (lane & 31);  // output column
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float mine[16], up[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mine[v] = acc[mt][q][v];
+        swiglu_exchange(xch, wave, lane, mine, up);
+        if (wave < 2 && j < I) {
+          const int64_t rb = m0 + mt * 32 + 4 * h;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int64_t row = rb + 8 * (v / 4) + (v % 4);
+            if (row < p.M) store_out(p.y, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[v], up[v]));
+          }
+        }
+      }
+    }
+    return;
+  }
+  const bool full = m0 + ROWS <= p.M;
+  const int64_t ldy = out_ld(w);
+  auto body = [&](auto yd, auto chk) __attribute__((always_inline)) {
+    typedef decltype(yd) Y;
+    constexpr bool CHK = decltype(chk)::value;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int64_t col = (int64_t)(s0 + 2 * q) * 16 + (lane & 31);
+      if (col >= w.N) continue;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int64_t rb = m0 + mt * 32 + 4 * h;
+        typename Y::T *py = (typename Y::T *)p.y + rb * ldy + col;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int rr = 8 * (v / 4) + (v % 4);
+          if (!CHK || rb + rr < p.M) py[rr * ldy] = Y::conv(acc[mt][q][v]);
+        }
+      }
+    }
+  };
+  with_y_dtype(p.y_dtype, [&](auto yd) __attribute__((always_inline)) {
+    if (full) body(yd, std::false_type{});
+    else body(yd, std::true_type{});
+  });
+}
+
 // Launch plan of the 32x32 kernel.  Two shapes: 64-row tiles with one 64-k
 // chunk per stage (GEMM32_MT, GEMM32_KS) for prefill, and for 17..96 rows
 // 32-row tiles with two chunks per stage: those launches have few tiles, so
@@ -656,10 +936,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
 // back, traffic worth spending only while the tiles are far fewer than the
 // CUs: small-row launches split while tiles fill at most half the workgroup
 // slots (<= 8 pieces), prefill launches only below CUs / 2 tiles
-// (<= 4 pieces; the 17408-row gate at 128 rows, 136 tiles, is faster whole).
-// Either bound keeps the partials under 32 MiB.
+// (<= 4 pieces; the 17408-row gate at 128 rows, 136 tiles, is faster whole),
+// and never past kGemm32MaxPartBytes of partials.
 constexpr int64_t kGemm32SmallRows = 96;
-constexpr int kGemm32MinChunks = 20;
+constexpr int kGemm32MinChunks = 20;  // 64-k steps per split-K piece, at least
+constexpr size_t kGemm32MaxPartBytes = (size_t)31 << 20;
 struct Gemm32Plan {
   int mt, ks, P;
   int64_t tiles;
@@ -668,35 +949,52 @@ struct Gemm32Plan {
 static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w) {
   Gemm32Plan g;
   const bool small = M <= kGemm32SmallRows;
-  g.mt = small ? 1 : GEMM32_MT;
-  g.ks = small ? 2 : GEMM32_KS;
+  g.mt = small ? 1 : (w.fmt == DIALQ_FORMAT_Q4_K ? GEMMQ4K_MT : GEMM32_MT);
+  g.ks = small ? 2 : GEMM32_KS;  // byte formats; a Q4_K stage is one 64-k quarter chunk
   const int64_t rows = 32 * g.mt, nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
   g.tiles = nt * ((M + rows - 1) / rows);
   g.P = 1;
-  const int64_t cus = device_cus(), slots = (int64_t)GEMM32_OCC * cus;
+  const int64_t occ = w.fmt == DIALQ_FORMAT_Q4_K ? GEMMQ4K_OCC : GEMM32_OCC;
+  const int64_t cus = device_cus(), slots = occ * cus;
   if (small ? g.tiles * 2 <= slots : g.tiles * 2 < cus) {
-    int64_t P = slots / g.tiles, cap = w.k_chunks / kGemm32MinChunks;
+    const int64_t steps = w.k_chunks * (w.fmt == DIALQ_FORMAT_Q4_K ? 4 : 1);
+    int64_t P = slots / g.tiles, cap = steps / kGemm32MinChunks;
     if (cap > (small ? 8 : 4)) cap = small ? 8 : 4;
     if (P > cap) P = cap;
     g.P = (int)(P < 1 ? 1 : P);
+    while (g.P > 1 && g.part_bytes() > kGemm32MaxPartBytes) --g.P;
   }
   return g;
 }
 
-static bool gemm32_applies(const WeightView &w) {
-  return (w.fmt == DIALQ_FORMAT_W8A16 || w.fmt == DIALQ_FORMAT_FP8_ROW) &&
-         w.n_strips * w.k_chunks * 1024 <= 0xffffffffLL;
+// The 32x32 kernels: W8A16 / FP8_ROW (k_gemm32) and Q4_K with bf16 or f16
+// activations (k_gemm_q4k; f32 activations keep the exact k_gemm).
+static bool gemm32_applies(const WeightView &w, int x_dtype) {
+  if (w.fmt == DIALQ_FORMAT_W8A16 || w.fmt == DIALQ_FORMAT_FP8_ROW) return w.n_strips * w.k_chunks * 1024 <= 0xffffffffLL;
+  if (w.fmt == DIALQ_FORMAT_Q4_K)
+    return x_dtype != DIALQ_F32 && w.n_strips * w.k_chunks * 2048 <= 0xffffffffLL;
+  return false;
 }
 
-void gemm_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count) {
+void gemm_workspace(int64_t M, const WeightView &w, int x_dtype, size_t &part_bytes, size_t &cnt_count) {
   part_bytes = 0;
   cnt_count = 0;
-  if (!gemm32_applies(w) || M <= 0) return;
+  if (!gemm32_applies(w, x_dtype) || M <= 0) return;
   const Gemm32Plan g = gemm32_plan(M, w);
   if (g.P > 1) {
     part_bytes = g.part_bytes();
     cnt_count = (size_t)g.tiles;
   }
+}
+
+template <int ACT, int MT>
+static hipError_t gemm_q4k_launch(const GemmParams &p, int64_t grid, hipStream_t st) {
+  constexpr int BUF = 32 * MT * (64 + 8);
+  static_assert(2 * BUF * 2 >= 8192, "the SwiGLU exchange reuses the staging LDS");
+  const size_t lds_bytes = 2 * BUF * 2 + 16;  // two staging buffers and the split-K arrival flag
+  if (p.w.pair) k_gemm_q4k<ACT, MT, GEMMQ4K_OCC, true><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
+  else k_gemm_q4k<ACT, MT, GEMMQ4K_OCC, false><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
+  return hipGetLastError();
 }
 
 template <int FMT, int ACT, int MT, int KS>
@@ -714,13 +1012,20 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
                                 size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st) {
   typedef GemmShape<FMT, ACT> S;
   if ((int64_t)S::ROWS * w.K * ActTraits<ACT>::BYTES > 0xffffffffLL) return hipErrorInvalidValue;
-  if constexpr (FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW) {
-    if (gemm32_applies(w)) {
+  constexpr bool BYTE = FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW;
+  constexpr bool Q4K = FMT == DIALQ_FORMAT_Q4_K && (ACT == DIALQ_BF16 || ACT == kActF16N);
+  if constexpr (BYTE || Q4K) {
+    if (gemm32_applies(w, ACT == DIALQ_F32 ? DIALQ_F32 : DIALQ_BF16)) {
       const Gemm32Plan g = gemm32_plan(M, w);
       if (g.P > 1 && ((size_t)g.tiles > cnt_count || g.part_bytes() > part_bytes)) return hipErrorInvalidValue;
       const GemmParams p{w, x, y, M, y_dtype, g.P, part, cnt};
-      if (g.mt == 1) return gemm32_launch<FMT, ACT, 1, 2>(p, g.tiles * g.P, st);
-      return gemm32_launch<FMT, ACT, GEMM32_MT, GEMM32_KS>(p, g.tiles * g.P, st);
+      if constexpr (Q4K) {
+        if (g.mt == 1) return gemm_q4k_launch<ACT, 1>(p, g.tiles * g.P, st);
+        return gemm_q4k_launch<ACT, GEMMQ4K_MT>(p, g.tiles * g.P, st);
+      } else {
+        if (g.mt == 1) return gemm32_launch<FMT, ACT, 1, 2>(p, g.tiles * g.P, st);
+        return gemm32_launch<FMT, ACT, GEMM32_MT, GEMM32_KS>(p, g.tiles * g.P, st);
+      }
     }
   }
   static_assert(S::LDS_BYTES >= 8192, "the SwiGLU exchange reuses the staging LDS");

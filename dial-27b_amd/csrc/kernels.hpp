@@ -87,9 +87,9 @@ void set_gemv_wait_limit(int64_t polls);
 int gemv_wait_limit();
 // Prefill GEMM with weight-only dequantization (bf16 / f16 MFMA operands).
 // Launches with fewer tiles than workgroup slots split each tile along K and
-// need gemm_workspace(M, w) of scratch: `part` (partial tiles) and `cnt`
-// (per-tile counters, zero before the call and left zero after it).
-void gemm_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count);
+// need gemm_workspace(M, w, x_dtype) of scratch: `part` (partial tiles) and
+// `cnt` (per-tile counters, zero before the call and left zero after it).
+void gemm_workspace(int64_t M, const WeightView &w, int x_dtype, size_t &part_bytes, size_t &cnt_count);
 hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype, float *part,
                        size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st);
 // Native low-precision prefill: FP8_BLOCK with per-token fp8 activations,

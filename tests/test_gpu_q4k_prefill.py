@@ -1,0 +1,111 @@
+"""Q4_K prefill (k_gemm_q4k): each weight is dequantized to d*sc*q - dmin*m
+in f32 and multiplied as f16 against f16 activations -- the weight DIAL's
+GGUF prefill builds once, build_worker_gguf_fp16_prefill_linear
+(qwen3_vl/worker_gguf.rs:426-455) -- or as a bf16 hi + lo pair against bf16
+activations.  Pinned three ways on the same inputs:
+  * f16 x: against the fp64 product with the f16-rounded dequantized weight
+    (the hybrid prefill's weight), to f32 accumulation (rel-L2 <= 2e-5; a
+    weight rounded once from the exact value instead of through f32 may
+    differ by one f16 ulp in rare ties);
+  * bf16 x: against the exact product (hi + lo carries 16 significant bits:
+    rel-L2 <= 2e-5 in f32 output);
+  * both against the exact oracle to the weight-only bar (1e-3).
+Row counts cover the 32-row tiles (<= 96 rows, split along K), the 64-row
+tiles, ragged row blocks, SwiGLU and graph replay of a split launch."""
+import numpy as np
+import pytest
+
+import dialq as dq
+import oracle as O
+from helpers import make_weight, reference_product, to_torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(n, k, seed):
+    raw, scales, kw, deq = make_weight(dq.Q4_K, n, k, seed=seed)
+    return dq.Linear.create(dq.Q4_K, n, k, raw, scales, **kw), deq
+
+
+@pytest.mark.parametrize("m", [17, 40, 96, 97, 130, 256, 300])
+@pytest.mark.parametrize("n,k", [(320, 512), (1024, 5120)], ids=["k512", "k5120"])
+def test_q4k_prefill_weights_and_parity(m, n, k, torch_dev):
+    import torch
+    lin, deq = _case(n, k, seed=m + k)
+    rng = np.random.default_rng(m)
+    x = O.round_bf16(rng.normal(0, 1, (m, k)).astype(np.float32))  # exact in bf16 and f16
+    for x_dtype in (dq.F16, dq.BF16):
+        y = torch.full((m, n), float("nan"), device=torch_dev, dtype=torch.float32)
+        lin.forward(to_torch(x, x_dtype, torch_dev), y, path=dq.PATH_GEMM)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        exact = O.matmul_f64(x, deq)
+        if x_dtype == dq.F16:
+            hybrid = O.matmul_f64(x, O.round_f16(deq))
+            assert O.rel_l2(got, hybrid) <= 2e-5, (m, "f16 weights")
+        else:
+            assert O.rel_l2(got, exact) <= 2e-5, (m, "hi + lo weights")
+        assert O.rel_l2(got, exact) <= 1e-3
+        # bf16 / f16 outputs of the same launch
+        y_dtype = dq.F16 if x_dtype == dq.F16 else dq.BF16
+        yo = torch.empty(m, n, device=torch_dev, dtype=torch.float16 if x_dtype == dq.F16 else torch.bfloat16)
+        lin.forward(to_torch(x, x_dtype, torch_dev), yo, path=dq.PATH_GEMM)
+        torch.cuda.synchronize()
+        assert O.rel_l2(yo.float().cpu().numpy(), reference_product(x, deq, y_dtype)) <= 1e-3
+
+
+def test_q4k_prefill_f32_activations_stay_exact(torch_dev):
+    # f32 activations keep the exact weight-only kernel
+    import torch
+    lin, deq = _case(256, 512, seed=3)
+    x = np.random.default_rng(3).normal(0, 1, (70, 512)).astype(np.float32)
+    y = torch.empty(70, 256, device=torch_dev, dtype=torch.float32)
+    lin.forward(torch.from_numpy(x).to(torch_dev), y, path=dq.PATH_GEMM)
+    torch.cuda.synchronize()
+    assert O.rel_l2(y.cpu().numpy(), O.matmul_f64(x, deq)) <= 1e-5
+
+
+@pytest.mark.parametrize("m", [33, 200])
+def test_q4k_prefill_swiglu(m, torch_dev):
+    import torch
+    i_dim, k = 512, 1024
+    lin, deq = _case(2 * i_dim, k, seed=m)
+    x = O.round_bf16(np.random.default_rng(m).normal(0, 1, (m, k)).astype(np.float32))
+    for x_dtype in (dq.F16, dq.BF16):
+        y = torch.full((m, i_dim), float("nan"), device=torch_dev, dtype=torch.float32)
+        lin.forward_swiglu(to_torch(x, x_dtype, torch_dev), y, path=dq.PATH_GEMM)
+        torch.cuda.synchronize()
+        want = O.swiglu(O.matmul_f64(x, deq))
+        assert O.rel_l2(y.cpu().numpy(), want) <= 1e-3, x_dtype
+
+
+def test_q4k_prefill_split_graph_replay(torch_dev):
+    # a split launch (48 rows of a 17408x5120 gate: 32-row tiles, 4 pieces)
+    # replays bit for bit, with eager split launches of another row count
+    # between the replays
+    import torch
+    n, k, m = 17408, 5120, 48
+    g = torch.Generator(device=torch_dev).manual_seed(5)
+    lin = dq.Linear.quantize(dq.Q4_K, torch.randn(n, k, device=torch_dev, generator=g) * 0.02)
+    x = torch.randn(m, k, device=torch_dev, generator=g).to(torch.float16)
+    x2 = torch.randn(20, k, device=torch_dev, generator=g).to(torch.float16)
+    y = torch.empty(m, n, device=torch_dev, dtype=torch.float16)
+    y2 = torch.empty(20, n, device=torch_dev, dtype=torch.float16)
+    lin.forward(x, y, path=dq.PATH_GEMM)
+    torch.cuda.synchronize()
+    want = y.clone()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        lin.forward(x, y, path=dq.PATH_GEMM, stream=torch.cuda.current_stream())
+    for _ in range(3):
+        y.zero_()
+        lin.forward(x2, y2, path=dq.PATH_GEMM)
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+    # sampled rows against the dequantized weight's f16 product
+    w16 = torch.empty(n, k, device=torch_dev, dtype=torch.float16)
+    lin.dequantize(w16)
+    ref = (x[:8].float() @ w16.float().t()).cpu().numpy()
+    assert O.rel_l2(want[:8].float().cpu().numpy(), ref) <= 1e-3
