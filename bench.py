@@ -26,8 +26,10 @@ without gate_up's SwiGLU epilogue), the quantized lm_head decode GEMV (vocab
 dominant kernel and the CPU baseline.
 
 `--profile` runs only the dominant kernel (the grouped W8A16 gate / up
-decode launch, eager, over rotating copies) plus a 256 MiB device-to-device
-copy used to scale the HBM byte counters; `--profile-lm-head` the same for the lm_head GEMV;
+decode launch, eager, over rotating copies; `--profile-format` another
+weight format) plus a 256 MiB device-to-device copy used to scale the HBM
+byte counters; `--profile-layer` replays only the headline decode step;
+`--profile-lm-head` the same for the lm_head GEMV;
 `--profile-prefill` runs only the prefill GEMMs of one
 layer per format, `--profile-prefill-gate` only the gate-shape prefill GEMM
 per format (the counter runs), `--profile-swiglu` the fused gate_up with and without its
@@ -74,6 +76,10 @@ def parse():
     ap.add_argument("--profile", action="store_true",
                     help="only the dominant kernel's launches and the calibration copy (for rocprofv3)")
     ap.add_argument("--profile-launches", type=int, default=50)
+    ap.add_argument("--profile-format", default="w8a16", choices=["w8a16", "q4_k", "fp8_block", "mxfp4"],
+                    help="weight format of the --profile launches")
+    ap.add_argument("--profile-layer", action="store_true",
+                    help="only decode-step replays of the W8A16 layer (for a per-launch kernel trace)")
     ap.add_argument("--profile-lm-head", action="store_true",
                     help="run only the W8A16 lm_head GEMV (vocab 248320 x 5120) for rocprofv3")
     ap.add_argument("--profile-prefill", action="store_true",
@@ -273,29 +279,43 @@ def time_per_linear(dq, torch, layers, dev):
     return out
 
 
-def profile_run(dq, torch, dev, launches):
+def profile_run(dq, torch, dev, launches, fmt_name="w8a16"):
     """Dominant kernel only -- the grouped gate / up decode launch (two
-    17408x5120 W8A16 members, 178 MB) over rotating copies, eager -- plus
-    the calibration copy."""
+    17408x5120 members, 178 MB in W8A16) over rotating copies, eager -- plus
+    the calibration copy.  `fmt_name` picks the weight format (copies enough
+    to exceed the 256 MB last-level cache)."""
     name, ns, k = DOM_GROUP
+    fmt = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}[fmt_name]
+    copies = DOM_GROUP_COPIES if fmt == dq.W8A16 else 6
     g = torch.Generator(device=dev).manual_seed(7)
     groups = []
-    for _ in range(DOM_GROUP_COPIES):
-        groups.append([dq.Linear.quantize(dq.W8A16, torch.randn(n, k, device=dev, generator=g) * 0.02,
+    for _ in range(copies):
+        groups.append([dq.Linear.quantize(fmt, torch.randn(n, k, device=dev, generator=g) * 0.02,
                                           scale_dtype=dq.BF16) for n in ns])
     x = torch.randn(1, k, device=dev).to(torch.bfloat16)
     y = torch.empty(1, sum(ns), device=dev, dtype=torch.bfloat16)
     stream = torch.cuda.current_stream()
     for i in range(launches):
-        dq.forward_group(groups[i % DOM_GROUP_COPIES], x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+        dq.forward_group(groups[i % copies], x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
     torch.cuda.synchronize()
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"# profile: {launches} grouped launches of W8A16 {name} 2 x [{ns[0]}x{k}] M=1; 3 copies of 256 MiB "
+    print(f"# profile: {launches} grouped launches of {fmt_name} {name} 2 x [{ns[0]}x{k}] M=1; 3 copies of 256 MiB "
           "(calibration: 268435456 bytes read and written per copy)", flush=True)
+
+
+def profile_layer_run(dq, torch, dev, replays=200):
+    """The headline decode step as timed: the 27B layer's four grouped /
+    single launches (q/k/v, o, gate/up, down) captured per layer copy and
+    replayed `replays` times, so a kernel trace shows every launch of the
+    step and the gaps between them."""
+    layers = build_layers(dq, torch, dq.W8A16, 3, dev)
+    time_decode(dq, torch, layers, replays, 20, dev, groups=LAYER_27B_GROUPS)
+    print(f"# profile: {replays} decode-step replays of the W8A16 27B layer (4 launches each), 3 copies",
+          flush=True)
 
 
 def profile_swiglu_run(dq, torch, dev, launches=20):
@@ -608,7 +628,10 @@ def main():
 
     dev = torch.device("cuda:0")
     if a.profile:
-        profile_run(dq, torch, dev, a.profile_launches)
+        profile_run(dq, torch, dev, a.profile_launches, a.profile_format)
+        return
+    if a.profile_layer:
+        profile_layer_run(dq, torch, dev)
         return
     if a.profile_lm_head:
         profile_lm_head_run(dq, torch, dev)
