@@ -19,7 +19,9 @@ Layer copies rotate so the weight working set (COPIES x 341 MB) exceeds the
 weight bytes streamed / wall time of the timed steps, in GB/s.  Extra keys
 report the same decode for Q4_K / FP8-128 / MXFP4, the prefill GEMM TFLOP/s
 (W8A16 and Q4_K at M = 2048 -- Q4_K also with f16 activations, the dtype
-of DIAL's GGUF worker --, FP8-128 and MXFP4 native at M = 1024; also over
+of DIAL's GGUF worker --, FP8-128 and MXFP4 native at M = 1024; q / k / v
+and gate / up as grouped forwards like the decode step, and as seven
+forwards in prefill_tflops_ungrouped; also over
 the fused qkv / o / gate_up / down projections DIAL's layers call, with and
 without gate_up's SwiGLU epilogue), the quantized lm_head decode GEMV (vocab
 248320 x 5120) and the device token selection after it, the roofline of the
@@ -390,16 +392,30 @@ def profile_prefill_run(dq, torch, dev, iters=5):
         torch.cuda.empty_cache()
 
 
-def time_prefill(dq, torch, lins, m, iters, dev, path, shapes=LAYER_27B, swiglu=(), act="bfloat16"):
+def time_prefill(dq, torch, lins, m, iters, dev, path, shapes=LAYER_27B, swiglu=(), act="bfloat16", groups=None):
     """Device time of one prefill pass over the layer's seven linears
     (activation quantization included for the native paths), captured in a
     HIP graph like the decode step and replayed `iters` times between HIP
-    events on the replay stream."""
+    events on the replay stream.  With `groups` ([(name, indices of
+    shapes)]), the linears of a group share one x and run as one grouped
+    forward into their concatenated output, as in the decode step."""
     stream = torch.cuda.current_stream()
-    xs = [torch.randn(m, k, device=dev).to(getattr(torch, act)) for _, n, k in shapes]
-    ys = [torch.empty(m, out_cols(name, n, swiglu), device=dev, dtype=getattr(torch, act)) for name, n, k in shapes]
+    dt = getattr(torch, act)
+    if groups is not None:
+        xs = [torch.randn(m, shapes[idx[0]][2], device=dev).to(dt) for _, idx in groups]
+        ys = [torch.empty(m, sum(shapes[i][1] for i in idx), device=dev, dtype=dt) for _, idx in groups]
+    else:
+        xs = [torch.randn(m, k, device=dev).to(dt) for _, n, k in shapes]
+        ys = [torch.empty(m, out_cols(name, n, swiglu), device=dev, dtype=dt) for name, n, k in shapes]
 
     def body(st):
+        if groups is not None:
+            for (_, idx), x, y in zip(groups, xs, ys):
+                if len(idx) == 1:
+                    lins[idx[0]].forward(x, y, path=path, stream=st)
+                else:
+                    dq.forward_group([lins[i] for i in idx], x, y, path=path, stream=st)
+            return
         for lin, x, y, (name, _, _) in zip(lins, xs, ys, shapes):
             run_linear(lin, name, x, y, swiglu, path=path, stream=st)
     body(stream)  # eager first: sizes the handles' scratch outside capture
@@ -694,11 +710,16 @@ def main():
              "decode_us_per_launch_w8a16":
              {k: round(v * 1e6, 2) for k, v in per.items()}, "prefill_tflops": {}, "prefill_pct_mfma_peak": {}}
     sweep = [s for s in a.sweep.split(",") if s]
+    extra["prefill_tflops_ungrouped"] = {}
     if "w8a16" in sweep:
-        tf, s2 = time_prefill(dq, torch, layers[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
+        tf, s2 = time_prefill(dq, torch, layers[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM,
+                              groups=LAYER_27B_GROUPS)
         extra["prefill_tflops"]["w8a16_m2048"] = round(tf, 1)
         extra["prefill_pct_mfma_peak"]["w8a16_m2048"] = round(100.0 * tf / MFMA_PEAK_TFLOPS["bf16"], 1)
-        print(f"# w8a16 prefill M=2048: {tf:.1f} TFLOP/s ({s2 * 1e3:.2f} ms/layer)", file=sys.stderr, flush=True)
+        tfu, _ = time_prefill(dq, torch, layers[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
+        extra["prefill_tflops_ungrouped"]["w8a16_m2048"] = round(tfu, 1)
+        print(f"# w8a16 prefill M=2048: {tf:.1f} TFLOP/s ({s2 * 1e3:.2f} ms/layer; {tfu:.1f} as seven forwards)",
+              file=sys.stderr, flush=True)
     del layers
     torch.cuda.empty_cache()
     # the same layer with fused qkv / gate_up projections (four linears)
@@ -748,10 +769,13 @@ def main():
         gbs = layer_bytes(dq, fmt) * max(a.steps // 3, 10) / sd / 1e9
         extra["decode_gbs"][name] = round(gbs, 1)
         if fmt in (dq.FP8_BLOCK, dq.MXFP4):
-            tf, s2 = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE)
+            tf, s2 = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE,
+                                  groups=LAYER_27B_GROUPS)
             extra["prefill_tflops"][name + "_native_m1024"] = round(tf, 1)
             peak = MFMA_PEAK_TFLOPS["fp8" if fmt == dq.FP8_BLOCK else "fp4"]
             extra["prefill_pct_mfma_peak"][name + "_native_m1024"] = round(100.0 * tf / peak, 1)
+            tfu, _ = time_prefill(dq, torch, ls[0], 1024, a.prefill_iters, dev, dq.PATH_GEMM_NATIVE)
+            extra["prefill_tflops_ungrouped"][name + "_native_m1024"] = round(tfu, 1)
             # the fused projections DIAL's layers call (qkv, o, gate_up, down)
             del ls
             torch.cuda.empty_cache()
@@ -763,11 +787,14 @@ def main():
                                    shapes=LAYER_27B_FUSED, swiglu=("gate_up",))
             extra.setdefault("prefill_tflops_fused_swiglu", {})[name + "_native_m1024"] = round(tff2, 1)
         else:
-            tf, s2 = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
+            tf, s2 = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, groups=LAYER_27B_GROUPS)
             extra["prefill_tflops"][name + "_m2048"] = round(tf, 1)
             extra["prefill_pct_mfma_peak"][name + "_m2048"] = round(100.0 * tf / MFMA_PEAK_TFLOPS["bf16"], 1)
+            tfu, _ = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
+            extra["prefill_tflops_ungrouped"][name + "_m2048"] = round(tfu, 1)
             if fmt == dq.Q4_K:  # the GGUF worker's f16 activations
-                tfh, _ = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, act="float16")
+                tfh, _ = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, act="float16",
+                                      groups=LAYER_27B_GROUPS)
                 extra["prefill_tflops"][name + "_f16act_m2048"] = round(tfh, 1)
                 extra["prefill_pct_mfma_peak"][name + "_f16act_m2048"] = round(100.0 * tfh / MFMA_PEAK_TFLOPS["f16"], 1)
         print(f"# {name}: decode {gbs:.1f} GB/s, prefill {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)

@@ -494,9 +494,47 @@ void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void 
 // y = cat([x W_0^T, ..., x W_{n-1}^T], -1) for handles that share x: the
 // decode path runs the strips of up to four same-format members in one
 // launch (one workgroup per strip, x staged once per workgroup as in a
-// single forward); every other case runs one launch per member, each
-// writing its columns of the concatenated output.
+// single forward); the prefill paths run the column tiles of up to four
+// same-format members in one GEMM launch (W8A16, FP8_ROW, Q4_K with bf16 /
+// f16 x; FP8_BLOCK and MXFP4 native on x quantized once); every other case
+// runs one launch per member, each writing its columns of the concatenated
+// output.
 constexpr int kGroupMax = 4;
+
+// One prefill launch over members Ls[0..n) (one format and K, resolved path
+// GEMM or GEMM_NATIVE), with Ls[0]'s scratch: false, launching nothing,
+// where no grouped kernel applies.
+bool run_prefill_group(Linear *const *Ls, const WeightView *ws, void *const *ys, int n, const void *x, int x_dtype,
+                       int64_t rows, int y_dtype, int path, hipStream_t st) {
+  Linear *L = Ls[0];
+  size_t part = 0, ncnt = 0;
+  if (path == DIALQ_PATH_GEMM) {
+    if (!gemm_group_workspace(rows, ws, n, x_dtype, part, ncnt)) return false;
+    std::lock_guard<std::mutex> lock(L->scratch_mu);
+    ensure_native_scratch(L, part, ncnt, st);
+    const hipError_t r = launch_gemm_group(ws, ys, n, x, x_dtype, rows, y_dtype, (float *)L->native_part.p,
+                                           L->native_part.n, (int *)L->native_cnt.p, L->native_cnt.n / sizeof(int), st);
+    if (r == hipErrorNotSupported) return false;
+    hip_check(r, "grouped GEMM launch");
+    return true;
+  }
+  if (!native_group_workspace(rows, ws, n, part, ncnt)) return false;
+  const ForwardPlan pl = plan_forward(L, ws[0], x_dtype, rows, path);  // activation codes, scales, k_pad
+  std::lock_guard<std::mutex> lock(L->scratch_mu);
+  ensure_scratch(L, pl.codes + pl.xscale, st);
+  ensure_native_scratch(L, part, ncnt, st);
+  uint8_t *codes = (uint8_t *)L->act_scratch.p;
+  void *xscale = codes + pl.codes;
+  if (L->desc.format == DIALQ_FORMAT_FP8_BLOCK)
+    hip_check(launch_act_fp8(x, x_dtype, rows, ws[0].K, pl.k_pad, codes, (float *)xscale, st), "activation quantizer");
+  else
+    hip_check(launch_act_mxfp4(x, x_dtype, rows, ws[0].K, pl.k_pad, codes, (uint8_t *)xscale, st),
+              "activation quantizer");
+  hip_check(launch_gemm_native_group(ws, ys, n, codes, xscale, rows, pl.k_pad, y_dtype, (float *)L->native_part.p,
+                                     L->native_part.n, (int *)L->native_cnt.p, L->native_cnt.n / sizeof(int), st),
+            "grouped native GEMM launch");
+  return true;
+}
 
 void forward_group_impl(Linear *const *Ls, int32_t n, const void *x, int32_t x_dtype, int64_t rows, void *y,
                         int32_t y_dtype, int32_t path, void *stream, int device_io) {
@@ -568,6 +606,19 @@ void forward_group_impl(Linear *const *Ls, int32_t n, const void *x, int32_t x_d
       else if (r != hipErrorNotSupported)
         hip_check(r, "grouped GEMV launch");
     }
+    j = e;
+  }
+  // runs of up to four consecutive prefill members of one format and path:
+  // one GEMM launch over all their column tiles (native: on x quantized once)
+  for (int j = 0; j < n;) {
+    if (paths[j] != DIALQ_PATH_GEMM && paths[j] != DIALQ_PATH_GEMM_NATIVE) {
+      ++j;
+      continue;
+    }
+    int e = j + 1;
+    while (e < n && e - j < kGroupMax && paths[e] == paths[j] && Ls[e]->desc.format == Ls[j]->desc.format) ++e;
+    if (e - j >= 2 && run_prefill_group(&Ls[j], &views[j], &outs[j], e - j, xp, x_dtype, rows, y_dtype, paths[j], st))
+      for (int i = j; i < e; ++i) done[i] = true;
     j = e;
   }
   for (int j = 0; j < n; ++j)
@@ -855,7 +906,7 @@ int dialq_linear_forward_group(void *const *linears, int32_t n, const void *x, i
 
 void dialq_debug_set_wait_limit(int64_t polls) { set_gemv_wait_limit(polls); }
 
-int64_t dialq_debug_grouped_launches(void) { return gemv_grouped_launches(); }
+int64_t dialq_debug_grouped_launches(void) { return gemv_grouped_launches() + gemm_grouped_launches(); }
 
 int dialq_linear_forward_noalloc(void *linear, const void *x, int32_t x_dtype, int64_t rows, void *y,
                                  int32_t y_dtype, int32_t path, void *stream, char *error, size_t error_size) {

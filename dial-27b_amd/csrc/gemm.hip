@@ -18,9 +18,30 @@
 // quantized first (per-token E4M3 with an f32 scale; per-32 MXFP4 with E8M0
 // scales) and the product runs on v_mfma_scale_f32_32x32x64_f8f6f4, with the
 // E8M0 scales of both operands applied by the instruction.
+#include <atomic>
+
 #include "tile_ops.hpp"
 
 namespace dialq {
+
+std::atomic<int64_t> g_prefill_grouped_launches{0};  // grouped prefill launches made (a test hook)
+
+// Grouped launch (nm > 1): weights that share x and K, their column tiles
+// laid end to end -- member j owns global column tiles [tbase[j],
+// tbase[j + 1]) and writes through ym[j] with its view's output stride.
+struct GemmGroup {
+  int nm = 0;
+  int tbase[kGemmMaxGroup + 1] = {};
+  WeightView wm[kGemmMaxGroup] = {};
+  void *ym[kGemmMaxGroup] = {};
+};
+
+// The member owning global column tile tn.
+__device__ __forceinline__ int group_member(const GemmGroup &g, int tn) {
+  int j = 0;
+  while (j + 1 < g.nm && tn >= g.tbase[j + 1]) ++j;
+  return j;
+}
 
 struct GemmParams {
   WeightView w;
@@ -28,12 +49,13 @@ struct GemmParams {
   void *y;
   int64_t M;
   int y_dtype;
-  // Split-K (k_gemm32, P > 1): each tile's chunks split into P pieces, one
-  // workgroup each; partial tiles in `part` ([tiles][P][rows x 256]), one
-  // arrival counter per tile in `cnt` (zero between launches).
+  // Split-K (k_gemm32, k_gemm_q4k; P > 1): each tile's chunks split into P
+  // pieces, one workgroup each; partial tiles in `part` ([tiles][P][rows x
+  // 256]), one arrival counter per tile in `cnt` (zero between launches).
   int P = 1;
   float *part = nullptr;
   int *cnt = nullptr;
+  GemmGroup g;  // k_gemm32, k_gemm_q4k
 };
 
 template <int FMT, int ACT>
@@ -485,15 +507,20 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   constexpr int ROWS = 32 * MT, STRIDE = SK + 8, BUF = PARTS * ROWS * STRIDE;
   constexpr int NQ = 2, PIECES = ROWS * SK / 8 / 256;
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // [2][PARTS][ROWS][STRIDE] bf16
-  const WeightView &w = p.w;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
   int tm, tn, piece;
-  const int nt = SWI ? (int)((w.pair + 7) / 8) : (int)((w.n_strips + 15) / 16);
+  const bool grp = !SWI && p.g.nm > 1;
+  const int nt = grp ? p.g.tbase[p.g.nm] : SWI ? (int)((p.w.pair + 7) / 8) : (int)((p.w.n_strips + 15) / 16);
   const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
   const int P = p.P;
   split_tile_of(nt, mtiles, P, tm, tn, piece);
+  const int tg = tn * mtiles + tm;  // split-K counter: the global tile
+  const int jm = grp ? group_member(p.g, tn) : 0;
+  const WeightView &w = grp ? p.g.wm[jm] : p.w;
+  void *const yout = grp ? p.g.ym[jm] : p.y;
+  if (grp) tn -= p.g.tbase[jm];
   const int m0 = tm * ROWS;
   int s0 = tn * 16 + wave * 4, slim = (int)w.n_strips, j0 = 0;
   if constexpr (SWI) swiglu_strips<16>(w, tn, wave, s0, slim, j0);
@@ -602,7 +629,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   }
   if (st < nstage) stage(wb[0], st);
 
-  if (P > 1 && !split_fixup<MT, NQ>(p, acc, tn * mtiles + tm, piece, (int *)(lds + 2 * BUF))) return;
+  if (P > 1 && !split_fixup<MT, NQ>(p, acc, tg, piece, (int *)(lds + 2 * BUF))) return;
 
   if constexpr (SWI) {
     // y[m, j] = silu(gate) * up, one 32x32 tile per exchange
@@ -624,7 +651,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int64_t row = rb + 8 * (v / 4) + (v % 4);
-            if (row < p.M) store_out(p.y, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[v], up[v]));
+            if (row < p.M) store_out(yout, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[v], up[v]));
           }
         }
       }
@@ -644,7 +671,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int64_t rb = m0 + mt * 32 + 4 * h;
-        typename Y::T *py = (typename Y::T *)p.y + rb * ldy + col;
+        typename Y::T *py = (typename Y::T *)yout + rb * ldy + col;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int rr = 8 * (v / 4) + (v % 4);
@@ -747,15 +774,20 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
   constexpr int ROWS = 32 * MT, STRIDE = SK + 8, BUF = ROWS * STRIDE;
   constexpr int NQ = 2, PIECES = ROWS * SK / 8 / 256;
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // [2][ROWS][STRIDE]
-  const WeightView &w = p.w;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
   int tm, tn, piece;
-  const int nt = SWI ? (int)((w.pair + 7) / 8) : (int)((w.n_strips + 15) / 16);
+  const bool grp = !SWI && p.g.nm > 1;
+  const int nt = grp ? p.g.tbase[p.g.nm] : SWI ? (int)((p.w.pair + 7) / 8) : (int)((p.w.n_strips + 15) / 16);
   const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
   const int P = p.P;
   split_tile_of(nt, mtiles, P, tm, tn, piece);
+  const int tg = tn * mtiles + tm;  // split-K counter: the global tile
+  const int jm = grp ? group_member(p.g, tn) : 0;
+  const WeightView &w = grp ? p.g.wm[jm] : p.w;
+  void *const yout = grp ? p.g.ym[jm] : p.y;
+  if (grp) tn -= p.g.tbase[jm];
   const int m0 = tm * ROWS;
   int s0 = tn * 16 + wave * 4, slim = (int)w.n_strips, j0 = 0;
   if constexpr (SWI) swiglu_strips<16>(w, tn, wave, s0, slim, j0);
@@ -871,7 +903,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
     stage(wb[1], st + 3, std::integral_constant<int, 3>{});
   }
 
-  if (P > 1 && !split_fixup<MT, NQ>(p, acc, tn * mtiles + tm, piece, (int *)(lds + 2 * BUF))) return;
+  if (P > 1 && !split_fixup<MT, NQ>(p, acc, tg, piece, (int *)(lds + 2 * BUF))) return;
 
   if constexpr (SWI) {
     const int64_t I = w.pair * 16;
@@ -890,7 +922,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int64_t row = rb + 8 * (v / 4) + (v % 4);
-            if (row < p.M) store_out(p.y, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[v], up[v]));
+            if (row < p.M) store_out(yout, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[v], up[v]));
           }
         }
       }
@@ -909,7 +941,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int64_t rb = m0 + mt * 32 + 4 * h;
-        typename Y::T *py = (typename Y::T *)p.y + rb * ldy + col;
+        typename Y::T *py = (typename Y::T *)yout + rb * ldy + col;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int rr = 8 * (v / 4) + (v % 4);
@@ -946,12 +978,16 @@ struct Gemm32Plan {
   int64_t tiles;
   size_t part_bytes() const { return P > 1 ? (size_t)(tiles * P) * 32 * mt * 256 * sizeof(float) : 0; }
 };
-static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w) {
+// 256-column tiles of a weight (pairs of gate / up strip groups for SwiGLU).
+static int64_t gemm32_col_tiles(const WeightView &w) { return w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16; }
+
+// nt: column tiles of the launch (all members of a grouped one).
+static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt) {
   Gemm32Plan g;
   const bool small = M <= kGemm32SmallRows;
   g.mt = small ? 1 : (w.fmt == DIALQ_FORMAT_Q4_K ? GEMMQ4K_MT : GEMM32_MT);
   g.ks = small ? 2 : GEMM32_KS;  // byte formats; a Q4_K stage is one 64-k quarter chunk
-  const int64_t rows = 32 * g.mt, nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
+  const int64_t rows = 32 * g.mt;
   g.tiles = nt * ((M + rows - 1) / rows);
   g.P = 1;
   const int64_t occ = w.fmt == DIALQ_FORMAT_Q4_K ? GEMMQ4K_OCC : GEMM32_OCC;
@@ -980,11 +1016,41 @@ void gemm_workspace(int64_t M, const WeightView &w, int x_dtype, size_t &part_by
   part_bytes = 0;
   cnt_count = 0;
   if (!gemm32_applies(w, x_dtype) || M <= 0) return;
-  const Gemm32Plan g = gemm32_plan(M, w);
+  const Gemm32Plan g = gemm32_plan(M, w, gemm32_col_tiles(w));
   if (g.P > 1) {
     part_bytes = g.part_bytes();
     cnt_count = (size_t)g.tiles;
   }
+}
+
+// The member table of a grouped 32x32-kernel launch, or false where one does
+// not apply (a member the 32x32 kernels do not take, mixed formats or K,
+// SwiGLU, more than kGemmMaxGroup members).
+static bool gemm_group_table(const WeightView *ws, void *const *ys, int n, int x_dtype, GemmGroup &g) {
+  if (n < 2 || n > kGemmMaxGroup) return false;
+  g.nm = n;
+  g.tbase[0] = 0;
+  for (int j = 0; j < n; ++j) {
+    if (ws[j].fmt != ws[0].fmt || ws[j].K != ws[0].K || ws[j].pair || !gemm32_applies(ws[j], x_dtype)) return false;
+    g.wm[j] = ws[j];
+    g.ym[j] = ys ? ys[j] : nullptr;
+    g.tbase[j + 1] = g.tbase[j] + (int)gemm32_col_tiles(ws[j]);
+  }
+  for (int j = n; j < kGemmMaxGroup; ++j) g.tbase[j + 1] = g.tbase[n];
+  return true;
+}
+
+bool gemm_group_workspace(int64_t M, const WeightView *ws, int n, int x_dtype, size_t &part_bytes, size_t &cnt_count) {
+  part_bytes = 0;
+  cnt_count = 0;
+  GemmGroup g;
+  if (M <= 0 || !gemm_group_table(ws, nullptr, n, x_dtype, g)) return false;
+  const Gemm32Plan pl = gemm32_plan(M, ws[0], g.tbase[n]);
+  if (pl.P > 1) {
+    part_bytes = pl.part_bytes();
+    cnt_count = (size_t)pl.tiles;
+  }
+  return true;
 }
 
 template <int ACT, int MT>
@@ -1007,18 +1073,22 @@ static hipError_t gemm32_launch(const GemmParams &p, int64_t grid, hipStream_t s
   return hipGetLastError();
 }
 
+// grp: the member table of a grouped launch (null: the single weight w).
 template <int FMT, int ACT>
 static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype, float *part,
-                                size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st) {
+                                size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st,
+                                const GemmGroup *grp = nullptr) {
   typedef GemmShape<FMT, ACT> S;
   if ((int64_t)S::ROWS * w.K * ActTraits<ACT>::BYTES > 0xffffffffLL) return hipErrorInvalidValue;
   constexpr bool BYTE = FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW;
   constexpr bool Q4K = FMT == DIALQ_FORMAT_Q4_K && (ACT == DIALQ_BF16 || ACT == kActF16N);
   if constexpr (BYTE || Q4K) {
     if (gemm32_applies(w, ACT == DIALQ_F32 ? DIALQ_F32 : DIALQ_BF16)) {
-      const Gemm32Plan g = gemm32_plan(M, w);
+      const Gemm32Plan g = gemm32_plan(M, w, grp ? grp->tbase[grp->nm] : gemm32_col_tiles(w));
       if (g.P > 1 && ((size_t)g.tiles > cnt_count || g.part_bytes() > part_bytes)) return hipErrorInvalidValue;
-      const GemmParams p{w, x, y, M, y_dtype, g.P, part, cnt};
+      if (g.tiles * g.P > 0x7fffffffLL) return hipErrorInvalidValue;
+      GemmParams p{w, x, y, M, y_dtype, g.P, part, cnt};
+      if (grp) p.g = *grp;
       if constexpr (Q4K) {
         if (g.mt == 1) return gemm_q4k_launch<ACT, 1>(p, g.tiles * g.P, st);
         return gemm_q4k_launch<ACT, GEMMQ4K_MT>(p, g.tiles * g.P, st);
@@ -1028,6 +1098,7 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
       }
     }
   }
+  if (grp) return hipErrorNotSupported;
   static_assert(S::LDS_BYTES >= 8192, "the SwiGLU exchange reuses the staging LDS");
   const int64_t nt = w.pair ? (w.pair + 2 * S::NS - 1) / (2 * S::NS) : (w.n_strips + 4 * S::NS - 1) / (4 * S::NS);
   dim3 grid((unsigned)(nt * ((M + S::ROWS - 1) / S::ROWS)));
@@ -1039,18 +1110,44 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
 
 template <int FMT>
 static hipError_t gemm_act(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype,
-                           float *part, size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st) {
+                           float *part, size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st,
+                           const GemmGroup *grp = nullptr) {
   switch (x_dtype) {
-    case DIALQ_BF16: return gemm_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
+    case DIALQ_BF16:
+      return gemm_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st, grp);
     // f16 activations go to f16 MFMAs as they are, against f16 weight
     // operands; MXFP4's scaled codes need bf16's exponent range (hi / lo parts)
     case DIALQ_F16:
       return gemm_dispatch<FMT, FMT == DIALQ_FORMAT_MXFP4 ? DIALQ_F16 : kActF16N>(w, x, M, y, y_dtype, part,
-                                                                                 part_bytes, cnt, cnt_count, st);
-    case DIALQ_F32: return gemm_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
+                                                                                 part_bytes, cnt, cnt_count, st, grp);
+    case DIALQ_F32:
+      return gemm_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st, grp);
   }
   return hipErrorInvalidValue;
 }
+
+hipError_t launch_gemm_group(const WeightView *ws, void *const *ys, int n, const void *x, int x_dtype, int64_t M,
+                             int y_dtype, float *part, size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st) {
+  GemmGroup g;
+  if (!gemm_group_table(ws, ys, n, x_dtype, g)) return hipErrorNotSupported;
+  hipError_t r = hipErrorNotSupported;
+  switch (ws[0].fmt) {
+    case DIALQ_FORMAT_W8A16:
+      r = gemm_act<DIALQ_FORMAT_W8A16>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g);
+      break;
+    case DIALQ_FORMAT_FP8_ROW:
+      r = gemm_act<DIALQ_FORMAT_FP8_ROW>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st,
+                                         &g);
+      break;
+    case DIALQ_FORMAT_Q4_K:
+      r = gemm_act<DIALQ_FORMAT_Q4_K>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g);
+      break;
+  }
+  if (r == hipSuccess) g_prefill_grouped_launches.fetch_add(1, std::memory_order_relaxed);
+  return r;
+}
+
+int64_t gemm_grouped_launches() { return g_prefill_grouped_launches.load(std::memory_order_relaxed); }
 
 hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype, float *part,
                        size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st) {
@@ -1112,6 +1209,7 @@ struct NativeParams {
   int P;
   float *part;  // [tiles][P][kNativeAcc][256] partial tiles
   int *cnt;     // [tiles] arrivals per split tile; zero between launches
+  GemmGroup g;
 };
 
 template <bool FP8>
@@ -1161,12 +1259,12 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
   __shared__ uint32_t lds_s[2][256];  // MXFP4: the 4 E8M0 scales of a row's chunk (rows < ROWS)
   __shared__ int lds_last;
 
-  const WeightView &w = p.w;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
-  const int kc = (int)w.k_chunks;
-  const int nt = SWI ? (int)((w.pair + 7) / 8) : (int)((w.n_strips + 15) / 16);
+  const int kc = (int)p.w.k_chunks;
+  const bool grp = !SWI && p.g.nm > 1;
+  const int nt = grp ? p.g.tbase[p.g.nm] : SWI ? (int)((p.w.pair + 7) / 8) : (int)((p.w.n_strips + 15) / 16);
   const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
   // One workgroup per (tile, k piece).  P == 1: whole tiles in the
   // XCD-aware order of tile_of.  P > 1: each tile's chunks split evenly into
@@ -1184,7 +1282,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
     tn = u / (mtiles * P);
   }
   const int c0 = (int)((int64_t)piece * kc / P), c1 = (int)((int64_t)(piece + 1) * kc / P);
-  const int t = tn * mtiles + tm;  // counter index of a split tile
+  const int t = tn * mtiles + tm;  // counter index of a split tile (the global tile)
+  const int jm = grp ? group_member(p.g, tn) : 0;
+  const WeightView &w = grp ? p.g.wm[jm] : p.w;
+  void *const yout = grp ? p.g.ym[jm] : p.y;
+  if (grp) tn -= p.g.tbase[jm];
   const uint32_t pitch = (uint32_t)(FP8 ? p.k_pad : p.k_pad / 2);
   const rsrc_t rt = make_rsrc(w.tiles, (uint32_t)(w.n_strips * w.k_chunks * TILE));
   rsrc_t rb = rt;
@@ -1475,7 +1577,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
               const int64_t row = rbase + 8 * (e / 4) + (e % 4);
-              if (row < p.M) store_out(p.y, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[e], up[e]));
+              if (row < p.M) store_out(yout, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[e], up[e]));
             }
           }
         }
@@ -1494,7 +1596,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const int64_t rbase = m0 + mt * 32 + 4 * h;
-          typename Y::T *py = (typename Y::T *)p.y + rbase * ldy + col;
+          typename Y::T *py = (typename Y::T *)yout + rbase * ldy + col;
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int rr = 8 * (e / 4) + (e % 4);
@@ -1524,7 +1626,7 @@ static int native_pieces(int fmt, int occ, int64_t tiles, int64_t kc) {
 template <int FMT, int MT, int OCC, int DEPTH>
 static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M, int64_t k_pad,
                                 void *y, int y_dtype, float *part, size_t part_bytes, int *cnt, size_t cnt_count,
-                                hipStream_t st) {
+                                hipStream_t st, const GemmGroup *grp = nullptr) {
   constexpr int ROWS = 32 * MT;
   constexpr int64_t TILE = FMT == DIALQ_FORMAT_FP8_BLOCK ? 2048 : 1024;
   const int64_t pitch = FMT == DIALQ_FORMAT_FP8_BLOCK ? k_pad : k_pad / 2;
@@ -1533,13 +1635,17 @@ static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const vo
     return hipErrorInvalidValue;
   static_assert(2 * ROWS * ((FMT == DIALQ_FORMAT_FP8_BLOCK ? 128 : 64) + 16) >= 8192,
                 "the SwiGLU exchange reuses the staging LDS");
-  const int64_t nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
+  const int64_t nt = grp ? grp->tbase[grp->nm] : w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
+  if (grp)
+    for (int j = 0; j < grp->nm; ++j)
+      if (grp->wm[j].n_strips * grp->wm[j].k_chunks * TILE >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   const int64_t tiles = nt * ((M + ROWS - 1) / ROWS);
   const int P = native_pieces(FMT, OCC, tiles, w.k_chunks);
   if (tiles * P > 0x7fffffffLL) return hipErrorInvalidValue;
   if (P > 1 && ((size_t)tiles > cnt_count || (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) > part_bytes))
     return hipErrorInvalidValue;
   NativeParams p{w, xq, xs, M, k_pad, y, y_dtype, P, part, cnt};
+  if (grp) p.g = *grp;
   if (w.pair) k_gemm_native<FMT, MT, OCC, DEPTH, true><<<dim3((unsigned)(tiles * P)), 256, 0, st>>>(p);
   else k_gemm_native<FMT, MT, OCC, DEPTH, false><<<dim3((unsigned)(tiles * P)), 256, 0, st>>>(p);
   return hipGetLastError();
@@ -1553,6 +1659,54 @@ void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t
   const int P = native_pieces(w.fmt, occ, tiles, w.k_chunks);
   part_bytes = P > 1 ? (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) : 0;
   cnt_count = P > 1 ? (size_t)tiles : 0;
+}
+
+// The member table of a grouped native launch (FP8_BLOCK or MXFP4 members of
+// one format and K), or false.
+static bool native_group_table(const WeightView *ws, void *const *ys, int n, GemmGroup &g) {
+  if (n < 2 || n > kGemmMaxGroup) return false;
+  if (ws[0].fmt != DIALQ_FORMAT_FP8_BLOCK && ws[0].fmt != DIALQ_FORMAT_MXFP4) return false;
+  g.nm = n;
+  g.tbase[0] = 0;
+  for (int j = 0; j < n; ++j) {
+    if (ws[j].fmt != ws[0].fmt || ws[j].K != ws[0].K || ws[j].pair) return false;
+    g.wm[j] = ws[j];
+    g.ym[j] = ys ? ys[j] : nullptr;
+    g.tbase[j + 1] = g.tbase[j] + (int)((ws[j].n_strips + 15) / 16);
+  }
+  for (int j = n; j < kGemmMaxGroup; ++j) g.tbase[j + 1] = g.tbase[n];
+  return true;
+}
+
+bool native_group_workspace(int64_t M, const WeightView *ws, int n, size_t &part_bytes, size_t &cnt_count) {
+  part_bytes = 0;
+  cnt_count = 0;
+  GemmGroup g;
+  if (M <= 0 || !native_group_table(ws, nullptr, n, g)) return false;
+  const bool fp8 = ws[0].fmt == DIALQ_FORMAT_FP8_BLOCK;
+  const int occ = fp8 ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4, rows = 32 * (fp8 ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
+  const int64_t tiles = (int64_t)g.tbase[n] * ((M + rows - 1) / rows);
+  const int P = native_pieces(ws[0].fmt, occ, tiles, ws[0].k_chunks);
+  part_bytes = P > 1 ? (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) : 0;
+  cnt_count = P > 1 ? (size_t)tiles : 0;
+  return true;
+}
+
+hipError_t launch_gemm_native_group(const WeightView *ws, void *const *ys, int n, const uint8_t *xq, const void *xs,
+                                    int64_t M, int64_t k_pad, int y_dtype, float *part, size_t part_bytes, int *cnt,
+                                    size_t cnt_count, hipStream_t st) {
+  GemmGroup g;
+  if (!native_group_table(ws, ys, n, g)) return hipErrorNotSupported;
+  if (k_pad != ws[0].k_chunks * 128) return hipErrorInvalidValue;
+  hipError_t r;
+  if (ws[0].fmt == DIALQ_FORMAT_FP8_BLOCK)
+    r = native_launch<DIALQ_FORMAT_FP8_BLOCK, NATIVE_MT_FP8, NATIVE_OCC_FP8, NATIVE_DEPTH_FP8>(
+        ws[0], xq, xs, M, k_pad, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g);
+  else
+    r = native_launch<DIALQ_FORMAT_MXFP4, NATIVE_MT_FP4, NATIVE_OCC_FP4, NATIVE_DEPTH_FP4>(
+        ws[0], xq, xs, M, k_pad, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g);
+  if (r == hipSuccess) g_prefill_grouped_launches.fetch_add(1, std::memory_order_relaxed);
+  return r;
 }
 
 hipError_t launch_gemm_native(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M,

@@ -20,6 +20,9 @@ struct DequantArgs {
   int out_dtype;
 };
 
+// Weights one grouped prefill launch covers (members that share x and K).
+constexpr int kGemmMaxGroup = 4;
+
 // Everything a product kernel needs to read one resident weight.
 struct WeightView {
   int fmt;
@@ -92,6 +95,22 @@ int gemv_wait_limit();
 void gemm_workspace(int64_t M, const WeightView &w, int x_dtype, size_t &part_bytes, size_t &cnt_count);
 hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype, float *part,
                        size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st);
+// Grouped prefill over n (2..kGemmMaxGroup) weights of one format and K that
+// share x: one launch over all members' column tiles, member j writing
+// [M, N_j] through ys[j] with its view's output stride.  The 32x32 kernels
+// (W8A16, FP8_ROW; Q4_K with bf16 / f16 x) and the native kernel (FP8_BLOCK,
+// MXFP4 on x quantized once).  *_group_workspace returns false, and the
+// launchers hipErrorNotSupported (launching nothing), where no grouped
+// kernel applies; the caller then launches per member.
+bool gemm_group_workspace(int64_t M, const WeightView *ws, int n, int x_dtype, size_t &part_bytes, size_t &cnt_count);
+hipError_t launch_gemm_group(const WeightView *ws, void *const *ys, int n, const void *x, int x_dtype, int64_t M,
+                             int y_dtype, float *part, size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st);
+bool native_group_workspace(int64_t M, const WeightView *ws, int n, size_t &part_bytes, size_t &cnt_count);
+hipError_t launch_gemm_native_group(const WeightView *ws, void *const *ys, int n, const uint8_t *xq, const void *xs,
+                                    int64_t M, int64_t k_pad, int y_dtype, float *part, size_t part_bytes, int *cnt,
+                                    size_t cnt_count, hipStream_t st);
+// Grouped prefill launches made by this process (a test hook).
+int64_t gemm_grouped_launches();
 // Native low-precision prefill: FP8_BLOCK with per-token fp8 activations,
 // MXFP4 with per-32 MXFP4 activations.  `xq` / `xs` are the quantized
 // activations (codes and scales) produced by launch_act_*.  The stream-K

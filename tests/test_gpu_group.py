@@ -1,15 +1,16 @@
 """dialq_linear_forward_group: y = cat([x W_j^T], -1) for handles that share
 x, the replacement of QkvProjection::Split / MlpGateUpProjection::Split
 (qwen3_vl/text.rs:1093-1101, :451-455).  Paths that run one launch per
-member (prefill, mixed formats) must equal each member's own
-dialq_linear_forward_ex output bit for bit (the same kernels with a
-strided output).  A grouped decode launch sizes its k-split and its waves
-per strip from all the group's strips, so a member's f32 sum may be split
-differently than in its own launch: those columns must agree with its own
-forward to f32 rounding (rel-L2 <= 2e-4 in bf16) and with the oracle
-(<= 1e-3).  Covered: decode row counts, prefill row counts, mixed formats,
-more members than one launch takes, misaligned and host inputs, the full
-27B q / k / v and gate / up shapes."""
+member (mixed formats, prefill formats without a grouped kernel) must
+equal each member's own dialq_linear_forward_ex output bit for bit (the
+same kernels with a strided output).  A grouped launch -- decode, or
+prefill of W8A16 / FP8_ROW / Q4_K (bf16, f16 x) / FP8_BLOCK and MXFP4
+native -- sizes its split along K from all the group's tiles, so a
+member's f32 sum may be split differently than in its own launch: those
+columns must agree with its own forward to f32 rounding (rel-L2 <= 2e-4 in
+bf16) and with the oracle (<= 1e-3).  Covered: decode row counts, prefill
+row counts, mixed formats, more members than one launch takes, misaligned
+and host inputs, the full 27B q / k / v and gate / up shapes."""
 import numpy as np
 import pytest
 
@@ -65,16 +66,18 @@ def test_group_equals_separate(fmts, rows, torch_dev):
     ns = [384, 64, 64][:len(fmts)] if len(fmts) == 3 else [320, 320]
     lins, deqs = _members(fmts, ns, k, seed=11 * rows)
     x = O.round_bf16(np.random.default_rng(rows).normal(0, 1, (rows, k)).astype(np.float32))
-    grouped = rows <= 16 and len(set(fmts)) == 1  # decode path: one grouped launch
     for x_dtype in (dq.BF16, dq.F16, dq.F32):
+        # decode: one grouped launch per row group of 16 (8 for the k-quants
+        # at M <= 8); prefill: one launch where a grouped kernel exists
+        prefill_grouped = fmts[0] in (dq.W8A16, dq.MXFP4) or (fmts[0] == dq.Q4_K and x_dtype != dq.F32)
+        grouped = len(set(fmts)) == 1 and (rows <= 16 or prefill_grouped)
         xt = to_torch(x, x_dtype, torch_dev)
         want = _separate(lins, xt, dq.BF16, dq.PATH_AUTO, torch_dev)
         got = torch.full_like(want, float("nan"))
         before = dq.grouped_launches()
         dq.forward_group(lins, xt, got)
         torch.cuda.synchronize()
-        # one grouped launch per row group of 16 (8 for the k-quants at M <= 8)
-        assert (dq.grouped_launches() > before) == grouped, (rows, fmts)
+        assert (dq.grouped_launches() > before) == grouped, (rows, fmts, x_dtype)
         _agree(got, want, not grouped, (x_dtype, rows))
     # and against the weight-only oracle, where the product is weight-only
     # (MXFP4 above 16 rows takes the native path, which quantizes x too)
@@ -84,6 +87,8 @@ def test_group_equals_separate(fmts, rows, torch_dev):
 
 
 def test_group_native_prefill_and_output_dtypes(torch_dev):
+    # native: one grouped launch on x quantized once; weight-only FP8_BLOCK
+    # (k_gemm): one launch per member, bit for bit
     import torch
     k = 1024
     lins, _ = _members((dq.FP8_BLOCK, dq.FP8_BLOCK), (256, 128), k, seed=3)
@@ -93,9 +98,12 @@ def test_group_native_prefill_and_output_dtypes(torch_dev):
         for path in (dq.PATH_GEMM_NATIVE, dq.PATH_GEMM):
             want = _separate(lins, x, y_dtype, path, torch_dev)
             got = torch.full_like(want, float("nan"))
+            before = dq.grouped_launches()
             dq.forward_group(lins, x, got, path=path)
             torch.cuda.synchronize()
-            assert torch.equal(_bits(got), _bits(want)), (y_dtype, path)
+            grouped = path == dq.PATH_GEMM_NATIVE
+            assert (dq.grouped_launches() == before + 1) == grouped, (y_dtype, path)
+            _agree(got, want, not grouped, (y_dtype, path))
 
 
 def test_group_of_more_members_than_one_launch(torch_dev):
@@ -167,3 +175,36 @@ def test_group_27b_shapes(group, fmt, torch_dev):
         if rows == 1:  # the benchmark's decode: must be one grouped launch
             assert dq.grouped_launches() == before + 1
         _agree(got, want, False, rows)
+
+
+@pytest.mark.parametrize("group", [[6144, 1024, 1024], [17408, 17408]], ids=["qkv", "gate_up"])
+@pytest.mark.parametrize("fmt,x_dtype,path", [(dq.W8A16, dq.BF16, dq.PATH_GEMM), (dq.FP8_ROW, dq.BF16, dq.PATH_GEMM),
+                                              (dq.Q4_K, dq.F16, dq.PATH_GEMM), (dq.Q4_K, dq.BF16, dq.PATH_GEMM),
+                                              (dq.FP8_BLOCK, dq.BF16, dq.PATH_GEMM_NATIVE),
+                                              (dq.MXFP4, dq.BF16, dq.PATH_GEMM_NATIVE)],
+                         ids=["w8a16", "fp8_row", "q4_k_f16", "q4_k_bf16", "fp8_block", "mxfp4"])
+def test_group_prefill_27b_shapes(group, fmt, x_dtype, path, torch_dev):
+    # prefill of DIAL's split projections: one grouped launch over every
+    # member's column tiles (small and large row counts: split along K or
+    # not), each member within f32 rounding of its own forward
+    import torch
+    k = 5120
+    g = torch.Generator(device=torch_dev).manual_seed(17)
+    lins = []
+    for n in group:
+        if fmt == dq.FP8_ROW:
+            raw, scales, kw, _ = make_weight(dq.FP8_ROW, n, k, seed=n)
+            lins.append(dq.Linear.create(dq.FP8_ROW, n, k, raw, scales, **kw))
+        else:
+            lins.append(dq.Linear.quantize(fmt, torch.randn(n, k, device=torch_dev, generator=g) * 0.02,
+                                           scale_dtype=dq.BF16))
+    tdt = torch.float16 if x_dtype == dq.F16 else torch.bfloat16
+    for rows in (40, 300):
+        x = torch.randn(rows, k, device=torch_dev, generator=g).to(tdt)
+        want = _separate(lins, x, x_dtype, path, torch_dev)
+        got = torch.full_like(want, float("nan"))
+        before = dq.grouped_launches()
+        dq.forward_group(lins, x, got, path=path)
+        torch.cuda.synchronize()
+        assert dq.grouped_launches() == before + 1, rows
+        _agree(got, want, False, (rows, path))
