@@ -971,6 +971,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
 // (<= 4 pieces; the 17408-row gate at 128 rows, 136 tiles, is faster whole),
 // and never past kGemm32MaxPartBytes of partials.
 constexpr int64_t kGemm32SmallRows = 96;
+// W8A16 / FP8_ROW from this many rows: 128-row tiles at 2 workgroups per CU
+// (gate 17408x5120 at M = 2048: 961 against 883 TFLOP/s with 64-row tiles at
+// 3 per CU; at M = 1024 the 544 tiles of 128 rows leave most of a second
+// round of 512 slots idle and lose, 763 against 842)
+constexpr int64_t kGemm32TallRows = 2048;
 constexpr int kGemm32MinChunks = 20;  // 64-k steps per split-K piece, at least
 constexpr size_t kGemm32MaxPartBytes = (size_t)31 << 20;
 struct Gemm32Plan {
@@ -985,12 +990,12 @@ static int64_t gemm32_col_tiles(const WeightView &w) { return w.pair ? (w.pair +
 static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt) {
   Gemm32Plan g;
   const bool small = M <= kGemm32SmallRows;
-  g.mt = small ? 1 : (w.fmt == DIALQ_FORMAT_Q4_K ? GEMMQ4K_MT : GEMM32_MT);
+  g.mt = small ? 1 : w.fmt == DIALQ_FORMAT_Q4_K ? GEMMQ4K_MT : M >= kGemm32TallRows ? 4 : GEMM32_MT;
   g.ks = small ? 2 : GEMM32_KS;  // byte formats; a Q4_K stage is one 64-k quarter chunk
   const int64_t rows = 32 * g.mt;
   g.tiles = nt * ((M + rows - 1) / rows);
   g.P = 1;
-  const int64_t occ = w.fmt == DIALQ_FORMAT_Q4_K ? GEMMQ4K_OCC : GEMM32_OCC;
+  const int64_t occ = w.fmt == DIALQ_FORMAT_Q4_K ? GEMMQ4K_OCC : g.mt == 4 ? 2 : GEMM32_OCC;
   const int64_t cus = device_cus(), slots = occ * cus;
   if (small ? g.tiles * 2 <= slots : g.tiles * 2 < cus) {
     const int64_t steps = w.k_chunks * (w.fmt == DIALQ_FORMAT_Q4_K ? 4 : 1);
@@ -1063,13 +1068,13 @@ static hipError_t gemm_q4k_launch(const GemmParams &p, int64_t grid, hipStream_t
   return hipGetLastError();
 }
 
-template <int FMT, int ACT, int MT, int KS>
+template <int FMT, int ACT, int MT, int KS, int OCC = GEMM32_OCC>
 static hipError_t gemm32_launch(const GemmParams &p, int64_t grid, hipStream_t st) {
   constexpr int BUF = ActTraits<ACT>::PARTS * 32 * MT * (KS * 64 + 8);
   static_assert(2 * BUF * 2 >= 8192, "the SwiGLU exchange reuses the staging LDS");
   const size_t lds_bytes = 2 * BUF * 2 + 16;  // two staging buffers and the split-K arrival flag
-  if (p.w.pair) k_gemm32<FMT, ACT, MT, KS, GEMM32_OCC, true><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
-  else k_gemm32<FMT, ACT, MT, KS, GEMM32_OCC, false><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
+  if (p.w.pair) k_gemm32<FMT, ACT, MT, KS, OCC, true><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
+  else k_gemm32<FMT, ACT, MT, KS, OCC, false><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
   return hipGetLastError();
 }
 
@@ -1094,6 +1099,7 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
         return gemm_q4k_launch<ACT, GEMMQ4K_MT>(p, g.tiles * g.P, st);
       } else {
         if (g.mt == 1) return gemm32_launch<FMT, ACT, 1, 2>(p, g.tiles * g.P, st);
+        if (g.mt == 4) return gemm32_launch<FMT, ACT, 4, 1, 2>(p, g.tiles * g.P, st);
         return gemm32_launch<FMT, ACT, GEMM32_MT, GEMM32_KS>(p, g.tiles * g.P, st);
       }
     }
@@ -1207,7 +1213,7 @@ struct NativeParams {
   int y_dtype;
   // Split-K: P pieces per tile (1: whole tiles, no partials).
   int P;
-  float *part;  // [tiles][P][kNativeAcc][256] partial tiles
+  float *part;  // [tiles][P][32 MT][256] partial tiles
   int *cnt;     // [tiles] arrivals per split tile; zero between launches
   GemmGroup g;
 };
@@ -1225,10 +1231,10 @@ __device__ __forceinline__ f32x16 mfma_scaled32(i32x8 a, i32x8 b, f32x16 c, int 
 #define NATIVE_OCC_FP8 2  // workgroups per CU the FP8_BLOCK kernel is built for
 #endif
 #ifndef NATIVE_MT_FP4
-#define NATIVE_MT_FP4 2
+#define NATIVE_MT_FP4 4
 #endif
 #ifndef NATIVE_OCC_FP4
-#define NATIVE_OCC_FP4 3
+#define NATIVE_OCC_FP4 2
 #endif
 #ifndef NATIVE_DEPTH_FP8
 #define NATIVE_DEPTH_FP8 2  // chunks of weights and activations in flight per wave (register ring slots)
@@ -1237,7 +1243,8 @@ __device__ __forceinline__ f32x16 mfma_scaled32(i32x8 a, i32x8 b, f32x16 c, int 
 #define NATIVE_DEPTH_FP4 2
 #endif
 
-constexpr int kNativeAcc = 64;       // f32 accumulators per thread (MT = 2: 2 x 2 tiles x 16)
+// f32 accumulators per thread of the native kernel: MT x 2 tiles x 16
+constexpr int native_acc(int fmt) { return 32 * (fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_MT_FP8 : NATIVE_MT_FP4); }
 // Fewest k chunks per piece of a split tile: a piece's partial (64 KB out,
 // read back by the last piece) must be worth the extra parallelism; fp4
 // chunks take half the MFMA time of fp8 ones (measured: MXFP4 k/v and q/o
@@ -1252,7 +1259,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
   constexpr int ROWS = 32 * MT, ABUF = ROWS * STRIDE;
   constexpr int NPIECE = ROWS * ROWB / 16, PIECES = (NPIECE + 255) / 256;
   static_assert(NPIECE % 256 == 0, "activation pieces must fill the workgroup");
-  static_assert(MT * 2 * 16 == kNativeAcc, "partial slots hold MT x 2 tiles of 16 values per thread");
+  constexpr int ACC = MT * 2 * 16;  // accumulators per thread: MT x 2 tiles of 16
   constexpr int TILE = FP8 ? 2048 : 1024;  // resident tile bytes
   constexpr int BW = FP8 ? 2 : 1;          // 16-byte loads per lane and B operand
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * ABUF];
@@ -1495,7 +1502,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
       if (c + slot < c1) chunk(slot, c + slot);
 
     // The segment's sum over its chunks, without the per-token factor.
-    float sum[kNativeAcc];
+    float sum[ACC];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -1509,18 +1516,18 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
       // in; the last to arrive adds the P partials in piece order -- the
       // same order whichever piece is last, so the result does not depend
       // on timing -- writes the tile and re-arms the counter.
-      float *mine = p.part + ((size_t)t * P + piece) * (kNativeAcc * 256);
+      float *mine = p.part + ((size_t)t * P + piece) * (ACC * 256);
 #pragma unroll
-      for (int e = 0; e < kNativeAcc; ++e)
+      for (int e = 0; e < ACC; ++e)
         __hip_atomic_store(&mine[e * 256 + tid], sum[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();  // every wave's partial stores are complete
       if (tid == 0) lds_last = __hip_atomic_fetch_add(&p.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1;
       __syncthreads();
       if (!lds_last) return;
-      const rsrc_t rp = make_rsrc(p.part, (uint32_t)((size_t)nt * mtiles * P * kNativeAcc * 256 * 4));
+      const rsrc_t rp = make_rsrc(p.part, (uint32_t)((size_t)nt * mtiles * P * ACC * 256 * 4));
 #pragma unroll
-      for (int eb = 0; eb < kNativeAcc; eb += 16) {  // 16 values at a time keeps registers in check
+      for (int eb = 0; eb < ACC; eb += 16) {  // 16 values at a time keeps registers in check
         float tot[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) tot[e] = 0.0f;
@@ -1530,7 +1537,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
             for (int e = 0; e < 16; ++e) tot[e] += sum[eb + e];
             continue;
           }
-          const uint32_t base_off = (uint32_t)(((size_t)t * P + u) * (kNativeAcc * 256) + tid) * 4u;
+          const uint32_t base_off = (uint32_t)(((size_t)t * P + u) * (ACC * 256) + tid) * 4u;
           float pv[16];
 #pragma unroll
           for (int e = 0; e < 16; ++e)
@@ -1620,6 +1627,8 @@ static int native_pieces(int fmt, int occ, int64_t tiles, int64_t kc) {
   int64_t P = tiles >= slots ? 1 : slots / tiles;
   const int64_t cap = kc / native_min_chunks(fmt);
   if (P > cap) P = cap;
+  // partials of at most kGemm32MaxPartBytes, as the 32x32 kernels
+  while (P > 1 && (size_t)(tiles * P) * native_acc(fmt) * 256 * sizeof(float) > kGemm32MaxPartBytes) --P;
   return (int)(P < 1 ? 1 : P);
 }
 
@@ -1642,7 +1651,7 @@ static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const vo
   const int64_t tiles = nt * ((M + ROWS - 1) / ROWS);
   const int P = native_pieces(FMT, OCC, tiles, w.k_chunks);
   if (tiles * P > 0x7fffffffLL) return hipErrorInvalidValue;
-  if (P > 1 && ((size_t)tiles > cnt_count || (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) > part_bytes))
+  if (P > 1 && ((size_t)tiles > cnt_count || (size_t)(tiles * P) * (32 * MT) * 256 * sizeof(float) > part_bytes))
     return hipErrorInvalidValue;
   NativeParams p{w, xq, xs, M, k_pad, y, y_dtype, P, part, cnt};
   if (grp) p.g = *grp;
@@ -1657,7 +1666,7 @@ void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t
   const int64_t nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
   const int64_t tiles = nt * ((M + rows - 1) / rows);
   const int P = native_pieces(w.fmt, occ, tiles, w.k_chunks);
-  part_bytes = P > 1 ? (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) : 0;
+  part_bytes = P > 1 ? (size_t)(tiles * P) * native_acc(w.fmt) * 256 * sizeof(float) : 0;
   cnt_count = P > 1 ? (size_t)tiles : 0;
 }
 
@@ -1687,7 +1696,7 @@ bool native_group_workspace(int64_t M, const WeightView *ws, int n, size_t &part
   const int occ = fp8 ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4, rows = 32 * (fp8 ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
   const int64_t tiles = (int64_t)g.tbase[n] * ((M + rows - 1) / rows);
   const int P = native_pieces(ws[0].fmt, occ, tiles, ws[0].k_chunks);
-  part_bytes = P > 1 ? (size_t)(tiles * P) * kNativeAcc * 256 * sizeof(float) : 0;
+  part_bytes = P > 1 ? (size_t)(tiles * P) * native_acc(ws[0].fmt) * 256 * sizeof(float) : 0;
   cnt_count = P > 1 ? (size_t)tiles : 0;
   return true;
 }

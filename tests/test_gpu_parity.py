@@ -440,3 +440,23 @@ def test_resident_bytes_reference_formulas(torch_dev):
     assert lin.resident_bytes() == 48 * 64 + 48 * 4
     lin, _, _, _ = _linear(dq.W8A16, 48, 64, scale_dtype=dq.F32)
     assert lin.resident_bytes() == 48 * 64 + 48 * 4
+
+
+@pytest.mark.parametrize("fmt", [dq.W8A16, dq.FP8_ROW], ids=["w8a16", "fp8_row"])
+def test_gemm_tall_tiles(fmt, torch_dev):
+    # from 2048 rows the byte formats take 128-row tiles: ragged row blocks,
+    # every activation dtype, the SwiGLU epilogue
+    import torch
+    n, k = 320, 512
+    lin, _, _, deq = _linear(fmt, n, k, seed=60 + fmt)
+    for m, x_dtype, y_dtype, tol in ((2048, dq.BF16, dq.BF16, TOL_BF16), (2100, dq.F16, dq.F16, TOL_BF16),
+                                     (2049, dq.F32, dq.F32, 1e-5), (2300, dq.BF16, dq.F32, 1e-5)):
+        rel = _run(lin, deq, m, x_dtype, y_dtype, dq.PATH_GEMM, torch_dev, seed=m)
+        assert rel <= tol, (m, x_dtype, rel)
+    gu, _, _, gdeq = _linear(fmt, 256, k, seed=70 + fmt)
+    x = np.random.default_rng(5).normal(0, 1, (2050, k)).astype(np.float32)
+    y = torch.empty(2050, 128, device=torch_dev, dtype=torch.float32)
+    gu.forward_swiglu(to_torch(x, dq.BF16, torch_dev), y, path=dq.PATH_GEMM)
+    torch.cuda.synchronize()
+    want = O.swiglu(O.matmul_f64(exact_inputs(x, dq.BF16), gdeq))
+    assert O.rel_l2(y.cpu().numpy(), want) <= 1e-5
