@@ -177,11 +177,17 @@ int dialq_linear_forward_ex(void *linear, const void *x, int32_t x_dtype,
  * projections the GGUF worker builds (text.rs:1387-1425).  All handles must
  * have the same in_dim and device.  The decode path runs the strips of up
  * to four consecutive same-format members in one launch (x staged once per
- * workgroup, one launch's fill and drain instead of one per member); other
- * cases run one launch per member, each writing its columns of y, with the
- * same kernels and results as dialq_linear_forward_ex per member.  Other
- * arguments as dialq_linear_forward_ex (x at any address; y aligned to its
- * element size; per-handle scratch grows outside stream capture only). */
+ * workgroup, one launch's fill and drain instead of one per member); the
+ * prefill paths run the column tiles of up to four consecutive same-format
+ * members in one GEMM launch (W8A16, FP8_ROW, Q4_K with bf16 / f16 x;
+ * FP8_BLOCK and MXFP4 native on x quantized once; the first member's
+ * scratch serves the launch).  A grouped launch splits its sums along K
+ * from the group's tile count, so a member may differ from its own forward
+ * by f32 rounding.  Other cases run one launch per member, each writing
+ * its columns of y, with the same kernels and results as
+ * dialq_linear_forward_ex per member.  Other arguments as
+ * dialq_linear_forward_ex (x at any address; y aligned to its element
+ * size; per-handle scratch grows outside stream capture only). */
 int dialq_linear_forward_group(void *const *linears, int32_t n, const void *x,
                                int32_t x_dtype, int64_t rows, void *y,
                                int32_t y_dtype, int32_t path, void *stream,
@@ -293,9 +299,9 @@ int dialq_local_q8_forward(void *linear, const void *x, int32_t x_dtype,
 void dialq_debug_set_wait_limit(int64_t polls);
 
 /* Test hook; no counterpart in the reference.  The number of grouped decode
- * launches (dialq_linear_forward_group members run as one kernel) this
- * process has made, so that tests can tell a grouped launch from the
- * per-member fallback, whose outputs are the same to rounding. */
+ * and prefill launches (dialq_linear_forward_group members run as one
+ * kernel) this process has made, so that tests can tell a grouped launch
+ * from the per-member fallback, whose outputs are the same to rounding. */
 int64_t dialq_debug_grouped_launches(void);
 
 #ifdef __cplusplus
