@@ -329,7 +329,7 @@ def forward_group(linears, x, y, rows=None, *, path=PATH_AUTO, stream=None, x_dt
 
 
 def grouped_launches():
-    """Test hook (dialq_debug_grouped_launches): grouped decode launches so far."""
+    """Test hook (dialq_debug_grouped_launches): grouped decode and prefill launches so far."""
     return int(lib.dialq_debug_grouped_launches())
 
 
