@@ -311,7 +311,15 @@ struct ForwardPlan {
   size_t xscale = 0;           // native: activation scales
   size_t part = 0;             // native: split-K partial tiles
   size_t ncnt = 0;             // native: split-K tile counters (ints)
+  size_t xh = 0;               // Q4_K GEMM on bf16 x: its f16 copy, then the row scales
 };
+
+// Bytes of the f16 copy of a bf16 x (and its row scales) that the Q4_K
+// prefill kernel multiplies; 0 where that path does not apply.
+size_t q4k_f16_stage_bytes(const Linear *L, int x_dtype, int64_t rows, int path) {
+  if (path != DIALQ_PATH_GEMM || L->desc.format != DIALQ_FORMAT_Q4_K || x_dtype != DIALQ_BF16) return 0;
+  return (size_t)(rows * L->desc.in_dim * 2 + 255) / 256 * 256 + (size_t)rows * sizeof(float);
+}
 
 // Where a call's scratch lives: the handle's own buffers, grown on demand,
 // or the allocation-free entry point's static array.  Counters are zero
@@ -326,7 +334,18 @@ struct ForwardBufs {
   size_t part_bytes = 0;
   int *ncnt = nullptr;
   size_t ncnt_count = 0;
+  uint8_t *xh = nullptr;  // f16 copy of a bf16 x, then its row scales (plan.xh bytes)
 };
+
+// A bf16 x of a Q4_K prefill as f16 rows in range (k_x_f16_rows): returns the
+// row scales the GEMM's epilogue multiplies by; `xf` becomes the f16 copy.
+const float *stage_q4k_f16(const void *x, int64_t rows, int64_t K, uint8_t *buf, const void *&xf, hipStream_t st) {
+  uint16_t *xh = (uint16_t *)buf;
+  float *rs = (float *)(buf + (size_t)(rows * K * 2 + 255) / 256 * 256);
+  hip_check(launch_x_f16_rows(x, rows, K, xh, rs, st), "bf16 -> f16 activation rows");
+  xf = xh;
+  return rs;
+}
 
 WeightView forward_view(const Linear *L, bool swiglu) {
   WeightView w = L->view();
@@ -334,7 +353,10 @@ WeightView forward_view(const Linear *L, bool swiglu) {
   return w;
 }
 
-ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int64_t rows, int path) {
+// stage_f16: a Q4_K GEMM on bf16 x runs the f16 kernel on an f16 copy of x
+// (false: the bf16 hi / lo kernel, no copy).
+ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int64_t rows, int path,
+                         bool stage_f16 = true) {
   const int fmt = L->desc.format;
   ForwardPlan pl;
   if (path == DIALQ_PATH_AUTO) {
@@ -364,7 +386,9 @@ ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int6
     pl.xscale = fmt == DIALQ_FORMAT_FP8_BLOCK ? (size_t)rows * sizeof(float) : (size_t)(rows * pl.k_pad / 32);
     native_workspace(rows, w, pl.part, pl.ncnt);
   } else if (path == DIALQ_PATH_GEMM) {
-    gemm_workspace(rows, w, x_dtype, pl.part, pl.ncnt);  // split-K partials of few-tile launches
+    if (stage_f16) pl.xh = q4k_f16_stage_bytes(L, x_dtype, rows, path);
+    // split-K partials of few-tile launches (the f16 kernel's tiling when x is staged as f16)
+    gemm_workspace(rows, w, pl.xh ? DIALQ_F16 : x_dtype, pl.part, pl.ncnt);
   } else {
     fail("unknown path %d", path);
   }
@@ -377,7 +401,10 @@ void launch_forward(const Linear *L, const WeightView &w, const ForwardPlan &pl,
     hip_check(launch_gemv(w, x, x_dtype, rows, y, y_dtype, b.gemv_ws, b.gemv_ws_bytes, b.gemv_cnt, L->gave_up.d, st),
               "GEMV launch");
   } else if (pl.path == DIALQ_PATH_GEMM) {
-    hip_check(launch_gemm(w, x, x_dtype, rows, y, y_dtype, b.part, b.part_bytes, b.ncnt, b.ncnt_count, st),
+    const void *xf = x;
+    const float *yrow = b.xh ? stage_q4k_f16(x, rows, w.K, b.xh, xf, st) : nullptr;
+    hip_check(launch_gemm(w, xf, b.xh ? DIALQ_F16 : x_dtype, rows, y, y_dtype, b.part, b.part_bytes, b.ncnt,
+                          b.ncnt_count, st, yrow),
               "GEMM launch");
   } else {
     if (L->desc.format == DIALQ_FORMAT_FP8_BLOCK)
@@ -410,6 +437,9 @@ void run_forward(Linear *L, const WeightView &w, const void *x, int x_dtype, int
       ensure_scratch(L, pl.codes + pl.xscale, st);
       b.codes = (uint8_t *)L->act_scratch.p;
       b.xscale = b.codes + pl.codes;
+    } else if (pl.xh) {
+      ensure_scratch(L, pl.xh, st);
+      b.xh = (uint8_t *)L->act_scratch.p;
     }
     // split-K partials and tile counters (native prefill, or a GEMM of few tiles)
     ensure_native_scratch(L, pl.part, pl.ncnt, st);
@@ -509,11 +539,20 @@ bool run_prefill_group(Linear *const *Ls, const WeightView *ws, void *const *ys,
   Linear *L = Ls[0];
   size_t part = 0, ncnt = 0;
   if (path == DIALQ_PATH_GEMM) {
-    if (!gemm_group_workspace(rows, ws, n, x_dtype, part, ncnt)) return false;
+    const size_t xh = q4k_f16_stage_bytes(L, x_dtype, rows, path);  // bf16 x of a Q4_K group: f16 once
+    const int kx = xh ? DIALQ_F16 : x_dtype;
+    if (!gemm_group_workspace(rows, ws, n, kx, part, ncnt)) return false;
     std::lock_guard<std::mutex> lock(L->scratch_mu);
     ensure_native_scratch(L, part, ncnt, st);
-    const hipError_t r = launch_gemm_group(ws, ys, n, x, x_dtype, rows, y_dtype, (float *)L->native_part.p,
-                                           L->native_part.n, (int *)L->native_cnt.p, L->native_cnt.n / sizeof(int), st);
+    const void *xf = x;
+    const float *yrow = nullptr;
+    if (xh) {
+      ensure_scratch(L, xh, st);
+      yrow = stage_q4k_f16(x, rows, ws[0].K, (uint8_t *)L->act_scratch.p, xf, st);
+    }
+    const hipError_t r = launch_gemm_group(ws, ys, n, xf, kx, rows, y_dtype, (float *)L->native_part.p,
+                                           L->native_part.n, (int *)L->native_cnt.p, L->native_cnt.n / sizeof(int), st,
+                                           yrow);
     if (r == hipErrorNotSupported) return false;
     hip_check(r, "grouped GEMM launch");
     return true;
@@ -696,14 +735,21 @@ void forward_noalloc_impl(Linear *L, const void *x, int32_t x_dtype, int64_t row
   }
   const int64_t K = L->desc.in_dim;
   const WeightView w = forward_view(L, false);
-  const ForwardPlan pl = plan_forward(L, w, x_dtype, rows, path);
+  auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+  const size_t xbytes = (size_t)(rows * K) * xs;
+  const bool stage_x = ((uintptr_t)x) & 15u;
+  ForwardPlan pl = plan_forward(L, w, x_dtype, rows, path);
+  // a Q4_K prefill on bf16 x whose f16 copy does not fit runs the bf16 hi / lo
+  // kernel on x as it is
+  if (pl.xh && kNoAllocCntBytes + up(pl.codes + pl.xscale) + up(pl.part) + up(pl.xh) +
+                       (stage_x ? up(xbytes) : 0) > kNoAllocScratchBytes)
+    pl = plan_forward(L, w, x_dtype, rows, path, false);
   const size_t cnt_ints = pl.path == DIALQ_PATH_GEMV ? pl.gemv_cnt : pl.ncnt;
   if (cnt_ints * sizeof(int) > kNoAllocCntBytes)
     fail("dialq_linear_forward_noalloc: this %s weight needs %zu counters; its scratch holds %zu (out_dim up to "
          "%zu rows for the decode path)", format_name(L->desc.format), cnt_ints, kNoAllocCntBytes / sizeof(int),
          (kNoAllocCntBytes / sizeof(int) - 2) * 16);
   // regions after the counters, 256-byte aligned
-  auto up = [](size_t v) { return (v + 255) / 256 * 256; };
   size_t off = kNoAllocCntBytes;
   ForwardBufs b;
   if (pl.path == DIALQ_PATH_GEMV) {
@@ -722,10 +768,12 @@ void forward_noalloc_impl(Linear *L, const void *x, int32_t x_dtype, int64_t row
     off += up(pl.part);
     b.ncnt = pl.ncnt ? (int *)base : nullptr;
     b.ncnt_count = pl.ncnt;
+    if (pl.xh) {
+      b.xh = base + off;
+      off += up(pl.xh);
+    }
   }
   const void *xp = x;
-  const size_t xbytes = (size_t)(rows * K) * xs;
-  const bool stage_x = ((uintptr_t)x) & 15u;
   const size_t need = off + (stage_x ? up(xbytes) : 0);
   if (need > kNoAllocScratchBytes)
     fail("dialq_linear_forward_noalloc: %lld rows of this %s [%lld, %lld] weight need %zu bytes of scratch; the "

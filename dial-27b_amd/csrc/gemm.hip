@@ -56,6 +56,9 @@ struct GemmParams {
   float *part = nullptr;
   int *cnt = nullptr;
   GemmGroup g;  // k_gemm32, k_gemm_q4k
+  // k_gemm_q4k: per-row output multipliers (bf16 activations scaled into f16
+  // range, 2^e per row); null = 1
+  const float *yrow = nullptr;
 };
 
 template <int FMT, int ACT>
@@ -922,7 +925,10 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int64_t row = rb + 8 * (v / 4) + (v % 4);
-            if (row < p.M) store_out(yout, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[v], up[v]));
+            if (row < p.M) {
+              const float f = p.yrow ? p.yrow[row] : 1.0f;
+              store_out(yout, row * out_ld(w) + j, p.y_dtype, silu_mul(mine[v] * f, up[v] * f));
+            }
           }
         }
       }
@@ -945,7 +951,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int rr = 8 * (v / 4) + (v % 4);
-          if (!CHK || rb + rr < p.M) py[rr * ldy] = Y::conv(acc[mt][q][v]);
+          if (!CHK || rb + rr < p.M) py[rr * ldy] = Y::conv(p.yrow ? acc[mt][q][v] * p.yrow[rb + rr] : acc[mt][q][v]);
         }
       }
     }
@@ -1082,7 +1088,7 @@ static hipError_t gemm32_launch(const GemmParams &p, int64_t grid, hipStream_t s
 template <int FMT, int ACT>
 static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, void *y, int y_dtype, float *part,
                                 size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st,
-                                const GemmGroup *grp = nullptr) {
+                                const GemmGroup *grp = nullptr, const float *yrow = nullptr) {
   typedef GemmShape<FMT, ACT> S;
   if ((int64_t)S::ROWS * w.K * ActTraits<ACT>::BYTES > 0xffffffffLL) return hipErrorInvalidValue;
   constexpr bool BYTE = FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW;
@@ -1094,6 +1100,8 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
       if (g.tiles * g.P > 0x7fffffffLL) return hipErrorInvalidValue;
       GemmParams p{w, x, y, M, y_dtype, g.P, part, cnt};
       if (grp) p.g = *grp;
+      p.yrow = yrow;
+      if (yrow && !Q4K) return hipErrorInvalidValue;
       if constexpr (Q4K) {
         if (g.mt == 1) return gemm_q4k_launch<ACT, 1>(p, g.tiles * g.P, st);
         return gemm_q4k_launch<ACT, GEMMQ4K_MT>(p, g.tiles * g.P, st);
@@ -1105,6 +1113,7 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
     }
   }
   if (grp) return hipErrorNotSupported;
+  if (yrow) return hipErrorInvalidValue;
   static_assert(S::LDS_BYTES >= 8192, "the SwiGLU exchange reuses the staging LDS");
   const int64_t nt = w.pair ? (w.pair + 2 * S::NS - 1) / (2 * S::NS) : (w.n_strips + 4 * S::NS - 1) / (4 * S::NS);
   dim3 grid((unsigned)(nt * ((M + S::ROWS - 1) / S::ROWS)));
@@ -1117,36 +1126,39 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
 template <int FMT>
 static hipError_t gemm_act(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype,
                            float *part, size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st,
-                           const GemmGroup *grp = nullptr) {
+                           const GemmGroup *grp = nullptr, const float *yrow = nullptr) {
   switch (x_dtype) {
     case DIALQ_BF16:
-      return gemm_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st, grp);
+      return gemm_dispatch<FMT, DIALQ_BF16>(w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st, grp, yrow);
     // f16 activations go to f16 MFMAs as they are, against f16 weight
     // operands; MXFP4's scaled codes need bf16's exponent range (hi / lo parts)
     case DIALQ_F16:
-      return gemm_dispatch<FMT, FMT == DIALQ_FORMAT_MXFP4 ? DIALQ_F16 : kActF16N>(w, x, M, y, y_dtype, part,
-                                                                                 part_bytes, cnt, cnt_count, st, grp);
+      return gemm_dispatch<FMT, FMT == DIALQ_FORMAT_MXFP4 ? DIALQ_F16 : kActF16N>(
+          w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st, grp, yrow);
     case DIALQ_F32:
-      return gemm_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st, grp);
+      return gemm_dispatch<FMT, DIALQ_F32>(w, x, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st, grp, yrow);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm_group(const WeightView *ws, void *const *ys, int n, const void *x, int x_dtype, int64_t M,
-                             int y_dtype, float *part, size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st) {
+                             int y_dtype, float *part, size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st,
+                             const float *yrow) {
   GemmGroup g;
   if (!gemm_group_table(ws, ys, n, x_dtype, g)) return hipErrorNotSupported;
   hipError_t r = hipErrorNotSupported;
   switch (ws[0].fmt) {
     case DIALQ_FORMAT_W8A16:
-      r = gemm_act<DIALQ_FORMAT_W8A16>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g);
+      r = gemm_act<DIALQ_FORMAT_W8A16>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g,
+                                       yrow);
       break;
     case DIALQ_FORMAT_FP8_ROW:
       r = gemm_act<DIALQ_FORMAT_FP8_ROW>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st,
-                                         &g);
+                                         &g, yrow);
       break;
     case DIALQ_FORMAT_Q4_K:
-      r = gemm_act<DIALQ_FORMAT_Q4_K>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g);
+      r = gemm_act<DIALQ_FORMAT_Q4_K>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g,
+                                      yrow);
       break;
   }
   if (r == hipSuccess) g_prefill_grouped_launches.fetch_add(1, std::memory_order_relaxed);
@@ -1156,9 +1168,9 @@ hipError_t launch_gemm_group(const WeightView *ws, void *const *ys, int n, const
 int64_t gemm_grouped_launches() { return g_prefill_grouped_launches.load(std::memory_order_relaxed); }
 
 hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype, float *part,
-                       size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st) {
+                       size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st, const float *yrow) {
 #define DIALQ_GEMM_FMT(F) \
-  case F: return gemm_act<F>(w, x, x_dtype, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
+  case F: return gemm_act<F>(w, x, x_dtype, M, y, y_dtype, part, part_bytes, cnt, cnt_count, st, nullptr, yrow);
   switch (w.fmt) {
     DIALQ_GEMM_FMT(DIALQ_FORMAT_W8A16)
     DIALQ_GEMM_FMT(DIALQ_FORMAT_FP8_ROW)

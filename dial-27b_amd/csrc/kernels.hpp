@@ -62,6 +62,10 @@ hipError_t launch_act_fp8(const void *x, int dtype, int64_t M, int64_t K, int64_
                           float *scale, hipStream_t st);
 hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad,
                             uint8_t *packed, uint8_t *scales, hipStream_t st);
+// bf16 rows [M, K] -> f16 rows scaled by 2^-e_m so that each row's maximum
+// sits in [2^14, 2^15); rs[m] = 2^e_m (the Q4_K prefill's f16 kernel on bf16
+// activations).  K % 8 == 0.
+hipError_t launch_x_f16_rows(const void *x, int64_t M, int64_t K, uint16_t *xh, float *rs, hipStream_t st);
 
 // Decode GEMV: y[M,N] = x[M,K] W^T for any M (16 rows per pass).
 // ws: gemv_workspace_bytes(w, x_dtype, M) of scratch (exactly what the
@@ -93,8 +97,9 @@ int gemv_wait_limit();
 // need gemm_workspace(M, w, x_dtype) of scratch: `part` (partial tiles) and
 // `cnt` (per-tile counters, zero before the call and left zero after it).
 void gemm_workspace(int64_t M, const WeightView &w, int x_dtype, size_t &part_bytes, size_t &cnt_count);
+// yrow: per-row output multipliers (k_gemm_q4k only; null = 1).
 hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype, float *part,
-                       size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st);
+                       size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st, const float *yrow = nullptr);
 // Grouped prefill over n (2..kGemmMaxGroup) weights of one format and K that
 // share x: one launch over all members' column tiles, member j writing
 // [M, N_j] through ys[j] with its view's output stride.  The 32x32 kernels
@@ -104,7 +109,8 @@ hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t 
 // kernel applies; the caller then launches per member.
 bool gemm_group_workspace(int64_t M, const WeightView *ws, int n, int x_dtype, size_t &part_bytes, size_t &cnt_count);
 hipError_t launch_gemm_group(const WeightView *ws, void *const *ys, int n, const void *x, int x_dtype, int64_t M,
-                             int y_dtype, float *part, size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st);
+                             int y_dtype, float *part, size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st,
+                             const float *yrow = nullptr);
 bool native_group_workspace(int64_t M, const WeightView *ws, int n, size_t &part_bytes, size_t &cnt_count);
 hipError_t launch_gemm_native_group(const WeightView *ws, void *const *ys, int n, const uint8_t *xq, const void *xs,
                                     int64_t M, int64_t k_pad, int y_dtype, float *part, size_t part_bytes, int *cnt,

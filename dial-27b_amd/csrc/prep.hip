@@ -772,6 +772,59 @@ static void act_fp8_dispatch(const void *x, int64_t M, int64_t K, int64_t k_pad,
   else k_act_fp8_v8<ACT, 0><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
 }
 
+// bf16 activations as f16 for the Q4_K prefill's f16 MFMA kernel.  Row m is
+// scaled by 2^-e_m, e_m the exponent that puts max|x_m| in [2^14, 2^15)
+// (clamped to [-120, 127]), and rounded to f16: exact for every value that
+// lands in f16's normal range, i.e. down to 2^-29 of the row's maximum (bf16
+// carries 8 significant bits); smaller ones keep what f16 subnormals hold
+// (absolute error <= 2^-25 * 2^e_m).  rs[m] = 2^e_m multiplies the row's
+// outputs.  A row of zeros, or one holding an infinity, keeps e_m = 0; NaN
+// stays NaN.
+__global__ __launch_bounds__(256) void k_x_f16_rows(const uint16_t *x, int64_t K, uint16_t *xh, float *rs) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  __shared__ float red[4];
+  const int64_t m = blockIdx.x;
+  const uint16_t *row = x + m * K;
+  float mx = 0.0f;
+  for (int64_t k = (int64_t)threadIdx.x * 8; k < K; k += 256 * 8) {
+    const u32x4 v = *(const u32x4 *)(row + k);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(v[i] & 0xffffu)), fabsf(bf16_bits_to_f32(v[i] >> 16))));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.4028235e38f) {
+    int ex;
+    (void)__builtin_frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+    e = ex - 15;
+    e = e < -120 ? -120 : (e > 127 ? 127 : e);
+  }
+  const float sc = __builtin_ldexpf(1.0f, -e);
+  uint16_t *out = xh + m * K;
+  for (int64_t k = (int64_t)threadIdx.x * 8; k < K; k += 256 * 8) {
+    const u32x4 v = *(const u32x4 *)(row + k);
+    u32x4 h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      h[i] = (uint32_t)f32_to_f16_bits(bf16_bits_to_f32(v[i] & 0xffffu) * sc) |
+             ((uint32_t)f32_to_f16_bits(bf16_bits_to_f32(v[i] >> 16) * sc) << 16);
+    *(u32x4 *)(out + k) = h;
+  }
+  if (threadIdx.x == 0) rs[m] = __builtin_ldexpf(1.0f, e);
+}
+
+hipError_t launch_x_f16_rows(const void *x, int64_t M, int64_t K, uint16_t *xh, float *rs, hipStream_t st) {
+  if (K % 8 != 0 || ((uintptr_t)x & 15u) != 0 || ((uintptr_t)xh & 15u) != 0 || M > 0x7fffffffLL)
+    return hipErrorInvalidValue;
+  if (M > 0) k_x_f16_rows<<<(unsigned)M, 256, 0, st>>>((const uint16_t *)x, K, xh, rs);
+  return hipGetLastError();
+}
+
 hipError_t launch_act_fp8(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad, uint8_t *q,
                           float *scale, hipStream_t st) {
   if (K % 8 != 0 || k_pad % 8 != 0 || ((uintptr_t)x & 15u) != 0 || ((uintptr_t)q & 7u) != 0)

@@ -1,16 +1,20 @@
 """Q4_K prefill (k_gemm_q4k): each weight is dequantized to d*sc*q - dmin*m
 in f32 and multiplied as f16 against f16 activations -- the weight DIAL's
 GGUF prefill builds once, build_worker_gguf_fp16_prefill_linear
-(qwen3_vl/worker_gguf.rs:426-455) -- or as a bf16 hi + lo pair against bf16
-activations.  Pinned three ways on the same inputs:
-  * f16 x: against the fp64 product with the f16-rounded dequantized weight
-    (the hybrid prefill's weight), to f32 accumulation (rel-L2 <= 2e-5; a
-    weight rounded once from the exact value instead of through f32 may
-    differ by one f16 ulp in rare ties);
-  * bf16 x: against the exact product (hi + lo carries 16 significant bits:
-    rel-L2 <= 2e-5 in f32 output);
-  * both against the exact oracle to the weight-only bar (1e-3).
-Row counts cover the 32-row tiles (<= 96 rows, split along K), the 64-row
+(qwen3_vl/worker_gguf.rs:426-455).  bf16 activations are first written as
+f16 rows scaled by a power of two that puts each row's maximum at the top
+of f16's range (k_x_f16_rows; the scale multiplies the row's outputs), or,
+where the allocation-free entry point
+has no room for that copy, multiply the f32 weight as a bf16 hi + lo pair.
+Pinned on the same inputs:
+  * f16 and bf16 x: against the fp64 product with the f16-rounded
+    dequantized weight (the hybrid prefill's weight), to f32 accumulation
+    (rel-L2 <= 2e-5; a weight rounded once from the exact value instead of
+    through f32 may differ by one f16 ulp in rare ties), row by row for rows
+    far outside f16 range;
+  * the hi + lo kernel against the exact product (rel-L2 <= 2e-5);
+  * all against the exact oracle to the weight-only bar (1e-3).
+Row counts cover the 32-row tiles (<= 96 rows, split along K), the 128-row
 tiles, ragged row blocks, SwiGLU and graph replay of a split launch."""
 import numpy as np
 import pytest
@@ -40,11 +44,8 @@ def test_q4k_prefill_weights_and_parity(m, n, k, torch_dev):
         torch.cuda.synchronize()
         got = y.cpu().numpy()
         exact = O.matmul_f64(x, deq)
-        if x_dtype == dq.F16:
-            hybrid = O.matmul_f64(x, O.round_f16(deq))
-            assert O.rel_l2(got, hybrid) <= 2e-5, (m, "f16 weights")
-        else:
-            assert O.rel_l2(got, exact) <= 2e-5, (m, "hi + lo weights")
+        hybrid = O.matmul_f64(x, O.round_f16(deq))
+        assert O.rel_l2(got, hybrid) <= 2e-5, (m, x_dtype, "f16 weights")
         assert O.rel_l2(got, exact) <= 1e-3
         # bf16 / f16 outputs of the same launch
         y_dtype = dq.F16 if x_dtype == dq.F16 else dq.BF16
@@ -109,3 +110,49 @@ def test_q4k_prefill_split_graph_replay(torch_dev):
     lin.dequantize(w16)
     ref = (x[:8].float() @ w16.float().t()).cpu().numpy()
     assert O.rel_l2(want[:8].float().cpu().numpy(), ref) <= 1e-3
+
+
+def test_q4k_prefill_bf16_rows_beyond_f16_range(torch_dev):
+    # bf16 rows far above and below f16's range are scaled by a power of
+    # two for the f16 kernel and scaled back in the epilogue: every row
+    # matches the hybrid product to f32 accumulation, none overflows or
+    # flushes to zero
+    import torch
+    n, k, m = 256, 1024, 130
+    lin, deq = _case(n, k, seed=9)
+    rng = np.random.default_rng(9)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    mult = np.ones(m, np.float32)
+    mult[1::7] = 1e5
+    mult[2::7] = 2.0 ** 100
+    mult[3::7] = 3e-30
+    x = O.round_bf16(x * mult[:, None])
+    y = torch.full((m, n), float("nan"), device=torch_dev, dtype=torch.float32)
+    lin.forward(to_torch(x, dq.BF16, torch_dev), y, path=dq.PATH_GEMM)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    want = O.matmul_f64(x, O.round_f16(deq))
+    assert np.all(np.isfinite(got))
+    for r in range(m):
+        assert O.rel_l2(got[r], want[r]) <= 2e-5, (r, mult[r])
+
+
+def test_q4k_prefill_noalloc_falls_back_to_hi_lo(torch_dev):
+    # 1024 rows at K = 17408: the f16 copy of x (35.7 MB) does not fit the
+    # allocation-free entry point's array, which runs the hi + lo kernel on
+    # x as it is; both agree with the exact product
+    import torch
+    n, k, m = 256, 17408, 1024
+    lin, deq = _case(n, k, seed=4)
+    x = O.round_bf16(np.random.default_rng(4).normal(0, 1, (m, k)).astype(np.float32))
+    xt = to_torch(x, dq.BF16, torch_dev)
+    y1 = torch.empty(m, n, device=torch_dev, dtype=torch.float32)
+    y2 = torch.empty(m, n, device=torch_dev, dtype=torch.float32)
+    lin.forward(xt, y1, path=dq.PATH_GEMM)
+    lin.forward_noalloc(xt, y2, path=dq.PATH_GEMM)
+    torch.cuda.synchronize()
+    rows = np.arange(0, m, 37)
+    exact = O.matmul_f64(x[rows], deq)
+    assert O.rel_l2(y2.cpu().numpy()[rows], exact) <= 2e-5  # hi + lo
+    assert O.rel_l2(y1.cpu().numpy()[rows], O.matmul_f64(x[rows], O.round_f16(deq))) <= 2e-5  # f16 copy
+    assert O.rel_l2(y1.cpu().numpy()[rows], exact) <= 1e-3

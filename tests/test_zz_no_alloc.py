@@ -55,6 +55,8 @@ CASES = {
     "decode_work_queue": (dq.W8A16, [(1024, 8704, 8, dq.PATH_GEMV, 0), (512, 8704, 4, dq.PATH_GEMV, 0)]),
     "decode_q4k_rows": (dq.Q4_K, [(4096, 4096, 8, dq.PATH_GEMV, 0), (256, 4096, 3, dq.PATH_GEMV, 0)]),
     "gemm": (dq.Q8_0, [(640, 1024, 300, dq.PATH_GEMM, 0), (640, 1024, 130, dq.PATH_GEMM, 0)]),
+    # Q4_K on bf16 x: the f16 copy of x and its row scales in the array
+    "gemm_q4k_bf16": (dq.Q4_K, [(1024, 2048, 300, dq.PATH_GEMM, 0), (512, 2048, 40, dq.PATH_GEMM, 0)]),
     "native_fp8_split_k": (dq.FP8_BLOCK, [(1024, 5120, 512, dq.PATH_GEMM_NATIVE, 0),
                                           (1024, 2048, 256, dq.PATH_GEMM_NATIVE, 0)]),
     "native_mxfp4_split_k": (dq.MXFP4, [(1024, 5120, 512, dq.PATH_GEMM_NATIVE, 0),
