@@ -17,8 +17,8 @@ linears as seven separate forwards are reported as decode_gbs_ungrouped.
 Layer copies rotate so the weight working set (COPIES x 341 MB) exceeds the
 256 MB Infinity Cache and the figure measures HBM.  `value` = algorithmic
 weight bytes streamed / wall time of the timed steps, in GB/s.  Extra keys
-report the same decode for Q4_K / FP8-128 / MXFP4, the prefill GEMM TFLOP/s
-(W8A16 and Q4_K at M = 2048 -- Q4_K also with f16 activations, the dtype
+report the same decode for Q4_K / Q8_0 / FP8-128 / MXFP4, the prefill GEMM
+TFLOP/s (W8A16, Q4_K and Q8_0 at M = 2048 -- Q4_K also with f16 activations, the dtype
 of DIAL's GGUF worker --, FP8-128 and MXFP4 native at M = 1024; q / k / v
 and gate / up as grouped forwards like the decode step, and as seven
 forwards in prefill_tflops_ungrouped; also over
@@ -73,7 +73,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the lm_head decode line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--sweep", default="w8a16,q4_k,fp8_block,mxfp4",
+    ap.add_argument("--sweep", default="w8a16,q4_k,q8_0,fp8_block,mxfp4",
                     help="formats for the extra decode / prefill numbers ('' = none)")
     ap.add_argument("--profile", action="store_true",
                     help="only the dominant kernel's launches and the calibration copy (for rocprofv3)")
@@ -549,13 +549,13 @@ def cpu_baseline(seconds):
 # activations of DIAL's GGUF worker, whose prefill multiplies f16-dequantized
 # weights (qwen3_vl/worker_gguf.rs:426-455).
 PREFILL_GATE = [("w8a16", 2048, "PATH_GEMM", "bf16", "bfloat16"), ("q4_k", 2048, "PATH_GEMM", "bf16", "bfloat16"),
-                ("q4_k_f16act", 2048, "PATH_GEMM", "f16", "float16"),
+                ("q4_k_f16act", 2048, "PATH_GEMM", "f16", "float16"), ("q8_0", 2048, "PATH_GEMM", "f16", "bfloat16"),
                 ("fp8_block", 1024, "PATH_GEMM_NATIVE", "fp8", "bfloat16"),
                 ("mxfp4", 1024, "PATH_GEMM_NATIVE", "fp4", "bfloat16")]
 
 
 def prefill_gate_linears(dq, torch, dev, name):
-    fmt = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "q4_k_f16act": dq.Q4_K, "fp8_block": dq.FP8_BLOCK,
+    fmt = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "q4_k_f16act": dq.Q4_K, "q8_0": dq.Q8_0, "fp8_block": dq.FP8_BLOCK,
            "mxfp4": dq.MXFP4}[name]
     _, n, k = DOM
     g = torch.Generator(device=dev).manual_seed(23)
@@ -664,7 +664,7 @@ def main():
     if a.profile_prefill_gate:
         profile_prefill_gate_run(dq, torch, dev)
         return
-    fmt_of = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}
+    fmt_of = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "q8_0": dq.Q8_0, "fp8_block": dq.FP8_BLOCK, "mxfp4": dq.MXFP4}
 
     # ---- headline: W8A16 decode over the 27B layer -----------------------
     layers = build_layers(dq, torch, dq.W8A16, a.copies, dev)

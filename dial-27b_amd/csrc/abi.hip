@@ -311,13 +311,15 @@ struct ForwardPlan {
   size_t xscale = 0;           // native: activation scales
   size_t part = 0;             // native: split-K partial tiles
   size_t ncnt = 0;             // native: split-K tile counters (ints)
-  size_t xh = 0;               // Q4_K GEMM on bf16 x: its f16 copy, then the row scales
+  size_t xh = 0;               // Q4_K / Q8_0 GEMM on bf16 x: its f16 copy, then the row scales
 };
 
-// Bytes of the f16 copy of a bf16 x (and its row scales) that the Q4_K
-// prefill kernel multiplies; 0 where that path does not apply.
-size_t q4k_f16_stage_bytes(const Linear *L, int x_dtype, int64_t rows, int path) {
-  if (path != DIALQ_PATH_GEMM || L->desc.format != DIALQ_FORMAT_Q4_K || x_dtype != DIALQ_BF16) return 0;
+// Bytes of the f16 copy of a bf16 x (and its row scales) that the GGUF
+// (Q4_K, Q8_0) prefill kernel multiplies; 0 where that path does not apply.
+size_t kq_f16_stage_bytes(const Linear *L, int x_dtype, int64_t rows, int path) {
+  const int fmt = L->desc.format;
+  if (path != DIALQ_PATH_GEMM || (fmt != DIALQ_FORMAT_Q4_K && fmt != DIALQ_FORMAT_Q8_0) || x_dtype != DIALQ_BF16)
+    return 0;
   return (size_t)(rows * L->desc.in_dim * 2 + 255) / 256 * 256 + (size_t)rows * sizeof(float);
 }
 
@@ -337,9 +339,9 @@ struct ForwardBufs {
   uint8_t *xh = nullptr;  // f16 copy of a bf16 x, then its row scales (plan.xh bytes)
 };
 
-// A bf16 x of a Q4_K prefill as f16 rows in range (k_x_f16_rows): returns the
+// A bf16 x of a Q4_K / Q8_0 prefill as f16 rows in range (k_x_f16_rows): returns the
 // row scales the GEMM's epilogue multiplies by; `xf` becomes the f16 copy.
-const float *stage_q4k_f16(const void *x, int64_t rows, int64_t K, uint8_t *buf, const void *&xf, hipStream_t st) {
+const float *stage_kq_f16(const void *x, int64_t rows, int64_t K, uint8_t *buf, const void *&xf, hipStream_t st) {
   uint16_t *xh = (uint16_t *)buf;
   float *rs = (float *)(buf + (size_t)(rows * K * 2 + 255) / 256 * 256);
   hip_check(launch_x_f16_rows(x, rows, K, xh, rs, st), "bf16 -> f16 activation rows");
@@ -353,7 +355,7 @@ WeightView forward_view(const Linear *L, bool swiglu) {
   return w;
 }
 
-// stage_f16: a Q4_K GEMM on bf16 x runs the f16 kernel on an f16 copy of x
+// stage_f16: a Q4_K / Q8_0 GEMM on bf16 x runs the f16 kernel on an f16 copy of x
 // (false: the bf16 hi / lo kernel, no copy).
 ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int64_t rows, int path,
                          bool stage_f16 = true) {
@@ -386,7 +388,7 @@ ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int6
     pl.xscale = fmt == DIALQ_FORMAT_FP8_BLOCK ? (size_t)rows * sizeof(float) : (size_t)(rows * pl.k_pad / 32);
     native_workspace(rows, w, pl.part, pl.ncnt);
   } else if (path == DIALQ_PATH_GEMM) {
-    if (stage_f16) pl.xh = q4k_f16_stage_bytes(L, x_dtype, rows, path);
+    if (stage_f16) pl.xh = kq_f16_stage_bytes(L, x_dtype, rows, path);
     // split-K partials of few-tile launches (the f16 kernel's tiling when x is staged as f16)
     gemm_workspace(rows, w, pl.xh ? DIALQ_F16 : x_dtype, pl.part, pl.ncnt);
   } else {
@@ -402,7 +404,7 @@ void launch_forward(const Linear *L, const WeightView &w, const ForwardPlan &pl,
               "GEMV launch");
   } else if (pl.path == DIALQ_PATH_GEMM) {
     const void *xf = x;
-    const float *yrow = b.xh ? stage_q4k_f16(x, rows, w.K, b.xh, xf, st) : nullptr;
+    const float *yrow = b.xh ? stage_kq_f16(x, rows, w.K, b.xh, xf, st) : nullptr;
     hip_check(launch_gemm(w, xf, b.xh ? DIALQ_F16 : x_dtype, rows, y, y_dtype, b.part, b.part_bytes, b.ncnt,
                           b.ncnt_count, st, yrow),
               "GEMM launch");
@@ -539,7 +541,7 @@ bool run_prefill_group(Linear *const *Ls, const WeightView *ws, void *const *ys,
   Linear *L = Ls[0];
   size_t part = 0, ncnt = 0;
   if (path == DIALQ_PATH_GEMM) {
-    const size_t xh = q4k_f16_stage_bytes(L, x_dtype, rows, path);  // bf16 x of a Q4_K group: f16 once
+    const size_t xh = kq_f16_stage_bytes(L, x_dtype, rows, path);  // bf16 x of a Q4_K / Q8_0 group: f16 once
     const int kx = xh ? DIALQ_F16 : x_dtype;
     if (!gemm_group_workspace(rows, ws, n, kx, part, ncnt)) return false;
     std::lock_guard<std::mutex> lock(L->scratch_mu);
@@ -548,7 +550,7 @@ bool run_prefill_group(Linear *const *Ls, const WeightView *ws, void *const *ys,
     const float *yrow = nullptr;
     if (xh) {
       ensure_scratch(L, xh, st);
-      yrow = stage_q4k_f16(x, rows, ws[0].K, (uint8_t *)L->act_scratch.p, xf, st);
+      yrow = stage_kq_f16(x, rows, ws[0].K, (uint8_t *)L->act_scratch.p, xf, st);
     }
     const hipError_t r = launch_gemm_group(ws, ys, n, xf, kx, rows, y_dtype, (float *)L->native_part.p,
                                            L->native_part.n, (int *)L->native_cnt.p, L->native_cnt.n / sizeof(int), st,
@@ -739,7 +741,7 @@ void forward_noalloc_impl(Linear *L, const void *x, int32_t x_dtype, int64_t row
   const size_t xbytes = (size_t)(rows * K) * xs;
   const bool stage_x = ((uintptr_t)x) & 15u;
   ForwardPlan pl = plan_forward(L, w, x_dtype, rows, path);
-  // a Q4_K prefill on bf16 x whose f16 copy does not fit runs the bf16 hi / lo
+  // a Q4_K / Q8_0 prefill on bf16 x whose f16 copy does not fit runs the bf16 hi / lo
   // kernel on x as it is
   if (pl.xh && kNoAllocCntBytes + up(pl.codes + pl.xscale) + up(pl.part) + up(pl.xh) +
                        (stage_x ? up(xbytes) : 0) > kNoAllocScratchBytes)

@@ -49,14 +49,14 @@ struct GemmParams {
   void *y;
   int64_t M;
   int y_dtype;
-  // Split-K (k_gemm32, k_gemm_q4k; P > 1): each tile's chunks split into P
+  // Split-K (k_gemm32, k_gemm_kq; P > 1): each tile's chunks split into P
   // pieces, one workgroup each; partial tiles in `part` ([tiles][P][rows x
   // 256]), one arrival counter per tile in `cnt` (zero between launches).
   int P = 1;
   float *part = nullptr;
   int *cnt = nullptr;
-  GemmGroup g;  // k_gemm32, k_gemm_q4k
-  // k_gemm_q4k: per-row output multipliers (bf16 activations scaled into f16
+  GemmGroup g;  // k_gemm32, k_gemm_kq
+  // k_gemm_kq: per-row output multipliers (bf16 activations scaled into f16
   // range, 2^e per row); null = 1
   const float *yrow = nullptr;
 };
@@ -128,11 +128,11 @@ constexpr int kXcds = 8, kPanel = 4;
 #ifndef GEMM32_KS
 #define GEMM32_KS 1  // 64-k chunks per pipeline stage in the 32x32 kernel
 #endif
-#ifndef GEMMQ4K_MT
-#define GEMMQ4K_MT 4  // 32-row MFMA tiles per workgroup in the Q4_K prefill kernel
+#ifndef GEMMKQ_MT
+#define GEMMKQ_MT 4  // 32-row MFMA tiles per workgroup in the GGUF (Q4_K, Q8_0) prefill kernel
 #endif
-#ifndef GEMMQ4K_OCC
-#define GEMMQ4K_OCC 2  // workgroups per CU the Q4_K prefill kernel is built for
+#ifndef GEMMKQ_OCC
+#define GEMMKQ_OCC 2  // workgroups per CU the GGUF prefill kernel is built for
 #endif
 #ifndef GEMM32_OCC
 #define GEMM32_OCC 3  // workgroups per CU the 32x32 kernel is built for
@@ -690,43 +690,35 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K prefill on v_mfma_f32_32x32x16 with dequantized weight operands.
-// The weight-only k_gemm keeps Q4_K exact (codes offset by 128, one extra
-// MFMA per 32-k slice for the min term, the sub-block scales applied to f32
-// partials), which leaves it bound by VALU and half its MFMAs on x * 1.
-// Prefill instead takes each weight as the value DIAL's GGUF prefill
-// multiplies by: d*sc*q - dmin*m in f32, rounded to f16 -- the weight
-// build_worker_gguf_fp16_prefill_linear dequantizes once
-// (qwen3_vl/worker_gguf.rs:426-455, candle's Q4K to_float) -- against f16
+// GGUF prefill (Q4_K, Q8_0) on v_mfma_f32_32x32x16 with dequantized weight
+// operands.  The weight-only k_gemm keeps these exact (codes as exact bf16,
+// block scales applied to f32 partials; Q4_K with one extra MFMA per 32-k
+// slice for its min term), which leaves it bound by VALU.  Prefill instead
+// takes each weight as the value DIAL's GGUF prefill multiplies by -- the
+// format's dequantized value in f32 (Q4_K d*sc*q - dmin*m, Q8_0 d*q) rounded
+// to f16, the weight build_worker_gguf_fp16_prefill_linear dequantizes once
+// (qwen3_vl/worker_gguf.rs:426-455, candle's to_float) -- against f16
 // activations (the GGUF worker's dtype), one MFMA per 16-k step.  bf16
-// activations take the f32 weight as a bf16 hi + lo pair (two MFMAs, 2^-17
-// relative), since one bf16 rounding of the weight alone (2^-9) would
-// dominate the product's error.
+// activations are made f16 rows in range first (k_x_f16_rows) or, where no
+// room is left for that copy, take the f32 weight as a bf16 hi + lo pair
+// (two MFMAs, 2^-17 relative), since one bf16 rounding of the weight alone
+// (2^-9) would dominate the product's error.
 //
 // Layout as k_gemm32: a 256-thread workgroup computes a (32*MT) x 256 tile;
 // wave v owns 32-column MFMA tiles q = 0, 1 (strips s0 + 2q, s0 + 2q + 1;
-// lane l: column l % 32, k group h = l / 32).  A stage is one quarter i of
-// a 256-k chunk: k = 64i + 8g + j (low nibbles, sub-block 2i) and
-// 64i + 32 + 8g + j (high nibbles, sub-block 2i + 1) sit in byte 8i + j of
-// tile lane r + 16g, so the stage's 16-k steps 0..3 read lane groups
-// g = h, 2 + h, h, 2 + h, low nibbles for steps 0-1 and high for 2-3: two
-// 8-byte loads per column tile, plus the row's 16-byte block header.
+// lane l: column l % 32, k group h = l / 32).  A stage is 64 k; step j of
+// a stage (16 k) reads lane group g = 2(j % 2) + h of the resident tile.
+//   Q4_K: a stage is quarter i of a 256-k chunk: k = 64i + 8g + j' (low
+//         nibbles, sub-block 2i) and 64i + 32 + 8g + j' (high nibbles,
+//         sub-block 2i + 1) sit in byte 8i + j' of tile lane r + 16g: steps
+//         0-1 take the low nibbles, 2-3 the high ones -- two 8-byte loads
+//         per column tile, plus the row's 16-byte block header.
+//   Q8_0: a stage is one 64-k tile: block b = j / 2 sits in bytes 8b..8b+7
+//         of lane r + 16g -- two 16-byte loads per column tile, plus the
+//         row's two f16 block scales.
 // ---------------------------------------------------------------------------
 template <int ACT>
-__device__ __forceinline__ void q4k_operand(uint32_t d0, uint32_t d1, bool high, float s1, float s2, u32x4 &hi,
-                                            u32x4 &lo) {
-  // the high nibbles are taken in place (16q) against s1 / 16 (exact)
-  const uint32_t m = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
-  const float sc = high ? s1 * 0.0625f : s1;
-  const uint32_t x[2] = {d0 & m, d1 & m};
-  float wv[8];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    wv[4 * i] = __builtin_fmaf(sc, (float)(x[i] & 0xffu), -s2);
-    wv[4 * i + 1] = __builtin_fmaf(sc, (float)((x[i] >> 8) & 0xffu), -s2);
-    wv[4 * i + 2] = __builtin_fmaf(sc, (float)((x[i] >> 16) & 0xffu), -s2);
-    wv[4 * i + 3] = __builtin_fmaf(sc, (float)(x[i] >> 24), -s2);
-  }
+__device__ __forceinline__ void kq_pack(const float (&wv)[8], u32x4 &hi, u32x4 &lo) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   typedef __bf16 b2 __attribute__((ext_vector_type(2)));
 #pragma unroll
@@ -745,33 +737,122 @@ __device__ __forceinline__ void q4k_operand(uint32_t d0, uint32_t d1, bool high,
   }
 }
 
-// d * sc and dmin * m (f32, exact) of sub-blocks 2i and 2i + 1 from a Q4_K
-// block header {d, dmin, scales[12]} (the 6-bit packing of
-// candle's get_scale_min_k4).
-template <int I>
-__device__ __forceinline__ void q4k_scales(u32x4 hd, float (&s1)[2], float (&s2)[2]) {
-  const float d = f16_bits_to_f32(hd[0] & 0xffffu), dmin = f16_bits_to_f32(hd[0] >> 16);
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int j = 2 * I + e;
-    uint32_t sc, mn;
-    if (j < 4) {
-      sc = (hd[1] >> (8 * j)) & 63u;
-      mn = (hd[2] >> (8 * j)) & 63u;
-    } else {
-      const int jj = j - 4;
-      const uint32_t b8 = (hd[3] >> (8 * jj)) & 0xffu;
-      sc = (b8 & 0xfu) | (((hd[1] >> (8 * jj + 6)) & 3u) << 4);
-      mn = (b8 >> 4) | (((hd[2] >> (8 * jj + 6)) & 3u) << 4);
-    }
-    s1[e] = d * (float)sc;
-    s2[e] = dmin * (float)mn;
-  }
-}
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-template <int ACT, int MT, int OCC, bool SWI>
-__global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
+template <int FMT>
+struct KqFmt;
+
+template <>
+struct KqFmt<DIALQ_FORMAT_Q4_K> {
+  static constexpr int CHUNK = 256, TILE = 2048, AUX = 256;
+  struct Slot {
+    u32x2 c[2];  // lane groups h and 2 + h: bytes 8i..8i+7
+    u32x4 hd;    // block header {d, dmin, scales[12]}
+  };
+  struct Sc {
+    float s1[2], s2[2];  // d*sc and dmin*m of sub-blocks 2i, 2i + 1
+  };
+  static __device__ __forceinline__ void fetch(Slot &sl, rsrc_t rt, rsrc_t ra, uint32_t tile, int i, bool valid, int r,
+                                               int h) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t off = tile * 2048u + (uint32_t)(i / 2) * 1024u + (uint32_t)(16 * (r + 16 * (2 * e + h)) + 8 * (i % 2));
+      sl.c[e] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rt, valid ? (int)off : (int)kOOB, 0, 0));
+    }
+    sl.hd = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, valid ? (int)(tile * 256u + 16u * (uint32_t)r) : (int)kOOB, 0, 0));
+  }
+  // the 6-bit packing of candle's get_scale_min_k4; products exact in f32
+  template <int I>
+  static __device__ __forceinline__ Sc scales(const Slot &sl) {
+    const u32x4 hd = sl.hd;
+    const float d = f16_bits_to_f32(hd[0] & 0xffffu), dmin = f16_bits_to_f32(hd[0] >> 16);
+    Sc o;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int j = 2 * I + e;
+      uint32_t sc, mn;
+      if (j < 4) {
+        sc = (hd[1] >> (8 * j)) & 63u;
+        mn = (hd[2] >> (8 * j)) & 63u;
+      } else {
+        const int jj = j - 4;
+        const uint32_t b8 = (hd[3] >> (8 * jj)) & 0xffu;
+        sc = (b8 & 0xfu) | (((hd[1] >> (8 * jj + 6)) & 3u) << 4);
+        mn = (b8 >> 4) | (((hd[2] >> (8 * jj + 6)) & 3u) << 4);
+      }
+      o.s1[e] = d * (float)sc;
+      o.s2[e] = dmin * (float)mn;
+    }
+    return o;
+  }
+  // f32 weights of step j: the high nibbles are taken in place (16q)
+  // against s1 / 16 (exact)
+  static __device__ __forceinline__ void weights(const Slot &sl, const Sc &sc, int j, float (&wv)[8]) {
+    const bool high = j >= 2;
+    const uint32_t m = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+    const float s1 = high ? sc.s1[1] * 0.0625f : sc.s1[0], s2 = high ? sc.s2[1] : sc.s2[0];
+    const uint32_t x[2] = {sl.c[j & 1][0] & m, sl.c[j & 1][1] & m};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      wv[4 * i] = __builtin_fmaf(s1, (float)(x[i] & 0xffu), -s2);
+      wv[4 * i + 1] = __builtin_fmaf(s1, (float)((x[i] >> 8) & 0xffu), -s2);
+      wv[4 * i + 2] = __builtin_fmaf(s1, (float)((x[i] >> 16) & 0xffu), -s2);
+      wv[4 * i + 3] = __builtin_fmaf(s1, (float)(x[i] >> 24), -s2);
+    }
+  }
+};
+
+template <>
+struct KqFmt<DIALQ_FORMAT_Q8_0> {
+  static constexpr int CHUNK = 64, TILE = 1024, AUX = 64;
+  struct Slot {
+    u32x4 c[2];  // lane groups h and 2 + h: blocks 0 (bytes 0-7) and 1 (8-15)
+    uint32_t d;  // the row's f16 scales of blocks 0 and 1
+  };
+  struct Sc {
+    float d[2];
+  };
+  static __device__ __forceinline__ void fetch(Slot &sl, rsrc_t rt, rsrc_t ra, uint32_t tile, int i, bool valid, int r,
+                                               int h) {
+    (void)i;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t off = tile * 1024u + (uint32_t)(16 * (r + 16 * (2 * e + h)));
+      sl.c[e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rt, valid ? (int)off : (int)kOOB, 0, 0));
+    }
+    sl.d = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ra, valid ? (int)(tile * 64u + 4u * (uint32_t)r) : (int)kOOB,
+                                                          0, 0);
+  }
+  template <int I>
+  static __device__ __forceinline__ Sc scales(const Slot &sl) {
+    Sc o;
+    o.d[0] = f16_bits_to_f32(sl.d & 0xffffu);
+    o.d[1] = f16_bits_to_f32(sl.d >> 16);
+    return o;
+  }
+  // f32 weights d*q of step j (exact: 11 x 8 significant bits): the codes
+  // are read as unsigned bytes q + 128 (sign bit flipped) and d*(q + 128) -
+  // 128 d is one fused multiply-add
+  static __device__ __forceinline__ void weights(const Slot &sl, const Sc &sc, int j, float (&wv)[8]) {
+    const int b = j >> 1;
+    const float d = sc.d[b], off = -128.0f * d;
+    const uint32_t x[2] = {sl.c[j & 1][2 * b] ^ 0x80808080u, sl.c[j & 1][2 * b + 1] ^ 0x80808080u};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      wv[4 * i] = __builtin_fmaf(d, (float)(x[i] & 0xffu), off);
+      wv[4 * i + 1] = __builtin_fmaf(d, (float)((x[i] >> 8) & 0xffu), off);
+      wv[4 * i + 2] = __builtin_fmaf(d, (float)((x[i] >> 16) & 0xffu), off);
+      wv[4 * i + 3] = __builtin_fmaf(d, (float)(x[i] >> 24), off);
+    }
+  }
+};
+
+template <int FMT, int ACT, int MT, int OCC, bool SWI>
+__global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
   static_assert(ACT == DIALQ_BF16 || ACT == kActF16N, "bf16 or f16 activations");
+  typedef KqFmt<FMT> F;
+  constexpr int SPC = F::CHUNK / 64;  // stages per resident chunk
   constexpr bool HL = ACT == DIALQ_BF16;  // weight as bf16 hi + lo
   constexpr int SK = 64, BY = 2;
   constexpr int ROWS = 32 * MT, STRIDE = SK + 8, BUF = ROWS * STRIDE;
@@ -795,13 +876,13 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
   int s0 = tn * 16 + wave * 4, slim = (int)w.n_strips, j0 = 0;
   if constexpr (SWI) swiglu_strips<16>(w, tn, wave, s0, slim, j0);
   const int K = (int)w.K;
-  // this workgroup's 256-k chunks [c0, c1): four stages each
+  // this workgroup's chunks [c0, c1): SPC stages each
   const int c0 = (int)((int64_t)piece * w.k_chunks / P), c1 = (int)((int64_t)(piece + 1) * w.k_chunks / P);
-  const int nstage = 4 * (c1 - c0);
-  const int kend = (c1 * 256 < K) ? c1 * 256 : K;
+  const int nstage = SPC * (c1 - c0);
+  const int kend = (c1 * F::CHUNK < K) ? c1 * F::CHUNK : K;
   const int64_t total = w.n_strips * w.k_chunks;
-  const rsrc_t rt = make_rsrc(w.tiles, (uint32_t)(total * 2048));
-  const rsrc_t ra = make_rsrc(w.aux, (uint32_t)(total * 256));
+  const rsrc_t rt = make_rsrc(w.tiles, (uint32_t)(total * F::TILE));
+  const rsrc_t ra = make_rsrc(w.aux, (uint32_t)(total * F::AUX));
   const int mrows = (int)((p.M - m0) < ROWS ? (p.M - m0) : ROWS);
   const rsrc_t rx = make_rsrc((const uint8_t *)p.x + (int64_t)m0 * K * BY, (uint32_t)((int64_t)mrows * K * BY));
 
@@ -810,7 +891,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
 #pragma unroll
     for (int q = 0; q < PIECES; ++q) {
       const int pc = tid + q * 256, row = pc / (SK / 8), kk = (pc % (SK / 8)) * 8;
-      const int k = c0 * 256 + st * SK + kk;
+      const int k = c0 * F::CHUNK + st * SK + kk;
       apre[q] = xraw_load<ACT>(rx, (st < nstage && k < kend) ? (uint32_t)((row * K + k) * BY) : kOOB);
     }
   };
@@ -822,27 +903,18 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
       *(u32x4 *)(base + row * STRIDE + kk) = apre[q].a;
     }
   };
-  // stage st's codes (lane groups h and 2 + h) and block header of column
-  // tile q, for this lane's weight row
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  // stage st's codes and scales of column tile q, for this lane's weight row
   struct Slot {
-    u32x2 c[NQ][2];
-    u32x4 hd[NQ];
+    typename F::Slot q[NQ];
   };
   auto fetch_b = [&](Slot &sl, int st) {
-    const int c = c0 + st / 4, i = st % 4;
+    const int c = c0 + st / SPC, i = st % SPC;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int strip = s0 + 2 * q + sub;
       const bool valid = st < nstage && strip < slim;
       const uint32_t tile = (uint32_t)strip * (uint32_t)w.k_chunks + (uint32_t)c;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const uint32_t off = tile * 2048u + (uint32_t)(i / 2) * 1024u + (uint32_t)(16 * (r + 16 * (2 * e + h)) + 8 * (i % 2));
-        sl.c[q][e] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rt, valid ? (int)off : (int)kOOB, 0, 0));
-      }
-      sl.hd[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                               ra, valid ? (int)(tile * 256u + 16u * (uint32_t)r) : (int)kOOB, 0, 0));
+      F::fetch(sl.q[q], rt, ra, tile, i, valid, r, h);
     }
   };
 
@@ -869,23 +941,21 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
     store_a((st + 1) & 1);
     fetch_a(st + 2);
     __builtin_amdgcn_sched_barrier(0);
-    float s1[NQ][2], s2[NQ][2];
+    typename F::Sc sc[NQ];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) q4k_scales<I>(sl.hd[q], s1[q], s2[q]);
-    u32x2 cw[NQ][2];
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      cw[q][0] = sl.c[q][0];
-      cw[q][1] = sl.c[q][1];
-    }
+    for (int q = 0; q < NQ; ++q) sc[q] = F::template scales<I>(sl.q[q]);
+    const Slot cur = sl;
     fetch_b(sl, st + 2);  // refill with stage st + 2
     const uint16_t *base = lds + (st & 1) * BUF;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       u32x4 bh[NQ], bl[NQ];
 #pragma unroll
-      for (int q = 0; q < NQ; ++q)
-        q4k_operand<ACT>(cw[q][j & 1][0], cw[q][j & 1][1], j >= 2, s1[q][j >> 1], s2[q][j >> 1], bh[q], bl[q]);
+      for (int q = 0; q < NQ; ++q) {
+        float wv[8];
+        F::weights(cur.q[q], sc[q], j, wv);
+        kq_pack<ACT>(wv, bh[q], bl[q]);
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int row = mt * 32 + (lane & 31), kk = j * 16 + 8 * h;
@@ -899,11 +969,20 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_q4k(GemmParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  for (int st = 0; st < nstage; st += 4) {
-    stage(wb[0], st, std::integral_constant<int, 0>{});
-    stage(wb[1], st + 1, std::integral_constant<int, 1>{});
-    stage(wb[0], st + 2, std::integral_constant<int, 2>{});
-    stage(wb[1], st + 3, std::integral_constant<int, 3>{});
+  if constexpr (SPC == 4) {
+    for (int st = 0; st < nstage; st += 4) {
+      stage(wb[0], st, std::integral_constant<int, 0>{});
+      stage(wb[1], st + 1, std::integral_constant<int, 1>{});
+      stage(wb[0], st + 2, std::integral_constant<int, 2>{});
+      stage(wb[1], st + 3, std::integral_constant<int, 3>{});
+    }
+  } else {
+    int st = 0;
+    for (; st + 1 < nstage; st += 2) {
+      stage(wb[0], st, std::integral_constant<int, 0>{});
+      stage(wb[1], st + 1, std::integral_constant<int, 0>{});
+    }
+    if (st < nstage) stage(wb[0], st, std::integral_constant<int, 0>{});
   }
 
   if (P > 1 && !split_fixup<MT, NQ>(p, acc, tg, piece, (int *)(lds + 2 * BUF))) return;
@@ -996,12 +1075,13 @@ static int64_t gemm32_col_tiles(const WeightView &w) { return w.pair ? (w.pair +
 static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt) {
   Gemm32Plan g;
   const bool small = M <= kGemm32SmallRows;
-  g.mt = small ? 1 : w.fmt == DIALQ_FORMAT_Q4_K ? GEMMQ4K_MT : M >= kGemm32TallRows ? 4 : GEMM32_MT;
+  const bool kq = w.fmt == DIALQ_FORMAT_Q4_K || w.fmt == DIALQ_FORMAT_Q8_0;
+  g.mt = small ? 1 : kq ? GEMMKQ_MT : M >= kGemm32TallRows ? 4 : GEMM32_MT;
   g.ks = small ? 2 : GEMM32_KS;  // byte formats; a Q4_K stage is one 64-k quarter chunk
   const int64_t rows = 32 * g.mt;
   g.tiles = nt * ((M + rows - 1) / rows);
   g.P = 1;
-  const int64_t occ = w.fmt == DIALQ_FORMAT_Q4_K ? GEMMQ4K_OCC : g.mt == 4 ? 2 : GEMM32_OCC;
+  const int64_t occ = kq ? GEMMKQ_OCC : g.mt == 4 ? 2 : GEMM32_OCC;
   const int64_t cus = device_cus(), slots = occ * cus;
   if (small ? g.tiles * 2 <= slots : g.tiles * 2 < cus) {
     const int64_t steps = w.k_chunks * (w.fmt == DIALQ_FORMAT_Q4_K ? 4 : 1);
@@ -1014,12 +1094,14 @@ static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt) {
   return g;
 }
 
-// The 32x32 kernels: W8A16 / FP8_ROW (k_gemm32) and Q4_K with bf16 or f16
-// activations (k_gemm_q4k; f32 activations keep the exact k_gemm).
+// The 32x32 kernels: W8A16 / FP8_ROW (k_gemm32) and Q4_K / Q8_0 with bf16
+// or f16 activations (k_gemm_kq; f32 activations keep the exact k_gemm).
 static bool gemm32_applies(const WeightView &w, int x_dtype) {
   if (w.fmt == DIALQ_FORMAT_W8A16 || w.fmt == DIALQ_FORMAT_FP8_ROW) return w.n_strips * w.k_chunks * 1024 <= 0xffffffffLL;
   if (w.fmt == DIALQ_FORMAT_Q4_K)
     return x_dtype != DIALQ_F32 && w.n_strips * w.k_chunks * 2048 <= 0xffffffffLL;
+  if (w.fmt == DIALQ_FORMAT_Q8_0)
+    return x_dtype != DIALQ_F32 && w.n_strips * w.k_chunks * 1024 <= 0xffffffffLL;
   return false;
 }
 
@@ -1064,13 +1146,13 @@ bool gemm_group_workspace(int64_t M, const WeightView *ws, int n, int x_dtype, s
   return true;
 }
 
-template <int ACT, int MT>
-static hipError_t gemm_q4k_launch(const GemmParams &p, int64_t grid, hipStream_t st) {
+template <int FMT, int ACT, int MT>
+static hipError_t gemm_kq_launch(const GemmParams &p, int64_t grid, hipStream_t st) {
   constexpr int BUF = 32 * MT * (64 + 8);
   static_assert(2 * BUF * 2 >= 8192, "the SwiGLU exchange reuses the staging LDS");
   const size_t lds_bytes = 2 * BUF * 2 + 16;  // two staging buffers and the split-K arrival flag
-  if (p.w.pair) k_gemm_q4k<ACT, MT, GEMMQ4K_OCC, true><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
-  else k_gemm_q4k<ACT, MT, GEMMQ4K_OCC, false><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
+  if (p.w.pair) k_gemm_kq<FMT, ACT, MT, GEMMKQ_OCC, true><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
+  else k_gemm_kq<FMT, ACT, MT, GEMMKQ_OCC, false><<<(unsigned)grid, 256, lds_bytes, st>>>(p);
   return hipGetLastError();
 }
 
@@ -1092,8 +1174,8 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
   typedef GemmShape<FMT, ACT> S;
   if ((int64_t)S::ROWS * w.K * ActTraits<ACT>::BYTES > 0xffffffffLL) return hipErrorInvalidValue;
   constexpr bool BYTE = FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW;
-  constexpr bool Q4K = FMT == DIALQ_FORMAT_Q4_K && (ACT == DIALQ_BF16 || ACT == kActF16N);
-  if constexpr (BYTE || Q4K) {
+  constexpr bool KQ = (FMT == DIALQ_FORMAT_Q4_K || FMT == DIALQ_FORMAT_Q8_0) && (ACT == DIALQ_BF16 || ACT == kActF16N);
+  if constexpr (BYTE || KQ) {
     if (gemm32_applies(w, ACT == DIALQ_F32 ? DIALQ_F32 : DIALQ_BF16)) {
       const Gemm32Plan g = gemm32_plan(M, w, grp ? grp->tbase[grp->nm] : gemm32_col_tiles(w));
       if (g.P > 1 && ((size_t)g.tiles > cnt_count || g.part_bytes() > part_bytes)) return hipErrorInvalidValue;
@@ -1101,10 +1183,10 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
       GemmParams p{w, x, y, M, y_dtype, g.P, part, cnt};
       if (grp) p.g = *grp;
       p.yrow = yrow;
-      if (yrow && !Q4K) return hipErrorInvalidValue;
-      if constexpr (Q4K) {
-        if (g.mt == 1) return gemm_q4k_launch<ACT, 1>(p, g.tiles * g.P, st);
-        return gemm_q4k_launch<ACT, GEMMQ4K_MT>(p, g.tiles * g.P, st);
+      if (yrow && !KQ) return hipErrorInvalidValue;
+      if constexpr (KQ) {
+        if (g.mt == 1) return gemm_kq_launch<FMT, ACT, 1>(p, g.tiles * g.P, st);
+        return gemm_kq_launch<FMT, ACT, GEMMKQ_MT>(p, g.tiles * g.P, st);
       } else {
         if (g.mt == 1) return gemm32_launch<FMT, ACT, 1, 2>(p, g.tiles * g.P, st);
         if (g.mt == 4) return gemm32_launch<FMT, ACT, 4, 1, 2>(p, g.tiles * g.P, st);
@@ -1158,6 +1240,10 @@ hipError_t launch_gemm_group(const WeightView *ws, void *const *ys, int n, const
       break;
     case DIALQ_FORMAT_Q4_K:
       r = gemm_act<DIALQ_FORMAT_Q4_K>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g,
+                                      yrow);
+      break;
+    case DIALQ_FORMAT_Q8_0:
+      r = gemm_act<DIALQ_FORMAT_Q8_0>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g,
                                       yrow);
       break;
   }

@@ -63,7 +63,7 @@ hipError_t launch_act_fp8(const void *x, int dtype, int64_t M, int64_t K, int64_
 hipError_t launch_act_mxfp4(const void *x, int dtype, int64_t M, int64_t K, int64_t k_pad,
                             uint8_t *packed, uint8_t *scales, hipStream_t st);
 // bf16 rows [M, K] -> f16 rows scaled by 2^-e_m so that each row's maximum
-// sits in [2^14, 2^15); rs[m] = 2^e_m (the Q4_K prefill's f16 kernel on bf16
+// sits in [2^14, 2^15); rs[m] = 2^e_m (the GGUF prefill's f16 kernel on bf16
 // activations).  K % 8 == 0.
 hipError_t launch_x_f16_rows(const void *x, int64_t M, int64_t K, uint16_t *xh, float *rs, hipStream_t st);
 
@@ -97,7 +97,7 @@ int gemv_wait_limit();
 // need gemm_workspace(M, w, x_dtype) of scratch: `part` (partial tiles) and
 // `cnt` (per-tile counters, zero before the call and left zero after it).
 void gemm_workspace(int64_t M, const WeightView &w, int x_dtype, size_t &part_bytes, size_t &cnt_count);
-// yrow: per-row output multipliers (k_gemm_q4k only; null = 1).
+// yrow: per-row output multipliers (k_gemm_kq only; null = 1).
 hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype, float *part,
                        size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st, const float *yrow = nullptr);
 // Grouped prefill over n (2..kGemmMaxGroup) weights of one format and K that

@@ -772,7 +772,7 @@ static void act_fp8_dispatch(const void *x, int64_t M, int64_t K, int64_t k_pad,
   else k_act_fp8_v8<ACT, 0><<<(unsigned)M, 256, 0, st>>>(x, K, q, scale, k_pad);
 }
 
-// bf16 activations as f16 for the Q4_K prefill's f16 MFMA kernel.  Row m is
+// bf16 activations as f16 for the GGUF (Q4_K, Q8_0) prefill's f16 MFMA kernel.  Row m is
 // scaled by 2^-e_m, e_m the exponent that puts max|x_m| in [2^14, 2^15)
 // (clamped to [-120, 127]), and rounded to f16: exact for every value that
 // lands in f16's normal range, i.e. down to 2^-29 of the row's maximum (bf16

@@ -4,7 +4,7 @@ x, the replacement of QkvProjection::Split / MlpGateUpProjection::Split
 member (mixed formats, prefill formats without a grouped kernel) must
 equal each member's own dialq_linear_forward_ex output bit for bit (the
 same kernels with a strided output).  A grouped launch -- decode, or
-prefill of W8A16 / FP8_ROW / Q4_K (bf16, f16 x) / FP8_BLOCK and MXFP4
+prefill of W8A16 / FP8_ROW / Q4_K and Q8_0 (bf16, f16 x) / FP8_BLOCK and MXFP4
 native -- sizes its split along K from all the group's tiles, so a
 member's f32 sum may be split differently than in its own launch: those
 columns must agree with its own forward to f32 rounding (rel-L2 <= 2e-4 in
@@ -180,9 +180,10 @@ def test_group_27b_shapes(group, fmt, torch_dev):
 @pytest.mark.parametrize("group", [[6144, 1024, 1024], [17408, 17408]], ids=["qkv", "gate_up"])
 @pytest.mark.parametrize("fmt,x_dtype,path", [(dq.W8A16, dq.BF16, dq.PATH_GEMM), (dq.FP8_ROW, dq.BF16, dq.PATH_GEMM),
                                               (dq.Q4_K, dq.F16, dq.PATH_GEMM), (dq.Q4_K, dq.BF16, dq.PATH_GEMM),
+                                              (dq.Q8_0, dq.BF16, dq.PATH_GEMM),
                                               (dq.FP8_BLOCK, dq.BF16, dq.PATH_GEMM_NATIVE),
                                               (dq.MXFP4, dq.BF16, dq.PATH_GEMM_NATIVE)],
-                         ids=["w8a16", "fp8_row", "q4_k_f16", "q4_k_bf16", "fp8_block", "mxfp4"])
+                         ids=["w8a16", "fp8_row", "q4_k_f16", "q4_k_bf16", "q8_0_bf16", "fp8_block", "mxfp4"])
 def test_group_prefill_27b_shapes(group, fmt, x_dtype, path, torch_dev):
     # prefill of DIAL's split projections: one grouped launch over every
     # member's column tiles (small and large row counts: split along K or
