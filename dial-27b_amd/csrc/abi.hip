@@ -527,8 +527,8 @@ void forward_impl(Linear *L, const void *x, int32_t x_dtype, int64_t rows, void 
 // decode path runs the strips of up to four same-format members in one
 // launch (one workgroup per strip, x staged once per workgroup as in a
 // single forward); the prefill paths run the column tiles of up to four
-// same-format members in one GEMM launch (W8A16, FP8_ROW, Q4_K with bf16 /
-// f16 x; FP8_BLOCK and MXFP4 native on x quantized once); every other case
+// same-format members in one GEMM launch (W8A16, FP8_ROW, Q4_K and Q8_0 with
+// bf16 / f16 x; FP8_BLOCK and MXFP4 native on x quantized once); every other case
 // runs one launch per member, each writing its columns of the concatenated
 // output.
 constexpr int kGroupMax = 4;

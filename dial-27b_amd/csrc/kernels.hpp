@@ -103,7 +103,7 @@ hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t 
 // Grouped prefill over n (2..kGemmMaxGroup) weights of one format and K that
 // share x: one launch over all members' column tiles, member j writing
 // [M, N_j] through ys[j] with its view's output stride.  The 32x32 kernels
-// (W8A16, FP8_ROW; Q4_K with bf16 / f16 x) and the native kernel (FP8_BLOCK,
+// (W8A16, FP8_ROW; Q4_K and Q8_0 with bf16 / f16 x) and the native kernel (FP8_BLOCK,
 // MXFP4 on x quantized once).  *_group_workspace returns false, and the
 // launchers hipErrorNotSupported (launching nothing), where no grouped
 // kernel applies; the caller then launches per member.
