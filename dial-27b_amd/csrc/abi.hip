@@ -318,7 +318,8 @@ struct ForwardPlan {
 // (Q4_K, Q8_0) prefill kernel multiplies; 0 where that path does not apply.
 size_t kq_f16_stage_bytes(const Linear *L, int x_dtype, int64_t rows, int path) {
   const int fmt = L->desc.format;
-  if (path != DIALQ_PATH_GEMM || (fmt != DIALQ_FORMAT_Q4_K && fmt != DIALQ_FORMAT_Q8_0) || x_dtype != DIALQ_BF16)
+  if (path != DIALQ_PATH_GEMM || x_dtype != DIALQ_BF16 ||
+      (fmt != DIALQ_FORMAT_Q4_K && fmt != DIALQ_FORMAT_Q8_0 && fmt != DIALQ_FORMAT_Q6_K))
     return 0;
   return (size_t)(rows * L->desc.in_dim * 2 + 255) / 256 * 256 + (size_t)rows * sizeof(float);
 }

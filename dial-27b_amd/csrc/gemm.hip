@@ -848,6 +848,66 @@ struct KqFmt<DIALQ_FORMAT_Q8_0> {
   }
 };
 
+template <>
+struct KqFmt<DIALQ_FORMAT_Q6_K> {
+  static constexpr int CHUNK = 256, TILE = 3072, AUX = 288;
+  // Stage i of the chunk: 32-k slices 2i, 2i + 1 (t = 4hh + qd, hh = i / 2,
+  // qd = 2(i % 2) + s / 2 for step s): the low nibble (i even) or high nibble
+  // (i odd) of ql bytes 8(s / 2)..+7 in plane hh, with bits 2qd of the qh
+  // bytes 8hh..8hh+7 (plane 2) on top; sub-block 4i + s is step s.
+  struct Slot {
+    u32x4 ql[2];   // lane groups h and 2 + h: plane hh, 16 bytes
+    u32x2 qh[2];   // the same lanes: plane 2, bytes 8hh..8hh+7
+    uint32_t sc;   // i8 scales of sub-blocks 4i..4i+3 of the lane's row
+    uint32_t d;    // the row's f16 d
+  };
+  struct Sc {
+    float s1[4];  // d * sc of the stage's four sub-blocks (exact)
+  };
+  static __device__ __forceinline__ void fetch(Slot &sl, rsrc_t rt, rsrc_t ra, uint32_t tile, int i, bool valid, int r,
+                                               int h) {
+    const uint32_t hh = (uint32_t)(i / 2);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t lo = tile * 3072u + 16u * (uint32_t)(r + 16 * (2 * e + h));
+      sl.ql[e] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rt, valid ? (int)(lo + hh * 1024u) : (int)kOOB, 0, 0));
+      sl.qh[e] = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(rt, valid ? (int)(lo + 2048u + 8u * hh) : (int)kOOB, 0, 0));
+    }
+    const uint32_t ab = tile * 288u;
+    sl.sc = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ra, valid ? (int)(ab + 16u * (uint32_t)r + 4u * (uint32_t)i)
+                                                                   : (int)kOOB, 0, 0);
+    sl.d = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(ra, valid ? (int)(ab + 256u + 2u * (uint32_t)r) : (int)kOOB,
+                                                          0, 0);
+  }
+  template <int I>
+  static __device__ __forceinline__ Sc scales(const Slot &sl) {
+    const float d = f16_bits_to_f32(sl.d & 0xffffu);
+    Sc o;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) o.s1[s] = d * sbyte_f32(sl.sc, s);
+    return o;
+  }
+  // f32 weights d*sc*(q6 - 32) of step j, each a single rounding of the
+  // exact value
+  template <int I>
+  static __device__ __forceinline__ void weights_i(const Slot &sl, const Sc &sc, int j, float (&wv)[8]) {
+    constexpr int NIB = 4 * (I % 2);
+    const int qd = 2 * (I % 2) + (j >> 1);
+    const float s1 = sc.s1[j], off = -32.0f * s1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t v = ((sl.ql[j & 1][2 * (j >> 1) + i] >> NIB) & 0x0f0f0f0fu) |
+                         (((sl.qh[j & 1][i] >> (2 * qd)) & 0x03030303u) << 4);
+      wv[4 * i] = __builtin_fmaf(s1, (float)(v & 0xffu), off);
+      wv[4 * i + 1] = __builtin_fmaf(s1, (float)((v >> 8) & 0xffu), off);
+      wv[4 * i + 2] = __builtin_fmaf(s1, (float)((v >> 16) & 0xffu), off);
+      wv[4 * i + 3] = __builtin_fmaf(s1, (float)(v >> 24), off);
+    }
+  }
+};
+
 template <int FMT, int ACT, int MT, int OCC, bool SWI>
 __global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
   static_assert(ACT == DIALQ_BF16 || ACT == kActF16N, "bf16 or f16 activations");
@@ -953,7 +1013,8 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         float wv[8];
-        F::weights(cur.q[q], sc[q], j, wv);
+        if constexpr (FMT == DIALQ_FORMAT_Q6_K) F::template weights_i<I>(cur.q[q], sc[q], j, wv);
+        else F::weights(cur.q[q], sc[q], j, wv);
         kq_pack<ACT>(wv, bh[q], bl[q]);
       }
 #pragma unroll
@@ -1075,7 +1136,7 @@ static int64_t gemm32_col_tiles(const WeightView &w) { return w.pair ? (w.pair +
 static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt) {
   Gemm32Plan g;
   const bool small = M <= kGemm32SmallRows;
-  const bool kq = w.fmt == DIALQ_FORMAT_Q4_K || w.fmt == DIALQ_FORMAT_Q8_0;
+  const bool kq = w.fmt == DIALQ_FORMAT_Q4_K || w.fmt == DIALQ_FORMAT_Q8_0 || w.fmt == DIALQ_FORMAT_Q6_K;
   g.mt = small ? 1 : kq ? GEMMKQ_MT : M >= kGemm32TallRows ? 4 : GEMM32_MT;
   g.ks = small ? 2 : GEMM32_KS;  // byte formats; a Q4_K stage is one 64-k quarter chunk
   const int64_t rows = 32 * g.mt;
@@ -1084,7 +1145,7 @@ static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt) {
   const int64_t occ = kq ? GEMMKQ_OCC : g.mt == 4 ? 2 : GEMM32_OCC;
   const int64_t cus = device_cus(), slots = occ * cus;
   if (small ? g.tiles * 2 <= slots : g.tiles * 2 < cus) {
-    const int64_t steps = w.k_chunks * (w.fmt == DIALQ_FORMAT_Q4_K ? 4 : 1);
+    const int64_t steps = w.k_chunks * (w.fmt == DIALQ_FORMAT_Q4_K || w.fmt == DIALQ_FORMAT_Q6_K ? 4 : 1);
     int64_t P = slots / g.tiles, cap = steps / kGemm32MinChunks;
     if (cap > (small ? 8 : 4)) cap = small ? 8 : 4;
     if (P > cap) P = cap;
@@ -1094,14 +1155,16 @@ static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt) {
   return g;
 }
 
-// The 32x32 kernels: W8A16 / FP8_ROW (k_gemm32) and Q4_K / Q8_0 with bf16
-// or f16 activations (k_gemm_kq; f32 activations keep the exact k_gemm).
+// The 32x32 kernels: W8A16 / FP8_ROW (k_gemm32) and Q4_K / Q8_0 / Q6_K with
+// bf16 or f16 activations (k_gemm_kq; f32 activations keep the exact k_gemm).
 static bool gemm32_applies(const WeightView &w, int x_dtype) {
   if (w.fmt == DIALQ_FORMAT_W8A16 || w.fmt == DIALQ_FORMAT_FP8_ROW) return w.n_strips * w.k_chunks * 1024 <= 0xffffffffLL;
   if (w.fmt == DIALQ_FORMAT_Q4_K)
     return x_dtype != DIALQ_F32 && w.n_strips * w.k_chunks * 2048 <= 0xffffffffLL;
   if (w.fmt == DIALQ_FORMAT_Q8_0)
     return x_dtype != DIALQ_F32 && w.n_strips * w.k_chunks * 1024 <= 0xffffffffLL;
+  if (w.fmt == DIALQ_FORMAT_Q6_K)
+    return x_dtype != DIALQ_F32 && w.n_strips * w.k_chunks * 3072 <= 0xffffffffLL;
   return false;
 }
 
@@ -1174,7 +1237,8 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
   typedef GemmShape<FMT, ACT> S;
   if ((int64_t)S::ROWS * w.K * ActTraits<ACT>::BYTES > 0xffffffffLL) return hipErrorInvalidValue;
   constexpr bool BYTE = FMT == DIALQ_FORMAT_W8A16 || FMT == DIALQ_FORMAT_FP8_ROW;
-  constexpr bool KQ = (FMT == DIALQ_FORMAT_Q4_K || FMT == DIALQ_FORMAT_Q8_0) && (ACT == DIALQ_BF16 || ACT == kActF16N);
+  constexpr bool KQ = (FMT == DIALQ_FORMAT_Q4_K || FMT == DIALQ_FORMAT_Q8_0 || FMT == DIALQ_FORMAT_Q6_K) &&
+                      (ACT == DIALQ_BF16 || ACT == kActF16N);
   if constexpr (BYTE || KQ) {
     if (gemm32_applies(w, ACT == DIALQ_F32 ? DIALQ_F32 : DIALQ_BF16)) {
       const Gemm32Plan g = gemm32_plan(M, w, grp ? grp->tbase[grp->nm] : gemm32_col_tiles(w));
@@ -1244,6 +1308,10 @@ hipError_t launch_gemm_group(const WeightView *ws, void *const *ys, int n, const
       break;
     case DIALQ_FORMAT_Q8_0:
       r = gemm_act<DIALQ_FORMAT_Q8_0>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g,
+                                      yrow);
+      break;
+    case DIALQ_FORMAT_Q6_K:
+      r = gemm_act<DIALQ_FORMAT_Q6_K>(ws[0], x, x_dtype, M, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g,
                                       yrow);
       break;
   }

@@ -4,7 +4,7 @@ x, the replacement of QkvProjection::Split / MlpGateUpProjection::Split
 member (mixed formats, prefill formats without a grouped kernel) must
 equal each member's own dialq_linear_forward_ex output bit for bit (the
 same kernels with a strided output).  A grouped launch -- decode, or
-prefill of W8A16 / FP8_ROW / Q4_K and Q8_0 (bf16, f16 x) / FP8_BLOCK and MXFP4
+prefill of W8A16 / FP8_ROW / Q4_K, Q8_0 and Q6_K (bf16, f16 x) / FP8_BLOCK and MXFP4
 native -- sizes its split along K from all the group's tiles, so a
 member's f32 sum may be split differently than in its own launch: those
 columns must agree with its own forward to f32 rounding (rel-L2 <= 2e-4 in
@@ -69,7 +69,7 @@ def test_group_equals_separate(fmts, rows, torch_dev):
     for x_dtype in (dq.BF16, dq.F16, dq.F32):
         # decode: one grouped launch per row group of 16 (8 for the k-quants
         # at M <= 8); prefill: one launch where a grouped kernel exists
-        prefill_grouped = fmts[0] in (dq.W8A16, dq.MXFP4) or (fmts[0] == dq.Q4_K and x_dtype != dq.F32)
+        prefill_grouped = fmts[0] in (dq.W8A16, dq.MXFP4) or (fmts[0] in (dq.Q4_K, dq.Q6_K) and x_dtype != dq.F32)
         grouped = len(set(fmts)) == 1 and (rows <= 16 or prefill_grouped)
         xt = to_torch(x, x_dtype, torch_dev)
         want = _separate(lins, xt, dq.BF16, dq.PATH_AUTO, torch_dev)

@@ -1,5 +1,6 @@
-"""GGUF prefill (k_gemm_kq: Q4_K, Q8_0): each weight is dequantized in f32
-(Q4_K d*sc*q - dmin*m, Q8_0 d*q) and multiplied as f16 against f16
+"""GGUF prefill (k_gemm_kq: Q4_K, Q8_0, Q6_K): each weight is dequantized in
+f32 (Q4_K d*sc*q - dmin*m, Q8_0 d*q, Q6_K d*sc*(q - 32)) and multiplied as
+f16 against f16
 activations -- the weight DIAL's GGUF prefill builds once,
 build_worker_gguf_fp16_prefill_linear
 (qwen3_vl/worker_gguf.rs:426-455).  bf16 activations are first written as
@@ -27,7 +28,8 @@ from helpers import make_weight, reference_product, to_torch
 pytestmark = pytest.mark.gpu
 
 
-FMTS = [dq.Q4_K, dq.Q8_0]
+FMTS = [dq.Q4_K, dq.Q8_0, dq.Q6_K]
+IDS = ["q4_k", "q8_0", "q6_k"]
 
 
 def _case(n, k, seed, fmt=dq.Q4_K):
@@ -35,7 +37,7 @@ def _case(n, k, seed, fmt=dq.Q4_K):
     return dq.Linear.create(fmt, n, k, raw, scales, **kw), deq
 
 
-@pytest.mark.parametrize("fmt", FMTS, ids=["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS, ids=IDS)
 @pytest.mark.parametrize("m", [17, 40, 96, 97, 130, 256, 300])
 @pytest.mark.parametrize("n,k", [(320, 512), (1024, 5120)], ids=["k512", "k5120"])
 def test_kq_prefill_weights_and_parity(fmt, m, n, k, torch_dev):
@@ -62,7 +64,7 @@ def test_kq_prefill_weights_and_parity(fmt, m, n, k, torch_dev):
         assert O.rel_l2(yo.float().cpu().numpy(), reference_product(x, O.round_f16(deq), y_dtype)) <= 1e-3
 
 
-@pytest.mark.parametrize("fmt", FMTS, ids=["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS, ids=IDS)
 def test_kq_prefill_f32_activations_stay_exact(fmt, torch_dev):
     # f32 activations keep the exact weight-only kernel
     import torch
@@ -74,7 +76,7 @@ def test_kq_prefill_f32_activations_stay_exact(fmt, torch_dev):
     assert O.rel_l2(y.cpu().numpy(), O.matmul_f64(x, deq)) <= 1e-5
 
 
-@pytest.mark.parametrize("fmt", FMTS, ids=["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS, ids=IDS)
 @pytest.mark.parametrize("m", [33, 200])
 def test_kq_prefill_swiglu(fmt, m, torch_dev):
     import torch
@@ -121,7 +123,7 @@ def test_q4k_prefill_split_graph_replay(torch_dev):
     assert O.rel_l2(want[:8].float().cpu().numpy(), ref) <= 1e-3
 
 
-@pytest.mark.parametrize("fmt", FMTS, ids=["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS, ids=IDS)
 def test_kq_prefill_bf16_rows_beyond_f16_range(fmt, torch_dev):
     # bf16 rows far above and below f16's range are scaled by a power of
     # two for the f16 kernel and scaled back in the epilogue: every row
@@ -147,7 +149,7 @@ def test_kq_prefill_bf16_rows_beyond_f16_range(fmt, torch_dev):
         assert O.rel_l2(got[r], want[r]) <= 2e-5, (r, mult[r])
 
 
-@pytest.mark.parametrize("fmt", FMTS, ids=["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS, ids=IDS)
 def test_kq_prefill_noalloc_falls_back_to_hi_lo(fmt, torch_dev):
     # 1024 rows at K = 17408: the f16 copy of x (35.7 MB) does not fit the
     # allocation-free entry point's array, which runs the hi + lo kernel on

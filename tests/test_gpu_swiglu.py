@@ -57,7 +57,7 @@ def _check(lin, deq, m, path, x_dtype, y_dtype, dev, seed, native=None):
     got = yt.float().cpu().numpy()
     assert np.all(np.isfinite(got))
     xr = _native_x(native, xe) if native else xe
-    if lin.desc.format in (dq.Q4_K, dq.Q8_0) and path == dq.PATH_GEMM and x_dtype != dq.F32:
+    if lin.desc.format in (dq.Q4_K, dq.Q8_0, dq.Q6_K) and path == dq.PATH_GEMM and x_dtype != dq.F32:
         deq = O.round_f16(deq)  # the GGUF prefill multiplies the f16-dequantized weight
     ref = _rounded(O.swiglu(O.matmul_f64(xr, deq)), y_dtype)
     return O.rel_l2(got, ref)
