@@ -19,7 +19,7 @@ Layer copies rotate so the weight working set (COPIES x 341 MB) exceeds the
 weight bytes streamed / wall time of the timed steps, in GB/s.  Extra keys
 report the same decode for Q4_K / Q8_0 / FP8-128 / MXFP4, the prefill GEMM
 TFLOP/s (W8A16, Q4_K and Q8_0 at M = 2048 -- Q4_K also with f16 activations, the dtype
-of DIAL's GGUF worker --, FP8-128 and MXFP4 native at M = 1024; q / k / v
+of DIAL's GGUF worker, and Q6_K on the gate shape from synthetic blocks --, FP8-128 and MXFP4 native at M = 1024; q / k / v
 and gate / up as grouped forwards like the decode step, and as seven
 forwards in prefill_tflops_ungrouped; also over
 the fused qkv / o / gate_up / down projections DIAL's layers call, with and
@@ -547,17 +547,33 @@ def cpu_baseline(seconds):
 
 # (key, rows, path, peak, activation dtype).  q4_k_f16act: Q4_K with the f16
 # activations of DIAL's GGUF worker, whose prefill multiplies f16-dequantized
-# weights (qwen3_vl/worker_gguf.rs:426-455).
+# weights (qwen3_vl/worker_gguf.rs:426-455).  q6_k: the second block type of a
+# Q4_K_M file (worker_gguf.rs:536-540).
 PREFILL_GATE = [("w8a16", 2048, "PATH_GEMM", "bf16", "bfloat16"), ("q4_k", 2048, "PATH_GEMM", "bf16", "bfloat16"),
                 ("q4_k_f16act", 2048, "PATH_GEMM", "f16", "float16"), ("q8_0", 2048, "PATH_GEMM", "f16", "bfloat16"),
+                ("q6_k", 2048, "PATH_GEMM", "f16", "bfloat16"),
                 ("fp8_block", 1024, "PATH_GEMM_NATIVE", "fp8", "bfloat16"),
                 ("mxfp4", 1024, "PATH_GEMM_NATIVE", "fp4", "bfloat16")]
 
 
+def q6_k_synthetic_blocks(n, k, seed=23):
+    """Synthetic Q6_K weight bytes (Q6_K arrives only from GGUF files and has
+    no quantizer here): uniform 6-bit codes and i8 sub-block scales, the f16
+    super-block scale d in [1e-4, 3e-4)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    nb = n * (k // 256)
+    b = rng.integers(0, 256, (nb, 210), dtype=np.uint8)
+    b[:, 208:210] = (1e-4 * rng.uniform(1.0, 3.0, nb)).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return b.reshape(n, (k // 256) * 210)
+
+
 def prefill_gate_linears(dq, torch, dev, name):
+    _, n, k = DOM
+    if name == "q6_k":
+        return dq.Linear.create(dq.Q6_K, n, k, q6_k_synthetic_blocks(n, k))
     fmt = {"w8a16": dq.W8A16, "q4_k": dq.Q4_K, "q4_k_f16act": dq.Q4_K, "q8_0": dq.Q8_0, "fp8_block": dq.FP8_BLOCK,
            "mxfp4": dq.MXFP4}[name]
-    _, n, k = DOM
     g = torch.Generator(device=dev).manual_seed(23)
     return dq.Linear.quantize(fmt, torch.randn(n, k, device=dev, generator=g) * 0.02, scale_dtype=dq.BF16)
 

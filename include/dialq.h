@@ -179,9 +179,9 @@ int dialq_linear_forward_ex(void *linear, const void *x, int32_t x_dtype,
  * to four consecutive same-format members in one launch (x staged once per
  * workgroup, one launch's fill and drain instead of one per member); the
  * prefill paths run the column tiles of up to four consecutive same-format
- * members in one GEMM launch (W8A16, FP8_ROW, Q4_K and Q8_0 with bf16 / f16 x;
- * FP8_BLOCK and MXFP4 native on x quantized once; the first member's
- * scratch serves the launch).  A grouped launch splits its sums along K
+ * members in one GEMM launch (W8A16, FP8_ROW, Q4_K, Q8_0 and Q6_K with
+ * bf16 / f16 x; FP8_BLOCK and MXFP4 native on x quantized once; the first
+ * member's scratch serves the launch).  A grouped launch splits its sums along K
  * from the group's tile count, so a member may differ from its own forward
  * by f32 rounding.  Other cases run one launch per member, each writing
  * its columns of y, with the same kernels and results as
