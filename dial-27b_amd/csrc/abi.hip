@@ -374,10 +374,12 @@ ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int6
     else path = DIALQ_PATH_GEMM;
   }
   pl.path = path;
+  // every kernel addresses the resident tiles with 32-bit buffer offsets and
+  // marks masked loads with an offset of 2^31, past any weight below 2 GiB
+  if (L->tiles.n >= ((size_t)1 << 31))
+    fail("%s kernel addresses weights with 32-bit offsets: %zu resident bytes exceed 2 GiB; split the "
+         "output dimension", path == DIALQ_PATH_GEMV ? "decode" : "prefill", L->tiles.n);
   if (path == DIALQ_PATH_GEMV) {
-    if (L->tiles.n >= ((size_t)1 << 31))
-      fail("decode kernel addresses weights with 32-bit offsets: %zu resident bytes exceed 2 GiB; split the "
-           "output dimension", L->tiles.n);
     pl.gemv_ws = gemv_workspace_bytes(w, x_dtype, rows);
     pl.gemv_cnt = (size_t)(L->n_strips + 2);
   } else if (path == DIALQ_PATH_GEMM_NATIVE) {

@@ -538,14 +538,23 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   const int mrows = (int)((p.M - m0) < ROWS ? (p.M - m0) : ROWS);
   const rsrc_t rx = make_rsrc((const uint8_t *)p.x + (int64_t)m0 * K * BY, (uint32_t)((int64_t)mrows * K * BY));
 
+  // Per-lane load bases, computed once: the loop adds a uniform stage offset
+  // and compares it with a per-lane limit, so it needs no index arithmetic
+  // and no reload of the weight view.  An activation piece is live while its
+  // k is below kend (which also ends it past the last stage).
   XRaw<ACT> apre[PIECES];
+  uint32_t abase[PIECES];
+  int alim[PIECES];
+#pragma unroll
+  for (int q = 0; q < PIECES; ++q) {
+    const int pc = tid + q * 256, row = pc / (SK / 8), kk = (pc % (SK / 8)) * 8;
+    abase[q] = (uint32_t)((row * K + c0 * CHUNK + kk) * BY);
+    alim[q] = kend - c0 * CHUNK - kk;
+  }
   auto fetch_a = [&](int st) {
 #pragma unroll
-    for (int q = 0; q < PIECES; ++q) {
-      const int pc = tid + q * 256, row = pc / (SK / 8), kk = (pc % (SK / 8)) * 8;
-      const int k = c0 * CHUNK + st * SK + kk;
-      apre[q] = xraw_load<ACT>(rx, (st < nstage && k < kend) ? (uint32_t)((row * K + k) * BY) : kOOB);
-    }
+    for (int q = 0; q < PIECES; ++q)
+      apre[q] = xraw_load<ACT>(rx, st * SK < alim[q] ? abase[q] + (uint32_t)(st * SK * BY) : kOOB);
   };
   auto store_a = [&](int buf) {
     uint16_t *base = lds + buf * BUF;
@@ -557,14 +566,21 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
       if constexpr (PARTS == 2) *(u32x4 *)(base + (ROWS + row) * STRIDE + kk) = o.lo;
     }
   };
-  // weight bytes of (stage st, 16-k step j, column tile q) for this lane
+  // weight bytes of (stage st, 16-k step j, column tile q) for this lane:
+  // bbase[q] + the chunk's offset within the piece; a strip past the weight
+  // keeps kOOB, which stays out of range under any in-piece offset
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  uint32_t bbase[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int strip = s0 + 2 * q + sub;
+    bbase[q] = strip < slim ? ((uint32_t)strip * (uint32_t)w.k_chunks + (uint32_t)c0) * 1024u +
+                                  (uint32_t)(r * 16 + 8 * h)
+                            : kOOB;
+  }
   auto bload = [&](int st, int j, int q) -> u32x2 {
-    const int c = c0 + st * KS + j / 4, strip = s0 + 2 * q + sub;
-    const bool valid = st < nstage && c < c1 && strip < slim;
-    const uint32_t off = valid ? ((uint32_t)strip * (uint32_t)w.k_chunks + (uint32_t)c) * 1024u +
-                                     (uint32_t)(((j % 4) * 16 + r) * 16 + 8 * h)
-                               : kOOB;
+    const int cc = st * KS + j / 4;  // chunk within the piece (uniform)
+    const uint32_t off = cc < kc ? bbase[q] + (uint32_t)(cc * 1024 + (j % 4) * 256) : kOOB;
     return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rt, (int)off, 0, 0));
   };
   u32x2 wb[2][STEPS][NQ];
@@ -946,14 +962,22 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
   const int mrows = (int)((p.M - m0) < ROWS ? (p.M - m0) : ROWS);
   const rsrc_t rx = make_rsrc((const uint8_t *)p.x + (int64_t)m0 * K * BY, (uint32_t)((int64_t)mrows * K * BY));
 
+  // Per-lane load bases, computed once (as in k_gemm32): the loop adds a
+  // uniform stage offset, and an activation piece is live while its k is
+  // below kend.
   XRaw<ACT> apre[PIECES];
+  uint32_t abase[PIECES];
+  int alim[PIECES];
+#pragma unroll
+  for (int q = 0; q < PIECES; ++q) {
+    const int pc = tid + q * 256, row = pc / (SK / 8), kk = (pc % (SK / 8)) * 8;
+    abase[q] = (uint32_t)((row * K + c0 * F::CHUNK + kk) * BY);
+    alim[q] = kend - c0 * F::CHUNK - kk;
+  }
   auto fetch_a = [&](int st) {
 #pragma unroll
-    for (int q = 0; q < PIECES; ++q) {
-      const int pc = tid + q * 256, row = pc / (SK / 8), kk = (pc % (SK / 8)) * 8;
-      const int k = c0 * F::CHUNK + st * SK + kk;
-      apre[q] = xraw_load<ACT>(rx, (st < nstage && k < kend) ? (uint32_t)((row * K + k) * BY) : kOOB);
-    }
+    for (int q = 0; q < PIECES; ++q)
+      apre[q] = xraw_load<ACT>(rx, st * SK < alim[q] ? abase[q] + (uint32_t)(st * SK * BY) : kOOB);
   };
   auto store_a = [&](int buf) {
     uint16_t *base = lds + buf * BUF;
@@ -967,15 +991,19 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
   struct Slot {
     typename F::Slot q[NQ];
   };
-  auto fetch_b = [&](Slot &sl, int st) {
-    const int c = c0 + st / SPC, i = st % SPC;
+  uint32_t tbase[NQ];  // tile index of this lane's strip at chunk c0
+  bool slive[NQ];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      const int strip = s0 + 2 * q + sub;
-      const bool valid = st < nstage && strip < slim;
-      const uint32_t tile = (uint32_t)strip * (uint32_t)w.k_chunks + (uint32_t)c;
-      F::fetch(sl.q[q], rt, ra, tile, i, valid, r, h);
-    }
+  for (int q = 0; q < NQ; ++q) {
+    const int strip = s0 + 2 * q + sub;
+    slive[q] = strip < slim;
+    tbase[q] = (uint32_t)strip * (uint32_t)w.k_chunks + (uint32_t)c0;
+  }
+  auto fetch_b = [&](Slot &sl, int st) {
+    const int i = st % SPC;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+      F::fetch(sl.q[q], rt, ra, tbase[q] + (uint32_t)(st / SPC), i, st < nstage && slive[q], r, h);
   };
 
   f32x16 acc[MT][NQ];
@@ -1478,14 +1506,17 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
     // DEPTH) into the double-buffered LDS stage (buffer = (c - c0) & 1).
     u32x4 apre[DEPTH][PIECES];
     uint32_t spre[DEPTH];
+    uint32_t abase[PIECES];
+#pragma unroll
+    for (int q = 0; q < PIECES; ++q) {
+      const int pc = tid + q * 256, row = pc / (ROWB / 16), kb = (pc % (ROWB / 16)) * 16;
+      abase[q] = (uint32_t)row * pitch + (uint32_t)kb;
+    }
+    const uint32_t xsbase = tid < ROWS ? (uint32_t)(tid * (p.k_pad / 32)) : kOOB;
     auto fetch_a = [&](int aslot, int c) {
 #pragma unroll
-      for (int q = 0; q < PIECES; ++q) {
-        const int pc = tid + q * 256, row = pc / (ROWB / 16), kb = (pc % (ROWB / 16)) * 16;
-        apre[aslot][q] = bload16(rx, c < c1 ? (uint32_t)row * pitch + (uint32_t)(c * ROWB + kb) : kOOB);
-      }
-      if constexpr (!FP8)
-        spre[aslot] = bload4(rs, (c < c1 && tid < ROWS) ? (uint32_t)(tid * (p.k_pad / 32) + c * 4) : kOOB);
+      for (int q = 0; q < PIECES; ++q) apre[aslot][q] = bload16(rx, c < c1 ? abase[q] + (uint32_t)(c * ROWB) : kOOB);
+      if constexpr (!FP8) spre[aslot] = bload4(rs, c < c1 ? xsbase + (uint32_t)(c * 4) : kOOB);
     };
     auto store_a = [&](int aslot, int buf) {
 #pragma unroll
@@ -1499,19 +1530,23 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
     // Weights: wb[slot][j][q] is the B operand of step j, column tile q (fp4
     // uses its low 4 dwords).  A slot is refilled in place, after the MFMAs
     // that read it, so the ring keeps its registers across the loop.
-    auto bload = [&](int c, int j, int q, int i) -> u32x4 {
+    // Per-lane bases of this lane's strips, computed once: a load adds the
+    // chunk's uniform offset; a strip past the weight keeps kOOB, which
+    // stays out of range under any in-weight offset.
+    uint32_t bbase[2], sbase[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
       const int strip = s0 + 2 * q + sub;
-      const bool valid = c < c1 && strip < slim;
+      const bool live = strip < slim;
+      bbase[q] = live ? (uint32_t)strip * (uint32_t)kc * TILE + (uint32_t)((h * 16 + r) * 16) : kOOB;
+      sbase[q] = live ? (uint32_t)strip * (uint32_t)kc * 64u + (uint32_t)(r * 4) : kOOB;
+    }
+    auto bload = [&](int c, int j, int q, int i) -> u32x4 {
       // slot 16(2j + h) + r; its 16-byte half i lives in plane i
-      const uint32_t off = valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * TILE +
-                                       (uint32_t)(1024 * i + ((2 * j + h) * 16 + r) * 16)
-                                 : kOOB;
-      return bload16(rt, off);
+      return bload16(rt, c < c1 ? bbase[q] + (uint32_t)(c * TILE + 1024 * i + 512 * j) : kOOB);
     };
     auto sbload = [&](int c, int q) -> uint32_t {  // MXFP4 weight scales of row r, k blocks 0..3
-      const int strip = s0 + 2 * q + sub;
-      const bool valid = c < c1 && strip < slim;
-      return bload4(rb, valid ? ((uint32_t)strip * (uint32_t)kc + (uint32_t)c) * 64u + (uint32_t)(r * 4) : kOOB);
+      return bload4(rb, c < c1 ? sbase[q] + (uint32_t)(c * 64) : kOOB);
     };
     i32x8 wb[DEPTH][2][2];
     uint32_t wsb[DEPTH][2];
