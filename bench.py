@@ -649,6 +649,45 @@ def time_prefill_gate(dq, torch, dev, reps=10):
     return out
 
 
+def time_dense_library(torch, dev, reps=20):
+    """The vendor library's dense GEMMs on the gate shape, on this GPU in
+    this run (torch.matmul / torch._scaled_mm -> hipBLASLt): bf16 and f16
+    at M = 2048 and per-tensor-scaled fp8 e4m3 at M = 1024 -- the dense
+    products the quantized kernels' MFMA fractions can be read against."""
+    _, n, k = DOM
+    out = {}
+
+    def rate(m, fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        e1.synchronize()
+        secs = e0.elapsed_time(e1) * 1e-3 / reps
+        return round(2.0 * m * n * k / secs / 1e12, 1)
+
+    for dt in ("bfloat16", "float16"):
+        a_ = torch.randn(2048, k, device=dev).to(getattr(torch, dt))
+        b_ = torch.randn(n, k, device=dev).to(getattr(torch, dt))
+        out[("bf16" if dt == "bfloat16" else "f16") + "_m2048"] = rate(2048, lambda: torch.matmul(a_, b_.t()))
+        del a_, b_
+    try:
+        a_ = torch.randn(1024, k, device=dev).to(torch.float8_e4m3fn)
+        b_ = torch.randn(n, k, device=dev).to(torch.float8_e4m3fn)
+        one = torch.tensor(1.0, device=dev)
+        out["fp8_e4m3_m1024"] = rate(1024, lambda: torch._scaled_mm(a_, b_.t(), scale_a=one, scale_b=one,
+                                                                    out_dtype=torch.bfloat16))
+        del a_, b_
+    except Exception as ex:  # a torch build without the fp8 GEMM
+        out["fp8_e4m3_m1024"] = None
+        out["fp8_error"] = str(ex)[:120]
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -818,6 +857,10 @@ def main():
         torch.cuda.empty_cache()
 
     roof_prefill = time_prefill_gate(dq, torch, dev) if sweep else None
+    dense_lib = time_dense_library(torch, dev) if sweep else None
+    if dense_lib:
+        print("# dense library GEMMs (gate 17408x5120): " + ", ".join(f"{k_} {v}" for k_, v in dense_lib.items()),
+              file=sys.stderr, flush=True)
     if roof_prefill:
         print("# prefill roofline (gate 17408x5120): " + ", ".join(
             f"{k_} {v['achieved']} TFLOP/s ({100 * v['frac']:.1f} %)" for k_, v in roof_prefill.items()),
@@ -859,6 +902,7 @@ def main():
             "us_per_launch": round(dom_secs * 1e6, 2),
         },
         "roofline_prefill": roof_prefill,
+        "dense_library_tflops_gate": dense_lib,
         "cpu_baseline": cpu,
         **extra,
     }

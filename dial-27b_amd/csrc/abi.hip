@@ -358,8 +358,10 @@ WeightView forward_view(const Linear *L, bool swiglu) {
 
 // stage_f16: a Q4_K / Q8_0 GEMM on bf16 x runs the f16 kernel on an f16 copy of x
 // (false: the bf16 hi / lo kernel, no copy).
+// tail: split the tiles of a partial last round of workgroups (more
+// scratch; false where the allocation-free entry point has no room).
 ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int64_t rows, int path,
-                         bool stage_f16 = true) {
+                         bool stage_f16 = true, bool tail = true) {
   const int fmt = L->desc.format;
   ForwardPlan pl;
   if (path == DIALQ_PATH_AUTO) {
@@ -393,7 +395,7 @@ ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int6
   } else if (path == DIALQ_PATH_GEMM) {
     if (stage_f16) pl.xh = kq_f16_stage_bytes(L, x_dtype, rows, path);
     // split-K partials of few-tile launches (the f16 kernel's tiling when x is staged as f16)
-    gemm_workspace(rows, w, pl.xh ? DIALQ_F16 : x_dtype, pl.part, pl.ncnt);
+    gemm_workspace(rows, w, pl.xh ? DIALQ_F16 : x_dtype, pl.part, pl.ncnt, tail);
   } else {
     fail("unknown path %d", path);
   }
@@ -744,11 +746,15 @@ void forward_noalloc_impl(Linear *L, const void *x, int32_t x_dtype, int64_t row
   const size_t xbytes = (size_t)(rows * K) * xs;
   const bool stage_x = ((uintptr_t)x) & 15u;
   ForwardPlan pl = plan_forward(L, w, x_dtype, rows, path);
-  // a Q4_K / Q8_0 prefill on bf16 x whose f16 copy does not fit runs the bf16 hi / lo
-  // kernel on x as it is
-  if (pl.xh && kNoAllocCntBytes + up(pl.codes + pl.xscale) + up(pl.part) + up(pl.xh) +
-                       (stage_x ? up(xbytes) : 0) > kNoAllocScratchBytes)
-    pl = plan_forward(L, w, x_dtype, rows, path, false);
+  auto fits = [&](const ForwardPlan &q) {
+    return kNoAllocCntBytes + up(q.gemv_ws) + up(q.codes + q.xscale) + up(q.part) + up(q.xh) +
+               (stage_x ? up(xbytes) : 0) <= kNoAllocScratchBytes;
+  };
+  // the tail split's partials first give way (the launch then keeps the
+  // last round's tiles whole), then a Q4_K / Q8_0 prefill on bf16 x whose
+  // f16 copy does not fit runs the bf16 hi / lo kernel on x as it is
+  if (!fits(pl)) pl = plan_forward(L, w, x_dtype, rows, path, true, false);
+  if (pl.xh && !fits(pl)) pl = plan_forward(L, w, x_dtype, rows, path, false, false);
   const size_t cnt_ints = pl.path == DIALQ_PATH_GEMV ? pl.gemv_cnt : pl.ncnt;
   if (cnt_ints * sizeof(int) > kNoAllocCntBytes)
     fail("dialq_linear_forward_noalloc: this %s weight needs %zu counters; its scratch holds %zu (out_dim up to "

@@ -55,6 +55,9 @@ struct GemmParams {
   int P = 1;
   float *part = nullptr;
   int *cnt = nullptr;
+  // Tail split (W > 0, P > 1): tiles [0, W) whole, the rest in P pieces;
+  // `part` / `cnt` are then indexed by the split tile's index past W.
+  int W = 0;
   GemmGroup g;  // k_gemm32, k_gemm_kq
   // k_gemm_kq: per-row output multipliers (bf16 activations scaled into f16
   // range, 2^e per row); null = 1
@@ -153,6 +156,43 @@ __device__ __forceinline__ void tile_coords(int L, int nt, int mt, int &tm, int 
 }
 __device__ __forceinline__ void tile_of(int b, int G, int nt, int mt, int &tm, int &tn) {
   tile_coords(xcd_rank(b, G), nt, mt, tm, tn);
+}
+
+// Split schedule of a launch over nt x mtiles tiles:
+//   P == 1            whole tiles in the XCD-aware order of tile_of;
+//   P > 1, W == 0     every tile split along K into P pieces (launches of
+//                     few tiles): units go (row block, piece, column tile)
+//                     over XCD-contiguous ranks, so the row blocks and pieces
+//                     of one column tile run on one XCD at once and share
+//                     its weight and activation lines in that L2;
+//   P > 1, W > 0      tail split: workgroups [0, W) take logical tiles
+//                     [0, W) whole -- the full rounds of workgroup slots --
+//                     and the rest, the last partial round's tiles, are cut
+//                     into P pieces each, so that round ends after 1/P of a
+//                     tile's time instead of a whole one.  Workgroups are
+//                     dispatched in index order, so the pieces go last.
+// sidx: the split index of the tile (its partials and arrival counter), or
+// -1 for a whole tile.
+__device__ __forceinline__ void sched_tile(int nt, int mtiles, int P, int W, int &tm, int &tn, int &piece, int &sidx) {
+  const int b = blockIdx.x, G = gridDim.x;
+  piece = 0;
+  sidx = -1;
+  if (P == 1) {
+    tile_of(b, G, nt, mtiles, tm, tn);
+  } else if (W == 0) {
+    const int u = xcd_rank(b, G);
+    tm = u % mtiles;
+    piece = (u / mtiles) % P;
+    tn = u / (mtiles * P);
+    sidx = tn * mtiles + tm;
+  } else if (b < W) {
+    tile_of(b, W, nt, mtiles, tm, tn);
+  } else {
+    const int u = xcd_rank(b - W, G - W);  // the pieces of one tile on one XCD
+    piece = u % P;
+    sidx = u / P;
+    tile_coords(W + sidx, nt, mtiles, tm, tn);
+  }
 }
 
 // SwiGLU epilogue (w.pair > 0, fused gate_up weight with gate rows [0, I)
@@ -436,23 +476,6 @@ __device__ __forceinline__ f32x16 mfma32_op(u32x4 a, u32x4 b, f32x16 c) {
   else return mfma32(a, b, c);
 }
 
-// Tile of a 32x32-kernel workgroup: (row block tm, column tile tn) and, when
-// the launch splits tiles along K (P > 1), its piece.  Split launches walk
-// (row block, piece, column tile) over XCD-contiguous ranks, as the native
-// kernel's split tiles: the row blocks and pieces of one column tile run on
-// one XCD at once and share its weight and activation lines in that L2.
-__device__ __forceinline__ void split_tile_of(int nt, int mtiles, int P, int &tm, int &tn, int &piece) {
-  piece = 0;
-  if (P == 1) {
-    tile_of(blockIdx.x, gridDim.x, nt, mtiles, tm, tn);
-    return;
-  }
-  const int u = xcd_rank(blockIdx.x, gridDim.x);
-  tm = u % mtiles;
-  piece = (u / mtiles) % P;
-  tn = u / (mtiles * P);
-}
-
 // Split-K fixup of a 32x32-kernel tile t: each of its P pieces publishes
 // its partial (agent-scope relaxed stores, complete before the count); the
 // last to arrive adds the P partials in piece order -- the same order
@@ -513,13 +536,12 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
-  int tm, tn, piece;
+  int tm, tn, piece, sidx;
   const bool grp = !SWI && p.g.nm > 1;
   const int nt = grp ? p.g.tbase[p.g.nm] : SWI ? (int)((p.w.pair + 7) / 8) : (int)((p.w.n_strips + 15) / 16);
   const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
-  const int P = p.P;
-  split_tile_of(nt, mtiles, P, tm, tn, piece);
-  const int tg = tn * mtiles + tm;  // split-K counter: the global tile
+  sched_tile(nt, mtiles, p.P, p.W, tm, tn, piece, sidx);
+  const int P = sidx < 0 ? 1 : p.P;  // pieces of this workgroup's tile
   const int jm = grp ? group_member(p.g, tn) : 0;
   const WeightView &w = grp ? p.g.wm[jm] : p.w;
   void *const yout = grp ? p.g.ym[jm] : p.y;
@@ -648,7 +670,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   }
   if (st < nstage) stage(wb[0], st);
 
-  if (P > 1 && !split_fixup<MT, NQ>(p, acc, tg, piece, (int *)(lds + 2 * BUF))) return;
+  if (sidx >= 0 && !split_fixup<MT, NQ>(p, acc, sidx, piece, (int *)(lds + 2 * BUF))) return;
 
   if constexpr (SWI) {
     // y[m, j] = silu(gate) * up, one 32x32 tile per exchange
@@ -937,13 +959,12 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r = lane & 15, sub = (lane >> 4) & 1;
-  int tm, tn, piece;
+  int tm, tn, piece, sidx;
   const bool grp = !SWI && p.g.nm > 1;
   const int nt = grp ? p.g.tbase[p.g.nm] : SWI ? (int)((p.w.pair + 7) / 8) : (int)((p.w.n_strips + 15) / 16);
   const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
-  const int P = p.P;
-  split_tile_of(nt, mtiles, P, tm, tn, piece);
-  const int tg = tn * mtiles + tm;  // split-K counter: the global tile
+  sched_tile(nt, mtiles, p.P, p.W, tm, tn, piece, sidx);
+  const int P = sidx < 0 ? 1 : p.P;  // pieces of this workgroup's tile
   const int jm = grp ? group_member(p.g, tn) : 0;
   const WeightView &w = grp ? p.g.wm[jm] : p.w;
   void *const yout = grp ? p.g.ym[jm] : p.y;
@@ -1074,7 +1095,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
     if (st < nstage) stage(wb[0], st, std::integral_constant<int, 0>{});
   }
 
-  if (P > 1 && !split_fixup<MT, NQ>(p, acc, tg, piece, (int *)(lds + 2 * BUF))) return;
+  if (sidx >= 0 && !split_fixup<MT, NQ>(p, acc, sidx, piece, (int *)(lds + 2 * BUF))) return;
 
   if constexpr (SWI) {
     const int64_t I = w.pair * 16;
@@ -1152,16 +1173,50 @@ constexpr int64_t kGemm32SmallRows = 96;
 constexpr int64_t kGemm32TallRows = 2048;
 constexpr int kGemm32MinChunks = 20;  // 64-k steps per split-K piece, at least
 constexpr size_t kGemm32MaxPartBytes = (size_t)31 << 20;
-struct Gemm32Plan {
-  int mt, ks, P;
-  int64_t tiles;
-  size_t part_bytes() const { return P > 1 ? (size_t)(tiles * P) * 32 * mt * 256 * sizeof(float) : 0; }
+// Tail split of a launch of `tiles` tiles over `slots` resident workgroup
+// slots whose last round is at most half full (the 27B gate 17408x5120 at
+// M = 2048 in 128-row tiles: 1088 tiles, two rounds of 512 and 64 left):
+// the full rounds' tiles stay whole and the last round's are cut along K
+// into P pieces, at most kTailMaxPieces, each at least kTailMinChunks
+// chunks, their partial tiles within `budget` bytes.  The tail then takes
+// about 1/P of a tile's time plus the last piece's read-back of the
+// partials, instead of a whole tile's time with most slots idle.
+constexpr int kTailMaxPieces = 8;
+constexpr int kTailMinChunks = 4;
+constexpr size_t kTailPartBytes = (size_t)32 << 20;  // default budget of the tail's partials
+
+struct SplitPlan {
+  int P = 1;           // pieces per split tile
+  int64_t W = 0;       // tail split: tiles [0, W) whole (0: every tile split when P > 1)
+  int64_t tiles = 0;
+  size_t tile_part = 0;  // bytes of one piece's partial tile
+  int64_t nsplit() const { return P > 1 ? (W > 0 ? tiles - W : tiles) : 0; }
+  size_t part_bytes() const { return (size_t)(nsplit() * P) * tile_part; }
+  int64_t grid() const { return P > 1 ? W + nsplit() * P : tiles; }
+};
+
+static void tail_split(SplitPlan &s, int64_t slots, int64_t kc, size_t budget) {
+  if (s.P > 1 || s.tiles <= slots) return;
+  const int64_t tail = s.tiles % slots;
+  if (tail == 0 || 2 * tail > slots) return;
+  int64_t P = slots / tail;
+  if (P > kTailMaxPieces) P = kTailMaxPieces;
+  if (P > kc / kTailMinChunks) P = kc / kTailMinChunks;
+  while (P > 1 && (size_t)(tail * P) * s.tile_part > budget) --P;
+  if (P < 2) return;
+  s.P = (int)P;
+  s.W = s.tiles - tail;
+}
+
+struct Gemm32Plan : SplitPlan {
+  int mt, ks;
 };
 // 256-column tiles of a weight (pairs of gate / up strip groups for SwiGLU).
 static int64_t gemm32_col_tiles(const WeightView &w) { return w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16; }
 
-// nt: column tiles of the launch (all members of a grouped one).
-static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt) {
+// nt: column tiles of the launch (all members of a grouped one); budget:
+// bytes allowed for a tail split's partials.
+static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt, size_t budget) {
   Gemm32Plan g;
   const bool small = M <= kGemm32SmallRows;
   const bool kq = w.fmt == DIALQ_FORMAT_Q4_K || w.fmt == DIALQ_FORMAT_Q8_0 || w.fmt == DIALQ_FORMAT_Q6_K;
@@ -1169,6 +1224,7 @@ static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt) {
   g.ks = small ? 2 : GEMM32_KS;  // byte formats; a Q4_K stage is one 64-k quarter chunk
   const int64_t rows = 32 * g.mt;
   g.tiles = nt * ((M + rows - 1) / rows);
+  g.tile_part = (size_t)rows * 256 * sizeof(float);
   g.P = 1;
   const int64_t occ = kq ? GEMMKQ_OCC : g.mt == 4 ? 2 : GEMM32_OCC;
   const int64_t cus = device_cus(), slots = occ * cus;
@@ -1180,6 +1236,7 @@ static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt) {
     g.P = (int)(P < 1 ? 1 : P);
     while (g.P > 1 && g.part_bytes() > kGemm32MaxPartBytes) --g.P;
   }
+  if (!small) tail_split(g, slots, w.k_chunks, budget);
   return g;
 }
 
@@ -1196,15 +1253,13 @@ static bool gemm32_applies(const WeightView &w, int x_dtype) {
   return false;
 }
 
-void gemm_workspace(int64_t M, const WeightView &w, int x_dtype, size_t &part_bytes, size_t &cnt_count) {
+void gemm_workspace(int64_t M, const WeightView &w, int x_dtype, size_t &part_bytes, size_t &cnt_count, bool tail) {
   part_bytes = 0;
   cnt_count = 0;
   if (!gemm32_applies(w, x_dtype) || M <= 0) return;
-  const Gemm32Plan g = gemm32_plan(M, w, gemm32_col_tiles(w));
-  if (g.P > 1) {
-    part_bytes = g.part_bytes();
-    cnt_count = (size_t)g.tiles;
-  }
+  const Gemm32Plan g = gemm32_plan(M, w, gemm32_col_tiles(w), tail ? kTailPartBytes : 0);
+  part_bytes = g.part_bytes();
+  cnt_count = (size_t)g.nsplit();
 }
 
 // The member table of a grouped 32x32-kernel launch, or false where one does
@@ -1229,11 +1284,9 @@ bool gemm_group_workspace(int64_t M, const WeightView *ws, int n, int x_dtype, s
   cnt_count = 0;
   GemmGroup g;
   if (M <= 0 || !gemm_group_table(ws, nullptr, n, x_dtype, g)) return false;
-  const Gemm32Plan pl = gemm32_plan(M, ws[0], g.tbase[n]);
-  if (pl.P > 1) {
-    part_bytes = pl.part_bytes();
-    cnt_count = (size_t)pl.tiles;
-  }
+  const Gemm32Plan pl = gemm32_plan(M, ws[0], g.tbase[n], kTailPartBytes);
+  part_bytes = pl.part_bytes();
+  cnt_count = (size_t)pl.nsplit();
   return true;
 }
 
@@ -1269,20 +1322,23 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
                       (ACT == DIALQ_BF16 || ACT == kActF16N);
   if constexpr (BYTE || KQ) {
     if (gemm32_applies(w, ACT == DIALQ_F32 ? DIALQ_F32 : DIALQ_BF16)) {
-      const Gemm32Plan g = gemm32_plan(M, w, grp ? grp->tbase[grp->nm] : gemm32_col_tiles(w));
-      if (g.P > 1 && ((size_t)g.tiles > cnt_count || g.part_bytes() > part_bytes)) return hipErrorInvalidValue;
-      if (g.tiles * g.P > 0x7fffffffLL) return hipErrorInvalidValue;
+      // the tail budget the workspace was sized with, or the buffer given
+      const Gemm32Plan g = gemm32_plan(M, w, grp ? grp->tbase[grp->nm] : gemm32_col_tiles(w),
+                                       part_bytes < kTailPartBytes ? part_bytes : kTailPartBytes);
+      if (g.P > 1 && ((size_t)g.nsplit() > cnt_count || g.part_bytes() > part_bytes)) return hipErrorInvalidValue;
+      if (g.grid() > 0x7fffffffLL) return hipErrorInvalidValue;
       GemmParams p{w, x, y, M, y_dtype, g.P, part, cnt};
+      p.W = (int)g.W;
       if (grp) p.g = *grp;
       p.yrow = yrow;
       if (yrow && !KQ) return hipErrorInvalidValue;
       if constexpr (KQ) {
-        if (g.mt == 1) return gemm_kq_launch<FMT, ACT, 1>(p, g.tiles * g.P, st);
-        return gemm_kq_launch<FMT, ACT, GEMMKQ_MT>(p, g.tiles * g.P, st);
+        if (g.mt == 1) return gemm_kq_launch<FMT, ACT, 1>(p, g.grid(), st);
+        return gemm_kq_launch<FMT, ACT, GEMMKQ_MT>(p, g.grid(), st);
       } else {
-        if (g.mt == 1) return gemm32_launch<FMT, ACT, 1, 2>(p, g.tiles * g.P, st);
-        if (g.mt == 4) return gemm32_launch<FMT, ACT, 4, 1, 2>(p, g.tiles * g.P, st);
-        return gemm32_launch<FMT, ACT, GEMM32_MT, GEMM32_KS>(p, g.tiles * g.P, st);
+        if (g.mt == 1) return gemm32_launch<FMT, ACT, 1, 2>(p, g.grid(), st);
+        if (g.mt == 4) return gemm32_launch<FMT, ACT, 4, 1, 2>(p, g.grid(), st);
+        return gemm32_launch<FMT, ACT, GEMM32_MT, GEMM32_KS>(p, g.grid(), st);
       }
     }
   }
@@ -1405,10 +1461,12 @@ struct NativeParams {
   int64_t M, k_pad;
   void *y;
   int y_dtype;
-  // Split-K: P pieces per tile (1: whole tiles, no partials).
+  // Split-K: P pieces per split tile (1: whole tiles, no partials); with
+  // W > 0 only the tiles past the first W are split (sched_tile).
   int P;
-  float *part;  // [tiles][P][32 MT][256] partial tiles
-  int *cnt;     // [tiles] arrivals per split tile; zero between launches
+  float *part;  // [split tiles][P][32 MT][256] partial tiles
+  int *cnt;     // [split tiles] arrivals per split tile; zero between launches
+  int W = 0;
   GemmGroup g;
 };
 
@@ -1467,23 +1525,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
   const bool grp = !SWI && p.g.nm > 1;
   const int nt = grp ? p.g.tbase[p.g.nm] : SWI ? (int)((p.w.pair + 7) / 8) : (int)((p.w.n_strips + 15) / 16);
   const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
-  // One workgroup per (tile, k piece).  P == 1: whole tiles in the
-  // XCD-aware order of tile_of.  P > 1: each tile's chunks split evenly into
-  // P pieces; units go (column tile, piece, row block) over XCD-contiguous
-  // ranks, so the row blocks that stream the same weight chunks run on one
-  // XCD at once and share them in its L2.
-  const int P = p.P;
-  int tm, tn, piece = 0;
-  if (P == 1) {
-    tile_of(blockIdx.x, gridDim.x, nt, mtiles, tm, tn);
-  } else {
-    const int u = xcd_rank(blockIdx.x, gridDim.x);
-    tm = u % mtiles;
-    piece = (u / mtiles) % P;
-    tn = u / (mtiles * P);
-  }
+  // One workgroup per tile or k piece of a tile (sched_tile).
+  int tm, tn, piece, t;  // t: split index of the tile, -1 when whole
+  sched_tile(nt, mtiles, p.P, p.W, tm, tn, piece, t);
+  const int P = t < 0 ? 1 : p.P;
   const int c0 = (int)((int64_t)piece * kc / P), c1 = (int)((int64_t)(piece + 1) * kc / P);
-  const int t = tn * mtiles + tm;  // counter index of a split tile (the global tile)
   const int jm = grp ? group_member(p.g, tn) : 0;
   const WeightView &w = grp ? p.g.wm[jm] : p.w;
   void *const yout = grp ? p.g.ym[jm] : p.y;
@@ -1711,7 +1757,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) sum[(mt * 2 + q) * 16 + e] = FP8 ? acc[mt][q][e] * mref : acc[mt][q][e];
 
-    if (P > 1) {
+    if (t >= 0) {
       // Split tile.  Each piece publishes its partial with agent-scope
       // relaxed atomic stores, waits for them (vmcnt 0), then counts itself
       // in; the last to arrive adds the P partials in piece order -- the
@@ -1726,7 +1772,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
       if (tid == 0) lds_last = __hip_atomic_fetch_add(&p.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1;
       __syncthreads();
       if (!lds_last) return;
-      const rsrc_t rp = make_rsrc(p.part, (uint32_t)((size_t)nt * mtiles * P * ACC * 256 * 4));
+      const rsrc_t rp = make_rsrc(p.part + (size_t)t * P * (ACC * 256), (uint32_t)((size_t)P * ACC * 256 * 4));
 #pragma unroll
       for (int eb = 0; eb < ACC; eb += 16) {  // 16 values at a time keeps registers in check
         float tot[16];
@@ -1738,7 +1784,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
             for (int e = 0; e < 16; ++e) tot[e] += sum[eb + e];
             continue;
           }
-          const uint32_t base_off = (uint32_t)(((size_t)t * P + u) * (ACC * 256) + tid) * 4u;
+          const uint32_t base_off = (uint32_t)((size_t)u * (ACC * 256) + tid) * 4u;
           float pv[16];
 #pragma unroll
           for (int e = 0; e < 16; ++e)
@@ -1822,15 +1868,21 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 
 // k pieces per tile: 1 (whole tiles) when the tiles fill every resident
 // workgroup slot, else as many as fit in one round of slots, each at least
-// native_min_chunks chunks long.
-static int native_pieces(int fmt, int occ, int64_t tiles, int64_t kc) {
+// native_min_chunks chunks long.  No tail split: on the 27B gate at
+// M = 1024 (544 / 1088 tiles on 512 slots) it measured slower, MXFP4 81 ->
+// 95 us and FP8 level (137 us), in builds timed side by side on one GPU.
+static SplitPlan native_plan(int fmt, int occ, int64_t tiles, int64_t kc) {
+  SplitPlan s;
+  s.tiles = tiles;
+  s.tile_part = (size_t)native_acc(fmt) * 256 * sizeof(float);
   const int64_t slots = (int64_t)occ * device_cus();
   int64_t P = tiles >= slots ? 1 : slots / tiles;
   const int64_t cap = kc / native_min_chunks(fmt);
   if (P > cap) P = cap;
+  s.P = (int)(P < 1 ? 1 : P);
   // partials of at most kGemm32MaxPartBytes, as the 32x32 kernels
-  while (P > 1 && (size_t)(tiles * P) * native_acc(fmt) * 256 * sizeof(float) > kGemm32MaxPartBytes) --P;
-  return (int)(P < 1 ? 1 : P);
+  while (s.P > 1 && s.part_bytes() > kGemm32MaxPartBytes) --s.P;
+  return s;
 }
 
 template <int FMT, int MT, int OCC, int DEPTH>
@@ -1850,14 +1902,14 @@ static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const vo
     for (int j = 0; j < grp->nm; ++j)
       if (grp->wm[j].n_strips * grp->wm[j].k_chunks * TILE >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   const int64_t tiles = nt * ((M + ROWS - 1) / ROWS);
-  const int P = native_pieces(FMT, OCC, tiles, w.k_chunks);
-  if (tiles * P > 0x7fffffffLL) return hipErrorInvalidValue;
-  if (P > 1 && ((size_t)tiles > cnt_count || (size_t)(tiles * P) * (32 * MT) * 256 * sizeof(float) > part_bytes))
-    return hipErrorInvalidValue;
-  NativeParams p{w, xq, xs, M, k_pad, y, y_dtype, P, part, cnt};
+  const SplitPlan s = native_plan(FMT, OCC, tiles, w.k_chunks);
+  if (s.grid() > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (s.P > 1 && ((size_t)s.nsplit() > cnt_count || s.part_bytes() > part_bytes)) return hipErrorInvalidValue;
+  NativeParams p{w, xq, xs, M, k_pad, y, y_dtype, s.P, part, cnt};
+  p.W = (int)s.W;
   if (grp) p.g = *grp;
-  if (w.pair) k_gemm_native<FMT, MT, OCC, DEPTH, true><<<dim3((unsigned)(tiles * P)), 256, 0, st>>>(p);
-  else k_gemm_native<FMT, MT, OCC, DEPTH, false><<<dim3((unsigned)(tiles * P)), 256, 0, st>>>(p);
+  if (w.pair) k_gemm_native<FMT, MT, OCC, DEPTH, true><<<dim3((unsigned)s.grid()), 256, 0, st>>>(p);
+  else k_gemm_native<FMT, MT, OCC, DEPTH, false><<<dim3((unsigned)s.grid()), 256, 0, st>>>(p);
   return hipGetLastError();
 }
 
@@ -1866,9 +1918,9 @@ void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t
   const int rows = 32 * (w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
   const int64_t nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
   const int64_t tiles = nt * ((M + rows - 1) / rows);
-  const int P = native_pieces(w.fmt, occ, tiles, w.k_chunks);
-  part_bytes = P > 1 ? (size_t)(tiles * P) * native_acc(w.fmt) * 256 * sizeof(float) : 0;
-  cnt_count = P > 1 ? (size_t)tiles : 0;
+  const SplitPlan s = native_plan(w.fmt, occ, tiles, w.k_chunks);
+  part_bytes = s.part_bytes();
+  cnt_count = (size_t)s.nsplit();
 }
 
 // The member table of a grouped native launch (FP8_BLOCK or MXFP4 members of
@@ -1896,9 +1948,9 @@ bool native_group_workspace(int64_t M, const WeightView *ws, int n, size_t &part
   const bool fp8 = ws[0].fmt == DIALQ_FORMAT_FP8_BLOCK;
   const int occ = fp8 ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4, rows = 32 * (fp8 ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
   const int64_t tiles = (int64_t)g.tbase[n] * ((M + rows - 1) / rows);
-  const int P = native_pieces(ws[0].fmt, occ, tiles, ws[0].k_chunks);
-  part_bytes = P > 1 ? (size_t)(tiles * P) * native_acc(ws[0].fmt) * 256 * sizeof(float) : 0;
-  cnt_count = P > 1 ? (size_t)tiles : 0;
+  const SplitPlan s = native_plan(ws[0].fmt, occ, tiles, ws[0].k_chunks);
+  part_bytes = s.part_bytes();
+  cnt_count = (size_t)s.nsplit();
   return true;
 }
 

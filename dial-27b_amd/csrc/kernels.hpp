@@ -93,10 +93,15 @@ int64_t gemv_grouped_launches();
 void set_gemv_wait_limit(int64_t polls);
 int gemv_wait_limit();
 // Prefill GEMM with weight-only dequantization (bf16 / f16 MFMA operands).
-// Launches with fewer tiles than workgroup slots split each tile along K and
-// need gemm_workspace(M, w, x_dtype) of scratch: `part` (partial tiles) and
+// Launches with fewer tiles than workgroup slots split each tile along K,
+// launches whose last round of tiles is at most half full split that
+// round's tiles (`tail`: false keeps them whole); both need
+// gemm_workspace(M, w, x_dtype) of scratch: `part` (partial tiles) and
 // `cnt` (per-tile counters, zero before the call and left zero after it).
-void gemm_workspace(int64_t M, const WeightView &w, int x_dtype, size_t &part_bytes, size_t &cnt_count);
+// The launch plans its split within the `part` bytes it is given, so a
+// buffer sized without the tail split runs without it.
+void gemm_workspace(int64_t M, const WeightView &w, int x_dtype, size_t &part_bytes, size_t &cnt_count,
+                    bool tail = true);
 // yrow: per-row output multipliers (k_gemm_kq only; null = 1).
 hipError_t launch_gemm(const WeightView &w, const void *x, int x_dtype, int64_t M, void *y, int y_dtype, float *part,
                        size_t part_bytes, int *cnt, size_t cnt_count, hipStream_t st, const float *yrow = nullptr);
@@ -119,9 +124,10 @@ hipError_t launch_gemm_native_group(const WeightView *ws, void *const *ys, int n
 int64_t gemm_grouped_launches();
 // Native low-precision prefill: FP8_BLOCK with per-token fp8 activations,
 // MXFP4 with per-32 MXFP4 activations.  `xq` / `xs` are the quantized
-// activations (codes and scales) produced by launch_act_*.  The stream-K
-// schedule needs native_workspace(M, w) of scratch: `part` (partial tiles)
-// and `cnt` (per-tile counters, zero before the call and left zero after it).
+// activations (codes and scales) produced by launch_act_*.  Launches of few
+// tiles split them along K and need native_workspace(M, w) of scratch:
+// `part` (partial tiles) and `cnt` (per-tile counters, zero before the call
+// and left zero after it).
 void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count);
 hipError_t launch_gemm_native(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M,
                               int64_t k_pad, void *y, int y_dtype, float *part, size_t part_bytes, int *cnt,

@@ -204,7 +204,10 @@ int dialq_linear_forward_group(void *const *linears, int32_t n, const void *x,
  * instead of the handle's grown buffers.  The call allocates and frees
  * nothing.  Sizes beyond the array (e.g. native prefill of 1024 rows at
  * K = 17408 plus split-K partials over 32 MiB, or an out_dim above 262112
- * rows) return -1 with a message naming the bytes needed.  The array is
+ * rows) return -1 with a message naming the bytes needed; a prefill whose
+ * last round of tiles would be split along K with partials that do not fit
+ * runs that round whole instead (equal to dialq_linear_forward_ex to f32
+ * rounding rather than bit for bit).  The array is
  * shared by every call on a device: calls that overlap on one device (two
  * streams, two host threads) race; serialize them.  The first call on a
  * device looks the array up and clears its counters: make it outside

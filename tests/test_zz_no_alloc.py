@@ -5,8 +5,9 @@ bit (the same kernels on the same numbers, with the scratch taken from the
 library's static per-device array instead of the handle's buffers), on two
 calls in a row with the second smaller, for every path that uses scratch:
 decode whole strips, the decode work queue (workspace + counters), the
-weight-only GEMM, the native fp8 / fp4 prefill with split-K partials, and a
-misaligned x.  It must refuse sizes beyond the array with a message, leave
+weight-only GEMM (whole, and with its last round of tiles split along K),
+the native fp8 / fp4 prefill with split-K partials, and a misaligned x.
+It must refuse sizes beyond the array with a message, leave
 the handle's own scratch untouched, and replay correctly from a graph."""
 import numpy as np
 import pytest
@@ -55,6 +56,9 @@ CASES = {
     "decode_work_queue": (dq.W8A16, [(1024, 8704, 8, dq.PATH_GEMV, 0), (512, 8704, 4, dq.PATH_GEMV, 0)]),
     "decode_q4k_rows": (dq.Q4_K, [(4096, 4096, 8, dq.PATH_GEMV, 0), (256, 4096, 3, dq.PATH_GEMV, 0)]),
     "gemm": (dq.Q8_0, [(640, 1024, 300, dq.PATH_GEMM, 0), (640, 1024, 130, dq.PATH_GEMM, 0)]),
+    # 544 tiles of 128 rows on 512 slots: the last round's 32 tiles split
+    # along K, their partials (16 MB) in the array
+    "gemm_tail_split": (dq.W8A16, [(8704, 1024, 2048, dq.PATH_GEMM, 0), (8704, 1024, 1024, dq.PATH_GEMM, 0)]),
     # Q4_K on bf16 x: the f16 copy of x and its row scales in the array
     "gemm_q4k_bf16": (dq.Q4_K, [(1024, 2048, 300, dq.PATH_GEMM, 0), (512, 2048, 40, dq.PATH_GEMM, 0)]),
     "native_fp8_split_k": (dq.FP8_BLOCK, [(1024, 5120, 512, dq.PATH_GEMM_NATIVE, 0),
