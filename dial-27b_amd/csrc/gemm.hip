@@ -541,6 +541,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   const int nt = grp ? p.g.tbase[p.g.nm] : SWI ? (int)((p.w.pair + 7) / 8) : (int)((p.w.n_strips + 15) / 16);
   const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
   sched_tile(nt, mtiles, p.P, p.W, tm, tn, piece, sidx);
+  if (tm >= mtiles || tn >= nt) return;  // a grid larger than the tiles (never planned)
   const int P = sidx < 0 ? 1 : p.P;  // pieces of this workgroup's tile
   const int jm = grp ? group_member(p.g, tn) : 0;
   const WeightView &w = grp ? p.g.wm[jm] : p.w;
@@ -964,6 +965,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
   const int nt = grp ? p.g.tbase[p.g.nm] : SWI ? (int)((p.w.pair + 7) / 8) : (int)((p.w.n_strips + 15) / 16);
   const int mtiles = (int)((p.M + ROWS - 1) / ROWS);
   sched_tile(nt, mtiles, p.P, p.W, tm, tn, piece, sidx);
+  if (tm >= mtiles || tn >= nt) return;  // a grid larger than the tiles (never planned)
   const int P = sidx < 0 ? 1 : p.P;  // pieces of this workgroup's tile
   const int jm = grp ? group_member(p.g, tn) : 0;
   const WeightView &w = grp ? p.g.wm[jm] : p.w;
@@ -1221,6 +1223,14 @@ static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt, size_t
   const bool small = M <= kGemm32SmallRows;
   const bool kq = w.fmt == DIALQ_FORMAT_Q4_K || w.fmt == DIALQ_FORMAT_Q8_0 || w.fmt == DIALQ_FORMAT_Q6_K;
   g.mt = small ? 1 : kq ? GEMMKQ_MT : M >= kGemm32TallRows ? 4 : GEMM32_MT;
+  // 128-row tiles that fill less than one round of their slots but too many
+  // to split along K (the 27B o and down projections at 2048 rows: 320
+  // tiles on 512 slots) leave a CU in four with two tiles and the rest
+  // with one; 64-row tiles at three per CU spread them more evenly (down
+  // 5120x17408: 440 -> 402 us, o 164 -> 160; q and k / v unchanged or
+  // worse, so not past the split-K range)
+  if (!kq && g.mt == 4 && nt * ((M + 127) / 128) < 2 * device_cus() && nt * ((M + 127) / 128) * 2 >= device_cus())
+    g.mt = GEMM32_MT;
   g.ks = small ? 2 : GEMM32_KS;  // byte formats; a Q4_K stage is one 64-k quarter chunk
   const int64_t rows = 32 * g.mt;
   g.tiles = nt * ((M + rows - 1) / rows);
@@ -1332,12 +1342,16 @@ static hipError_t gemm_dispatch(const WeightView &w, const void *x, int64_t M, v
       if (grp) p.g = *grp;
       p.yrow = yrow;
       if (yrow && !KQ) return hipErrorInvalidValue;
+      // the plan's tile height must be one this launcher instantiates: the
+      // grid and the split indices were counted in its tiles
       if constexpr (KQ) {
         if (g.mt == 1) return gemm_kq_launch<FMT, ACT, 1>(p, g.grid(), st);
+        if (g.mt != GEMMKQ_MT) return hipErrorInvalidValue;
         return gemm_kq_launch<FMT, ACT, GEMMKQ_MT>(p, g.grid(), st);
       } else {
         if (g.mt == 1) return gemm32_launch<FMT, ACT, 1, 2>(p, g.grid(), st);
         if (g.mt == 4) return gemm32_launch<FMT, ACT, 4, 1, 2>(p, g.grid(), st);
+        if (g.mt != GEMM32_MT) return hipErrorInvalidValue;
         return gemm32_launch<FMT, ACT, GEMM32_MT, GEMM32_KS>(p, g.grid(), st);
       }
     }
@@ -1528,6 +1542,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
   // One workgroup per tile or k piece of a tile (sched_tile).
   int tm, tn, piece, t;  // t: split index of the tile, -1 when whole
   sched_tile(nt, mtiles, p.P, p.W, tm, tn, piece, t);
+  if (tm >= mtiles || tn >= nt) return;  // a grid larger than the tiles (never planned)
   const int P = t < 0 ? 1 : p.P;
   const int c0 = (int)((int64_t)piece * kc / P), c1 = (int)((int64_t)(piece + 1) * kc / P);
   const int jm = grp ? group_member(p.g, tn) : 0;

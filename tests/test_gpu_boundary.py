@@ -90,3 +90,22 @@ def test_misaligned_x_in_capture_needs_an_eager_call_first(torch_dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, want)
+
+
+def test_weights_past_2_gib_are_refused_on_every_path(torch_dev):
+    # every kernel addresses the resident tiles with 32-bit buffer offsets and
+    # masks loads with the offset 2^31: a handle of 2 GiB or more is refused
+    # with a message at forward time, decode and prefill alike (the largest
+    # DIAL linear, the 27B lm_head in W8A16, is 1.27 GB)
+    import torch
+    n, k = 262144 + 16, 8192  # 2,147,614,720 bytes of int8 codes, 2^31 + 131072
+    codes = torch.zeros(n, k, dtype=torch.int8, device=torch_dev)
+    scales = torch.ones(n, dtype=torch.float32, device=torch_dev)
+    lin = dq.Linear.create(dq.W8A16, n, k, codes, scales)
+    del codes
+    x = torch.zeros(32, k, dtype=torch.bfloat16, device=torch_dev)
+    y = torch.empty(32, n, dtype=torch.bfloat16, device=torch_dev)
+    for rows, kind in ((1, "decode"), (32, "prefill")):
+        with pytest.raises(dq.DialqError, match=kind + r" kernel addresses weights with 32-bit offsets"):
+            lin.forward(x[:rows], y[:rows])
+    lin.close()
