@@ -391,7 +391,7 @@ ForwardPlan plan_forward(const Linear *L, const WeightView &w, int x_dtype, int6
     const size_t codes = fmt == DIALQ_FORMAT_FP8_BLOCK ? (size_t)(rows * pl.k_pad) : (size_t)(rows * pl.k_pad / 2);
     pl.codes = (codes + 255) / 256 * 256;
     pl.xscale = fmt == DIALQ_FORMAT_FP8_BLOCK ? (size_t)rows * sizeof(float) : (size_t)(rows * pl.k_pad / 32);
-    native_workspace(rows, w, pl.part, pl.ncnt);
+    native_workspace(rows, w, pl.part, pl.ncnt, tail);
   } else if (path == DIALQ_PATH_GEMM) {
     if (stage_f16) pl.xh = kq_f16_stage_bytes(L, x_dtype, rows, path);
     // split-K partials of few-tile launches (the f16 kernel's tiling when x is staged as f16)

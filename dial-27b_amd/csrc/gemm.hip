@@ -1197,12 +1197,12 @@ struct SplitPlan {
   int64_t grid() const { return P > 1 ? W + nsplit() * P : tiles; }
 };
 
-static void tail_split(SplitPlan &s, int64_t slots, int64_t kc, size_t budget) {
+static void tail_split(SplitPlan &s, int64_t slots, int64_t kc, size_t budget, int max_pieces = kTailMaxPieces) {
   if (s.P > 1 || s.tiles <= slots) return;
   const int64_t tail = s.tiles % slots;
   if (tail == 0 || 2 * tail > slots) return;
   int64_t P = slots / tail;
-  if (P > kTailMaxPieces) P = kTailMaxPieces;
+  if (P > max_pieces) P = max_pieces;
   if (P > kc / kTailMinChunks) P = kc / kTailMinChunks;
   while (P > 1 && (size_t)(tail * P) * s.tile_part > budget) --P;
   if (P < 2) return;
@@ -1787,29 +1787,26 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
       if (tid == 0) lds_last = __hip_atomic_fetch_add(&p.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1;
       __syncthreads();
       if (!lds_last) return;
+      // All P partials in piece order (this piece's own read back as
+      // well), up to 64 values of one piece in flight per round trip: the
+      // read-back is a single workgroup's, so its round trips, not its
+      // bytes, set its time.
       const rsrc_t rp = make_rsrc(p.part + (size_t)t * P * (ACC * 256), (uint32_t)((size_t)P * ACC * 256 * 4));
+      constexpr int HB = ACC < 64 ? ACC : 64;
 #pragma unroll
-      for (int eb = 0; eb < ACC; eb += 16) {  // 16 values at a time keeps registers in check
-        float tot[16];
+      for (int e = 0; e < ACC; ++e) sum[e] = 0.0f;
+      for (int u = 0; u < P; ++u) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) tot[e] = 0.0f;
-        for (int u = 0; u < P; ++u) {
-          if (u == piece) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) tot[e] += sum[eb + e];
-            continue;
-          }
+        for (int hb = 0; hb < ACC; hb += HB) {
           const uint32_t base_off = (uint32_t)((size_t)u * (ACC * 256) + tid) * 4u;
-          float pv[16];
+          float pv[HB];
 #pragma unroll
-          for (int e = 0; e < 16; ++e)
+          for (int e = 0; e < HB; ++e)
             pv[e] = __uint_as_float(
-                (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, (int)(base_off + (eb + e) * 1024u), 0, kSC1));
+                (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, (int)(base_off + (hb + e) * 1024u), 0, kSC1));
 #pragma unroll
-          for (int e = 0; e < 16; ++e) tot[e] += pv[e];
+          for (int e = 0; e < HB; ++e) sum[hb + e] += pv[e];
         }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sum[eb + e] = tot[e];
       }
       if (tid == 0) __hip_atomic_store(&p.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1883,10 +1880,12 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 
 // k pieces per tile: 1 (whole tiles) when the tiles fill every resident
 // workgroup slot, else as many as fit in one round of slots, each at least
-// native_min_chunks chunks long.  No tail split: on the 27B gate at
-// M = 1024 (544 / 1088 tiles on 512 slots) it measured slower, MXFP4 81 ->
-// 95 us and FP8 level (137 us), in builds timed side by side on one GPU.
-static SplitPlan native_plan(int fmt, int occ, int64_t tiles, int64_t kc) {
+// native_min_chunks chunks long; past one round, a tail split of the last,
+// partial round into at most kNativeTailPieces pieces (budget: bytes
+// allowed for its partials).  The last piece reads the partials back 64
+// values per thread and round trip.
+constexpr int kNativeTailPieces = 2;
+static SplitPlan native_plan(int fmt, int occ, int64_t tiles, int64_t kc, size_t budget) {
   SplitPlan s;
   s.tiles = tiles;
   s.tile_part = (size_t)native_acc(fmt) * 256 * sizeof(float);
@@ -1897,6 +1896,7 @@ static SplitPlan native_plan(int fmt, int occ, int64_t tiles, int64_t kc) {
   s.P = (int)(P < 1 ? 1 : P);
   // partials of at most kGemm32MaxPartBytes, as the 32x32 kernels
   while (s.P > 1 && s.part_bytes() > kGemm32MaxPartBytes) --s.P;
+  tail_split(s, slots, kc, budget, kNativeTailPieces);
   return s;
 }
 
@@ -1917,7 +1917,8 @@ static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const vo
     for (int j = 0; j < grp->nm; ++j)
       if (grp->wm[j].n_strips * grp->wm[j].k_chunks * TILE >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   const int64_t tiles = nt * ((M + ROWS - 1) / ROWS);
-  const SplitPlan s = native_plan(FMT, OCC, tiles, w.k_chunks);
+  // the tail budget the workspace was sized with, or the buffer given
+  const SplitPlan s = native_plan(FMT, OCC, tiles, w.k_chunks, part_bytes < kTailPartBytes ? part_bytes : kTailPartBytes);
   if (s.grid() > 0x7fffffffLL) return hipErrorInvalidValue;
   if (s.P > 1 && ((size_t)s.nsplit() > cnt_count || s.part_bytes() > part_bytes)) return hipErrorInvalidValue;
   NativeParams p{w, xq, xs, M, k_pad, y, y_dtype, s.P, part, cnt};
@@ -1928,12 +1929,12 @@ static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const vo
   return hipGetLastError();
 }
 
-void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count) {
+void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count, bool tail) {
   const int occ = w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4;
   const int rows = 32 * (w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
   const int64_t nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
   const int64_t tiles = nt * ((M + rows - 1) / rows);
-  const SplitPlan s = native_plan(w.fmt, occ, tiles, w.k_chunks);
+  const SplitPlan s = native_plan(w.fmt, occ, tiles, w.k_chunks, tail ? kTailPartBytes : 0);
   part_bytes = s.part_bytes();
   cnt_count = (size_t)s.nsplit();
 }
@@ -1963,7 +1964,7 @@ bool native_group_workspace(int64_t M, const WeightView *ws, int n, size_t &part
   const bool fp8 = ws[0].fmt == DIALQ_FORMAT_FP8_BLOCK;
   const int occ = fp8 ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4, rows = 32 * (fp8 ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
   const int64_t tiles = (int64_t)g.tbase[n] * ((M + rows - 1) / rows);
-  const SplitPlan s = native_plan(ws[0].fmt, occ, tiles, ws[0].k_chunks);
+  const SplitPlan s = native_plan(ws[0].fmt, occ, tiles, ws[0].k_chunks, kTailPartBytes);
   part_bytes = s.part_bytes();
   cnt_count = (size_t)s.nsplit();
   return true;

@@ -124,11 +124,12 @@ hipError_t launch_gemm_native_group(const WeightView *ws, void *const *ys, int n
 int64_t gemm_grouped_launches();
 // Native low-precision prefill: FP8_BLOCK with per-token fp8 activations,
 // MXFP4 with per-32 MXFP4 activations.  `xq` / `xs` are the quantized
-// activations (codes and scales) produced by launch_act_*.  Launches of few
-// tiles split them along K and need native_workspace(M, w) of scratch:
-// `part` (partial tiles) and `cnt` (per-tile counters, zero before the call
-// and left zero after it).
-void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count);
+// activations (codes and scales) produced by launch_act_*.  Split tiles (few
+// tiles, or the last partial round's: `tail`) need native_workspace(M, w) of
+// scratch: `part` (partial tiles) and `cnt` (per-tile counters, zero before
+// the call and left zero after it).  As for launch_gemm, the launch plans
+// its split within the `part` bytes it is given.
+void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count, bool tail = true);
 hipError_t launch_gemm_native(const WeightView &w, const uint8_t *xq, const void *xs, int64_t M,
                               int64_t k_pad, void *y, int y_dtype, float *part, size_t part_bytes, int *cnt,
                               size_t cnt_count, hipStream_t st);

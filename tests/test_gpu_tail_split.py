@@ -1,12 +1,13 @@
-"""Prefill launches of the 32x32 kernels whose last round of tiles is at
-most half full split that round's tiles along K (the tail split):
-workgroups [0, W) run whole tiles, the rest run k pieces whose partials
-the last arriving piece adds in piece order.  W8A16 / Q8_0 / Q4_K at
-M = 2048 (128-row tiles) with N = 8704 give 34 column tiles x 16 row blocks
-= 544 tiles on a 256-CU MI355X's 512 slots (two workgroups per CU): 512
-whole and 32 split.  The native kernels keep whole tiles at such shapes
-(their cases here, 544 tiles as well, pin that path's results at the same
-sizes).
+"""Prefill launches whose last round of tiles is at most half full split
+that round's tiles along K (the tail split): workgroups [0, W) run whole
+tiles, the rest run k pieces whose partials the last arriving piece adds in
+piece order.  The shapes give 544 tiles on a 256-CU MI355X's 512 slots (two
+workgroups per CU), 512 whole and 32 split:
+
+  W8A16 / Q8_0 / Q4_K, M = 2048 (128-row tiles): N = 8704 is 34 column
+  tiles x 16 row blocks, split in 4 pieces (2 for Q4_K's 8 chunks);
+  FP8-128 native, M = 1024 (64-row tiles): the same 544, and MXFP4 native,
+  M = 1024 (128-row tiles): N = 17408, 68 x 8, split in 2 pieces.
 
 Every output element is compared with the fp64 oracle product (split and
 whole tiles alike), and three calls give the same bits (the piece order of
