@@ -1509,8 +1509,6 @@ __device__ __forceinline__ f32x16 mfma_scaled32(i32x8 a, i32x8 b, f32x16 c, int 
 #define NATIVE_DEPTH_FP4 2
 #endif
 
-// f32 accumulators per thread of the native kernel: MT x 2 tiles x 16
-constexpr int native_acc(int fmt) { return 32 * (fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_MT_FP8 : NATIVE_MT_FP4); }
 // Fewest k chunks per piece of a split tile: a piece's partial (64 KB out,
 // read back by the last piece) must be worth the extra parallelism; fp4
 // chunks take half the MFMA time of fp8 ones (measured: MXFP4 k/v and q/o
@@ -1885,10 +1883,10 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_native(NativeParams p) {
 // allowed for its partials).  The last piece reads the partials back 64
 // values per thread and round trip.
 constexpr int kNativeTailPieces = 2;
-static SplitPlan native_plan(int fmt, int occ, int64_t tiles, int64_t kc, size_t budget) {
+static SplitPlan native_plan(int fmt, int mt, int occ, int64_t tiles, int64_t kc, size_t budget) {
   SplitPlan s;
   s.tiles = tiles;
-  s.tile_part = (size_t)native_acc(fmt) * 256 * sizeof(float);
+  s.tile_part = (size_t)mt * 32 * 256 * sizeof(float);  // MT x 2 column tiles x 16 values per thread
   const int64_t slots = (int64_t)occ * device_cus();
   int64_t P = tiles >= slots ? 1 : slots / tiles;
   const int64_t cap = kc / native_min_chunks(fmt);
@@ -1898,6 +1896,17 @@ static SplitPlan native_plan(int fmt, int occ, int64_t tiles, int64_t kc, size_t
   while (s.P > 1 && s.part_bytes() > kGemm32MaxPartBytes) --s.P;
   tail_split(s, slots, kc, budget, kNativeTailPieces);
   return s;
+}
+
+// 32-row MFMA tiles per workgroup of a native launch over nt column tiles.
+// MXFP4 takes 128-row tiles, or 64-row ones when 128-row tiles would leave
+// more than half the CUs without a tile (the 27B k / v at 1024 rows: 32
+// tiles, 32 -> 23 us as 64 of 64 rows; at q / o / down, 160-192 tiles,
+// 64-row tiles measured 6-18 % slower, and the grouped q / k / v 14 %).
+static int native_mt(int fmt, int64_t M, int64_t nt) {
+  if (fmt == DIALQ_FORMAT_FP8_BLOCK) return NATIVE_MT_FP8;
+  const int64_t rows = 32 * NATIVE_MT_FP4;
+  return nt * ((M + rows - 1) / rows) * 2 < device_cus() ? 2 : NATIVE_MT_FP4;
 }
 
 template <int FMT, int MT, int OCC, int DEPTH>
@@ -1918,7 +1927,7 @@ static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const vo
       if (grp->wm[j].n_strips * grp->wm[j].k_chunks * TILE >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   const int64_t tiles = nt * ((M + ROWS - 1) / ROWS);
   // the tail budget the workspace was sized with, or the buffer given
-  const SplitPlan s = native_plan(FMT, OCC, tiles, w.k_chunks, part_bytes < kTailPartBytes ? part_bytes : kTailPartBytes);
+  const SplitPlan s = native_plan(FMT, MT, OCC, tiles, w.k_chunks, part_bytes < kTailPartBytes ? part_bytes : kTailPartBytes);
   if (s.grid() > 0x7fffffffLL) return hipErrorInvalidValue;
   if (s.P > 1 && ((size_t)s.nsplit() > cnt_count || s.part_bytes() > part_bytes)) return hipErrorInvalidValue;
   NativeParams p{w, xq, xs, M, k_pad, y, y_dtype, s.P, part, cnt};
@@ -1931,10 +1940,10 @@ static hipError_t native_launch(const WeightView &w, const uint8_t *xq, const vo
 
 void native_workspace(int64_t M, const WeightView &w, size_t &part_bytes, size_t &cnt_count, bool tail) {
   const int occ = w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4;
-  const int rows = 32 * (w.fmt == DIALQ_FORMAT_FP8_BLOCK ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
   const int64_t nt = w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16;
+  const int mt = native_mt(w.fmt, M, nt), rows = 32 * mt;
   const int64_t tiles = nt * ((M + rows - 1) / rows);
-  const SplitPlan s = native_plan(w.fmt, occ, tiles, w.k_chunks, tail ? kTailPartBytes : 0);
+  const SplitPlan s = native_plan(w.fmt, mt, occ, tiles, w.k_chunks, tail ? kTailPartBytes : 0);
   part_bytes = s.part_bytes();
   cnt_count = (size_t)s.nsplit();
 }
@@ -1962,9 +1971,10 @@ bool native_group_workspace(int64_t M, const WeightView *ws, int n, size_t &part
   GemmGroup g;
   if (M <= 0 || !native_group_table(ws, nullptr, n, g)) return false;
   const bool fp8 = ws[0].fmt == DIALQ_FORMAT_FP8_BLOCK;
-  const int occ = fp8 ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4, rows = 32 * (fp8 ? NATIVE_MT_FP8 : NATIVE_MT_FP4);
+  const int occ = fp8 ? NATIVE_OCC_FP8 : NATIVE_OCC_FP4;
+  const int mt = native_mt(ws[0].fmt, M, g.tbase[n]), rows = 32 * mt;
   const int64_t tiles = (int64_t)g.tbase[n] * ((M + rows - 1) / rows);
-  const SplitPlan s = native_plan(ws[0].fmt, occ, tiles, ws[0].k_chunks, kTailPartBytes);
+  const SplitPlan s = native_plan(ws[0].fmt, mt, occ, tiles, ws[0].k_chunks, kTailPartBytes);
   part_bytes = s.part_bytes();
   cnt_count = (size_t)s.nsplit();
   return true;
@@ -1980,6 +1990,9 @@ hipError_t launch_gemm_native_group(const WeightView *ws, void *const *ys, int n
   if (ws[0].fmt == DIALQ_FORMAT_FP8_BLOCK)
     r = native_launch<DIALQ_FORMAT_FP8_BLOCK, NATIVE_MT_FP8, NATIVE_OCC_FP8, NATIVE_DEPTH_FP8>(
         ws[0], xq, xs, M, k_pad, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g);
+  else if (native_mt(DIALQ_FORMAT_MXFP4, M, g.tbase[n]) == 2)
+    r = native_launch<DIALQ_FORMAT_MXFP4, 2, NATIVE_OCC_FP4, NATIVE_DEPTH_FP4>(
+        ws[0], xq, xs, M, k_pad, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g);
   else
     r = native_launch<DIALQ_FORMAT_MXFP4, NATIVE_MT_FP4, NATIVE_OCC_FP4, NATIVE_DEPTH_FP4>(
         ws[0], xq, xs, M, k_pad, ys[0], y_dtype, part, part_bytes, cnt, cnt_count, st, &g);
@@ -1994,9 +2007,13 @@ hipError_t launch_gemm_native(const WeightView &w, const uint8_t *xq, const void
   if (w.fmt == DIALQ_FORMAT_FP8_BLOCK)
     return native_launch<DIALQ_FORMAT_FP8_BLOCK, NATIVE_MT_FP8, NATIVE_OCC_FP8, NATIVE_DEPTH_FP8>(
         w, xq, xs, M, k_pad, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
-  if (w.fmt == DIALQ_FORMAT_MXFP4)
+  if (w.fmt == DIALQ_FORMAT_MXFP4) {
+    if (native_mt(w.fmt, M, w.pair ? (w.pair + 7) / 8 : (w.n_strips + 15) / 16) == 2)
+      return native_launch<DIALQ_FORMAT_MXFP4, 2, NATIVE_OCC_FP4, NATIVE_DEPTH_FP4>(
+          w, xq, xs, M, k_pad, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
     return native_launch<DIALQ_FORMAT_MXFP4, NATIVE_MT_FP4, NATIVE_OCC_FP4, NATIVE_DEPTH_FP4>(
         w, xq, xs, M, k_pad, y, y_dtype, part, part_bytes, cnt, cnt_count, st);
+  }
   return hipErrorInvalidValue;
 }
 
