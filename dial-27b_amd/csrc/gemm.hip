@@ -632,24 +632,29 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
   fetch_b(wb[1], 1);
   __builtin_amdgcn_sched_barrier(0);
 
-  auto stage = [&](u32x2 (&slot)[STEPS][NQ], int st) {
+  auto bconv = [&](u32x2 v) -> u32x4 {
+    constexpr bool F16 = ActTraits<ACT>::F16OP;
+    if constexpr (FMT == DIALQ_FORMAT_W8A16) return F16 ? i8x8_to_f16(v[0], v[1]) : i8x8_to_bf16(v[0], v[1]);
+    else return F16 ? e4m3x8_to_f16(v[0], v[1]) : e4m3x8_to_bf16(v[0], v[1]);
+  };
+  // B operands of a stage's first 16-k step, converted at the end of the
+  // stage before: after the barrier the first MFMAs wait only for their
+  // activation reads, so the two waves a barrier lines up on a SIMD do not
+  // both spend the stage's start on conversions while the MFMA pipe idles.
+  u32x4 b0[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) b0[q] = bconv(wb[0][0][q]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto stage = [&](u32x2 (&slot)[STEPS][NQ], u32x2 (&nxt)[STEPS][NQ], int st) {
     __syncthreads();  // buffer st&1 written; buffer (st+1)&1 no longer read
-    store_a((st + 1) & 1);
-    fetch_a(st + 2);
-    // the activation loads of stage st+2 stay ahead of this stage's weight
-    // refills, so the next stage's wait for them leaves the refills in flight
-    __builtin_amdgcn_sched_barrier(0);
     const uint16_t *base = lds + (st & 1) * BUF;
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
       u32x4 b[NQ];
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
-        constexpr bool F16 = ActTraits<ACT>::F16OP;
-        if constexpr (FMT == DIALQ_FORMAT_W8A16)
-          b[q] = F16 ? i8x8_to_f16(slot[j][q][0], slot[j][q][1]) : i8x8_to_bf16(slot[j][q][0], slot[j][q][1]);
-        else
-          b[q] = F16 ? e4m3x8_to_f16(slot[j][q][0], slot[j][q][1]) : e4m3x8_to_bf16(slot[j][q][0], slot[j][q][1]);
+        b[q] = j == 0 ? b0[q] : bconv(slot[j][q]);
         slot[j][q] = bload(st + 2, j, q);  // refill with stage st+2
       }
 #pragma unroll
@@ -661,15 +666,25 @@ __global__ __launch_bounds__(256, OCC) void k_gemm32(GemmParams p) {
 #pragma unroll
           for (int q = 0; q < NQ; ++q) acc[mt][q] = mfma32_op<ACT>(a, b[q], acc[mt][q]);
         }
+      if (j == 0) {
+        // the next stage's activations into the buffer the barrier freed,
+        // behind this step's MFMAs; then the loads of stage st+2
+        __builtin_amdgcn_sched_barrier(0);
+        store_a((st + 1) & 1);
+        fetch_a(st + 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) b0[q] = bconv(nxt[0][q]);
     __builtin_amdgcn_sched_barrier(0);
   };
   int st = 0;
   for (; st + 1 < nstage; st += 2) {
-    stage(wb[0], st);
-    stage(wb[1], st + 1);
+    stage(wb[0], wb[1], st);
+    stage(wb[1], wb[0], st + 1);
   }
-  if (st < nstage) stage(wb[0], st);
+  if (st < nstage) stage(wb[0], wb[1], st);
 
   if (sidx >= 0 && !split_fixup<MT, NQ>(p, acc, sidx, piece, (int *)(lds + 2 * BUF))) return;
 

@@ -81,6 +81,31 @@ def test_noalloc_matches_forward_ex(case, torch_dev):
         lin.close()
 
 
+def test_noalloc_runs_an_unfitting_tail_split_whole(torch_dev):
+    # 1088 tiles of 128 rows on 512 slots: the allocating entry point splits
+    # the last 64 tiles into 4 pieces (32 MiB of partials); beside the
+    # counters that does not fit the 32 MiB array, so the allocation-free
+    # call runs those tiles whole -- the same products summed in another
+    # order: f32 rounding apart, and both within the oracle's bar
+    import torch
+    from helpers import reference_product
+    n, k, rows = 17408, 1024, 2048
+    raw, scales, kw, deq = make_weight(dq.W8A16, n, k, seed=21)
+    lin = dq.Linear.create(dq.W8A16, n, k, raw, scales, **kw)
+    x = O.round_bf16(np.random.default_rng(22).normal(0, 1, (rows, k)).astype(np.float32))
+    xt = to_torch(x, dq.BF16, torch_dev)
+    want = torch.empty(rows, n, device=torch_dev, dtype=torch.float32)
+    got = torch.empty_like(want)
+    lin.forward(xt, want, path=dq.PATH_GEMM)
+    lin.forward_noalloc(xt, got, path=dq.PATH_GEMM)
+    torch.cuda.synchronize()
+    w_, g_ = want.cpu().numpy(), got.cpu().numpy()
+    assert O.rel_l2(g_, w_) <= 1e-6
+    ref = reference_product(x, deq, dq.F32)
+    assert O.rel_l2(g_, ref) <= 1e-5 and O.rel_l2(w_, ref) <= 1e-5
+    lin.close()
+
+
 def test_noalloc_refuses_beyond_its_scratch(torch_dev):
     import torch
     # native fp8 prefill of 2048 rows at K = 17408: 35.7 MB of activation
