@@ -846,7 +846,11 @@ struct KqFmt<DIALQ_FORMAT_Q4_K> {
     const bool high = j >= 2;
     const uint32_t m = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
     const float s1 = high ? sc.s1[1] * 0.0625f : sc.s1[0], s2 = high ? sc.s2[1] : sc.s2[0];
-    const uint32_t x[2] = {sl.c[j & 1][0] & m, sl.c[j & 1][1] & m};
+    uint32_t x[2] = {sl.c[j & 1][0] & m, sl.c[j & 1][1] & m};
+    // opaque to the optimizer: it would otherwise fold each byte's mask into
+    // a bit-field extract and convert from byte 0 (two instructions per
+    // value); this way one AND per four values and v_cvt_f32_ubyte0..3
+    asm("" : "+v"(x[0]), "+v"(x[1]));
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       wv[4 * i] = __builtin_fmaf(s1, (float)(x[i] & 0xffu), -s2);
