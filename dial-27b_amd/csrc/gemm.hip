@@ -1065,12 +1065,37 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
   fetch_b(wb[1], 1);
   __builtin_amdgcn_sched_barrier(0);
 
-  auto stage = [&](Slot &sl, int st, auto quarter) {
+  // B operands of a stage's first 16-k step, built at the end of the stage
+  // before (as in k_gemm32): after the barrier the first MFMAs wait only
+  // for their activation reads.  Q8_0 only: its 27B layer at M = 2048 gains
+  // 3 % (791-792 -> 812-817 TFLOP/s) while Q4_K's loses 2-4 % (its larger
+  // per-step build then sits on the stage's critical tail), Q6_K's kernel
+  // already holds 256 VGPRs (the early operands spill 136 bytes per lane)
+  // and the bf16 hi + lo form would spill 12.
+  constexpr bool PRE = FMT == DIALQ_FORMAT_Q8_0 && !HL;
+  u32x4 b0h[NQ], b0l[NQ];
+  auto first_ops = [&](const Slot &sl, auto quarter) {
+    constexpr int I = decltype(quarter)::value;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const typename F::Sc sc = F::template scales<I>(sl.q[q]);
+      float wv[8];
+      if constexpr (FMT == DIALQ_FORMAT_Q6_K) F::template weights_i<I>(sl.q[q], sc, 0, wv);
+      else F::weights(sl.q[q], sc, 0, wv);
+      kq_pack<ACT>(wv, b0h[q], b0l[q]);
+    }
+  };
+  if constexpr (PRE) first_ops(wb[0], std::integral_constant<int, 0>{});
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto stage = [&](Slot &sl, const Slot &nxt, int st, auto quarter, auto nquarter) {
     constexpr int I = decltype(quarter)::value;
     __syncthreads();  // buffer st&1 written; buffer (st+1)&1 no longer read
-    store_a((st + 1) & 1);
-    fetch_a(st + 2);
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!PRE) {
+      store_a((st + 1) & 1);
+      fetch_a(st + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     typename F::Sc sc[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) sc[q] = F::template scales<I>(sl.q[q]);
@@ -1082,6 +1107,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
       u32x4 bh[NQ], bl[NQ];
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
+        if (PRE && j == 0) {
+          bh[q] = b0h[q];
+          bl[q] = b0l[q];
+          continue;
+        }
         float wv[8];
         if constexpr (FMT == DIALQ_FORMAT_Q6_K) F::template weights_i<I>(cur.q[q], sc[q], j, wv);
         else F::weights(cur.q[q], sc[q], j, wv);
@@ -1097,23 +1127,36 @@ __global__ __launch_bounds__(256, OCC) void k_gemm_kq(GemmParams p) {
           if constexpr (HL) acc[mt][q] = mfma32_op<ACT>(a, bl[q], acc[mt][q]);
         }
       }
+      if (PRE && j == 0) {
+        // the next stage's activations into the buffer the barrier freed,
+        // behind this step's MFMAs; then the loads of stage st+2
+        __builtin_amdgcn_sched_barrier(0);
+        store_a((st + 1) & 1);
+        fetch_a(st + 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
+    if constexpr (PRE) first_ops(nxt, nquarter);
     __builtin_amdgcn_sched_barrier(0);
   };
+  using Q0 = std::integral_constant<int, 0>;
+  using Q1 = std::integral_constant<int, 1>;
+  using Q2 = std::integral_constant<int, 2>;
+  using Q3 = std::integral_constant<int, 3>;
   if constexpr (SPC == 4) {
     for (int st = 0; st < nstage; st += 4) {
-      stage(wb[0], st, std::integral_constant<int, 0>{});
-      stage(wb[1], st + 1, std::integral_constant<int, 1>{});
-      stage(wb[0], st + 2, std::integral_constant<int, 2>{});
-      stage(wb[1], st + 3, std::integral_constant<int, 3>{});
+      stage(wb[0], wb[1], st, Q0{}, Q1{});
+      stage(wb[1], wb[0], st + 1, Q1{}, Q2{});
+      stage(wb[0], wb[1], st + 2, Q2{}, Q3{});
+      stage(wb[1], wb[0], st + 3, Q3{}, Q0{});
     }
   } else {
     int st = 0;
     for (; st + 1 < nstage; st += 2) {
-      stage(wb[0], st, std::integral_constant<int, 0>{});
-      stage(wb[1], st + 1, std::integral_constant<int, 0>{});
+      stage(wb[0], wb[1], st, Q0{}, Q0{});
+      stage(wb[1], wb[0], st + 1, Q0{}, Q0{});
     }
-    if (st < nstage) stage(wb[0], st, std::integral_constant<int, 0>{});
+    if (st < nstage) stage(wb[0], wb[1], st, Q0{}, Q0{});
   }
 
   if (sidx >= 0 && !split_fixup<MT, NQ>(p, acc, sidx, piece, (int *)(lds + 2 * BUF))) return;
