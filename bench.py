@@ -163,20 +163,20 @@ def run_linear(lin, name, x, y, swiglu, **kw):
         lin.forward(x, y, **kw)
 
 
-def decode_pass(dq, lins, xs, ys, stream, shapes=LAYER_27B, swiglu=(), groups=None):
+def decode_pass(dq, lins, xs, ys, stream, shapes=LAYER_27B, swiglu=(), groups=None, rows=1):
     if groups is not None:
         for (gname, idx), x, y in zip(groups, xs, ys):
             if len(idx) == 1:
-                lins[idx[0]].forward(x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+                lins[idx[0]].forward(x, y, rows=rows, path=dq.PATH_GEMV, stream=stream)
             else:
-                dq.forward_group([lins[i] for i in idx], x, y, rows=1, path=dq.PATH_GEMV, stream=stream)
+                dq.forward_group([lins[i] for i in idx], x, y, rows=rows, path=dq.PATH_GEMV, stream=stream)
         return
     for lin, x, y, (name, _, _) in zip(lins, xs, ys, shapes):
-        run_linear(lin, name, x, y, swiglu, rows=1, path=dq.PATH_GEMV, stream=stream)
+        run_linear(lin, name, x, y, swiglu, rows=rows, path=dq.PATH_GEMV, stream=stream)
 
 
 def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B, swiglu=(), xdtype=None, settle=0.0,
-                groups=None):
+                groups=None, rows=1):
     """Wall time of `steps` decode passes, one HIP-graph replay per pass,
     rotating layer copies.  Linears named in `swiglu` (a fused gate_up) run
     with the SwiGLU epilogue; activations and outputs are bf16 unless
@@ -184,19 +184,19 @@ def time_decode(dq, torch, layers, steps, warmup, dev, shapes=LAYER_27B, swiglu=
     untimed for `settle` seconds of wall time (clock ramp-up), then exactly
     `steps` replays are timed.  With `groups` ([(name, indices of shapes)]),
     the linears of a group share one x and run as one grouped forward into
-    their concatenated output."""
+    their concatenated output.  `rows`: tokens per pass (decode GEMV)."""
     xdtype = xdtype or torch.bfloat16
     if groups is not None:
-        xs = [torch.randn(1, shapes[idx[0]][2], device=dev).to(xdtype) for _, idx in groups]
-        ys = [torch.empty(1, sum(shapes[i][1] for i in idx), device=dev, dtype=xdtype) for _, idx in groups]
+        xs = [torch.randn(rows, shapes[idx[0]][2], device=dev).to(xdtype) for _, idx in groups]
+        ys = [torch.empty(rows, sum(shapes[i][1] for i in idx), device=dev, dtype=xdtype) for _, idx in groups]
     else:
-        xs = [torch.randn(1, k, device=dev).to(xdtype) for _, n, k in shapes]
-        ys = [torch.empty(1, out_cols(name, n, swiglu), device=dev, dtype=xdtype) for name, n, k in shapes]
+        xs = [torch.randn(rows, k, device=dev).to(xdtype) for _, n, k in shapes]
+        ys = [torch.empty(rows, out_cols(name, n, swiglu), device=dev, dtype=xdtype) for name, n, k in shapes]
     stream = torch.cuda.current_stream()
     for lins in layers:  # eager first: sizes the GEMV workspaces outside capture
-        decode_pass(dq, lins, xs, ys, stream, shapes, swiglu, groups)
+        decode_pass(dq, lins, xs, ys, stream, shapes, swiglu, groups, rows)
     torch.cuda.synchronize()
-    graphs = [capture(torch, lambda st, l=lins: decode_pass(dq, l, xs, ys, st, shapes, swiglu, groups))
+    graphs = [capture(torch, lambda st, l=lins: decode_pass(dq, l, xs, ys, st, shapes, swiglu, groups, rows))
               for lins in layers]
     for i in range(warmup):
         graphs[i % len(graphs)].replay()
@@ -736,6 +736,9 @@ def main():
     fsteps16 = max(a.steps // 3, 10)
     s16 = time_decode(dq, torch, layers, fsteps16, 10, dev, xdtype=torch.float16, groups=LAYER_27B_GROUPS)
     value_f16 = layer_bytes(dq, dq.W8A16) * fsteps16 / s16 / 1e9
+    # the 27B sweep's other decode row count (8 tokens per pass)
+    s8 = time_decode(dq, torch, layers, fsteps16, 10, dev, groups=LAYER_27B_GROUPS, rows=8)
+    value_m8 = layer_bytes(dq, dq.W8A16) * fsteps16 / s8 / 1e9
     del layers
     torch.cuda.empty_cache()
     # dominant kernel: the grouped gate / up launch (the largest of the four),
@@ -763,7 +766,8 @@ def main():
              "decode_gbs_ungrouped": {"w8a16": round(value_ungrouped, 1)},
              "decode_us_per_launch_w8a16_grouped": {k: round(v * 1e6, 2) for k, v in per_group.items()},
              "decode_us_per_launch_w8a16":
-             {k: round(v * 1e6, 2) for k, v in per.items()}, "prefill_tflops": {}, "prefill_pct_mfma_peak": {}}
+             {k: round(v * 1e6, 2) for k, v in per.items()}, "prefill_tflops": {}, "prefill_pct_mfma_peak": {},
+             "sweep_27b": {"w8a16": {"decode_gbs_m1": round(value, 1), "decode_gbs_m8": round(value_m8, 1)}}}
     sweep = [s for s in a.sweep.split(",") if s]
     extra["prefill_tflops_ungrouped"] = {}
     if "w8a16" in sweep:
@@ -773,6 +777,8 @@ def main():
         extra["prefill_pct_mfma_peak"]["w8a16_m2048"] = round(100.0 * tf / MFMA_PEAK_TFLOPS["bf16"], 1)
         tfu, _ = time_prefill(dq, torch, layers[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
         extra["prefill_tflops_ungrouped"]["w8a16_m2048"] = round(tfu, 1)
+        t256, _ = time_prefill(dq, torch, layers[0], 256, a.prefill_iters, dev, dq.PATH_GEMM, groups=LAYER_27B_GROUPS)
+        extra["sweep_27b"]["w8a16"].update({"prefill_tflops_m256": round(t256, 1), "prefill_tflops_m2048": round(tf, 1)})
         print(f"# w8a16 prefill M=2048: {tf:.1f} TFLOP/s ({s2 * 1e3:.2f} ms/layer; {tfu:.1f} as seven forwards)",
               file=sys.stderr, flush=True)
     del layers
@@ -847,6 +853,15 @@ def main():
             extra["prefill_pct_mfma_peak"][name + "_m2048"] = round(100.0 * tf / MFMA_PEAK_TFLOPS["bf16"], 1)
             tfu, _ = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM)
             extra["prefill_tflops_ungrouped"][name + "_m2048"] = round(tfu, 1)
+            if fmt == dq.Q4_K:  # the 27B sweep's other row counts: decode 8, prefill 256
+                s8q = time_decode(dq, torch, ls, max(a.steps // 3, 10), 10, dev, groups=LAYER_27B_GROUPS, rows=8)
+                t256q, _ = time_prefill(dq, torch, ls[0], 256, a.prefill_iters, dev, dq.PATH_GEMM,
+                                        groups=LAYER_27B_GROUPS)
+                extra["sweep_27b"]["q4_k"] = {"decode_gbs_m1": round(gbs, 1),
+                                              "decode_gbs_m8": round(layer_bytes(dq, fmt) * max(a.steps // 3, 10)
+                                                                     / s8q / 1e9, 1),
+                                              "prefill_tflops_m256": round(t256q, 1),
+                                              "prefill_tflops_m2048": round(tf, 1)}
             if fmt == dq.Q4_K:  # the GGUF worker's f16 activations
                 tfh, _ = time_prefill(dq, torch, ls[0], 2048, a.prefill_iters, dev, dq.PATH_GEMM, act="float16",
                                       groups=LAYER_27B_GROUPS)
