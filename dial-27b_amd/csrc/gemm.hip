@@ -1282,8 +1282,15 @@ static int64_t gemm32_col_tiles(const WeightView &w) { return w.pair ? (w.pair +
 // bytes allowed for a tail split's partials.
 static Gemm32Plan gemm32_plan(int64_t M, const WeightView &w, int64_t nt, size_t budget) {
   Gemm32Plan g;
-  const bool small = M <= kGemm32SmallRows;
+  // Launches of very few 128-row tiles (the 27B k / v at 256-512 rows: 8-16
+  // tiles) take the small-row plan too -- 32-row tiles split along K -- so
+  // that more than a handful of CUs work: W8A16 k / v at M = 256 23.7 ->
+  // 19 us, the W8A16 layer at M = 512 597 -> 670 TFLOP/s (down 200 -> 152
+  // us), Q4_K k / v at M = 256 59 -> 33 us.  The GGUF kernel dequantizes its
+  // weight tile once per 32 rows there, so it takes this plan only below
+  // CUs / 8 tiles (at 40-96 tiles its M = 512 layer lost 29 %).
   const bool kq = w.fmt == DIALQ_FORMAT_Q4_K || w.fmt == DIALQ_FORMAT_Q8_0 || w.fmt == DIALQ_FORMAT_Q6_K;
+  const bool small = M <= kGemm32SmallRows || nt * ((M + 127) / 128) * (kq ? 8 : 2) < device_cus();
   g.mt = small ? 1 : kq ? GEMMKQ_MT : M >= kGemm32TallRows ? 4 : GEMM32_MT;
   // 128-row tiles that fill less than one round of their slots but too many
   // to split along K (the 27B o and down projections at 2048 rows: 320
