@@ -691,7 +691,7 @@ def time_dense_library(torch, dev, reps=20):
 def main():
     a = parse()
     if a.gpus != 1:
-        print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported (this build "
+        print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported (the library "
               "has no multi-GPU path)", file=sys.stderr)
         sys.exit(2)
     import torch
