@@ -73,10 +73,14 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 typedef __attribute__((address_space(3))) float lds_f32;
 
+// Zero block after the staged rows: lanes that feed zeros read it at the
+// same offsets (up to 7 x 64 + 16 bytes) as a staged row of one chunk.
+constexpr int kXZeroBytes = 512;
+
 struct Ctx {
   rsrc_t rt, ra, rx;
   const lds_u8 *xl;    // staged rows (XL)
-  const lds_u8 *zero;  // 32 zero bytes (XL)
+  const lds_u8 *zero;  // kXZeroBytes zero bytes (XL)
   const lds_f32 *xs;   // [mrows][nsub] activation sums per scale sub-block (policies with XS)
   int nsub;            // sub-blocks per row in xs
   int pitch;           // bytes per staged row
@@ -279,7 +283,7 @@ struct Q4kRowsPolicy {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           const u32x4 wb = nib8_off<F16>(qd[2 * (t >> 1)], qd[2 * (t >> 1) + 1], (t & 1) ? 4 : 0);
-          const lds_u8 *src = (jj == (t & 3) && row < cx.mrows) ? rowp + 64 * t : cx.zero;
+          const lds_u8 *src = ((jj == (t & 3) && row < cx.mrows) ? rowp : cx.zero) + 64 * t;
           XOp<ACT> av;
           av.hi = *(const u32x4 __attribute__((address_space(3))) *)src;
           cq[t >> 2] = mfma_x<ACT>(av, wb, cq[t >> 2]);
@@ -416,7 +420,7 @@ struct Q6kRowsPolicy {
           if constexpr (XL && ONEPART) {
             // one-part operands straight from the staged rows; lanes that
             // feed zeros (or rows past the last) read the zero block
-            const lds_u8 *p = (on && row < cx.mrows) ? rowp + 64 * (2 * u + v) : cx.zero;
+            const lds_u8 *p = ((on && row < cx.mrows) ? rowp : cx.zero) + 64 * (2 * u + v);
             av.hi = *(const u32x4 __attribute__((address_space(3))) *)p;
           } else {
             av.hi = on ? src.hi : z4;
@@ -527,9 +531,9 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
   // LDS: [staged x][32 zero bytes][activation sums (XSUB)][parked accumulators]
   constexpr bool XSUMS = XL && Pol::XSUB > 0;
   cx.nsub = XSUMS ? (int)(w.k_chunks * FmtTraits<FMT>::CHUNK / (XSUMS ? Pol::XSUB : 1)) : 0;
-  lds_f32 *xsums = (lds_f32 *)(smem + (XL ? mrows * p.x_pitch + 32 : 0));
+  lds_f32 *xsums = (lds_f32 *)(smem + (XL ? mrows * p.x_pitch + kXZeroBytes : 0));
   cx.xs = xsums;
-  float *part = (float *)(smem + (XL ? mrows * p.x_pitch + 32 : 0) + (size_t)mrows * cx.nsub * 4);
+  float *part = (float *)(smem + (XL ? mrows * p.x_pitch + kXZeroBytes : 0) + (size_t)mrows * cx.nsub * 4);
   cx.rt = make_rsrc(w.tiles, (uint32_t)(total * 64 * FmtTraits<FMT>::LANE));
   cx.ra = cx.rt;
   if constexpr (FMT == DIALQ_FORMAT_Q8_0 || FMT == DIALQ_FORMAT_MXFP4)
@@ -555,7 +559,8 @@ __global__ __launch_bounds__(64 * WV) void k_gemv(GemvParams p) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(cx.rx, (__attribute__((address_space(3))) void *)(smem + m * p.x_pitch + kb),
                                                 16, col < row_bytes ? m * row_bytes + col : (int)kOOB, 0, 0, 0);
     }
-    if (threadIdx.x < 2) *(u32x4 __attribute__((address_space(3))) *)(smem + mrows * p.x_pitch + 16 * threadIdx.x) = (u32x4){0, 0, 0, 0};
+    if (threadIdx.x < kXZeroBytes / 16)
+      *(u32x4 __attribute__((address_space(3))) *)(smem + mrows * p.x_pitch + 16 * threadIdx.x) = (u32x4){0, 0, 0, 0};
   }
   // each wave clears its own parking slots (a wave may skip a strip)
   for (int j = 0; j < nseg; ++j)
@@ -940,7 +945,7 @@ __global__ __launch_bounds__(64 * (kDynWaves + 1)) void k_gemv_dyn(DynParams p) 
   int *ng = q + QD;           // ordinals queued so far
   int *done = q + QD + 1;     // [QD] waves finished with the unit in each slot
   uint8_t *xbase = smem + kDynCtlBytes;
-  float *park = (float *)(xbase + (XL ? mrows * p.x_pitch + 32 : 0));
+  float *park = (float *)(xbase + (XL ? mrows * p.x_pitch + kXZeroBytes : 0));
 
   Ctx cx;
   cx.mrows = mrows;
@@ -985,7 +990,8 @@ __global__ __launch_bounds__(64 * (kDynWaves + 1)) void k_gemv_dyn(DynParams p) 
                                                   16, col < row_bytes ? m * row_bytes + col : (int)kOOB, 0, 0, 0);
       }
     }
-    if (threadIdx.x < 2) *(u32x4 __attribute__((address_space(3))) *)(xbase + mrows * p.x_pitch + 16 * threadIdx.x) = (u32x4){0, 0, 0, 0};
+    if (threadIdx.x < kXZeroBytes / 16)
+      *(u32x4 __attribute__((address_space(3))) *)(xbase + mrows * p.x_pitch + 16 * threadIdx.x) = (u32x4){0, 0, 0, 0};
   }
   __builtin_amdgcn_sched_barrier(0);
   lds_barrier();  // queue and counters initialised
@@ -1137,7 +1143,7 @@ static hipError_t launch_ranges(GemvParams &p, hipStream_t st) {
   const size_t xsums = (XL && Pol::XSUB > 0)
                            ? (size_t)mrows * (p.w.k_chunks * FmtTraits<FMT>::CHUNK / (Pol::XSUB > 0 ? Pol::XSUB : 1)) * 4
                            : 0;
-  const size_t lds = park + (XL ? (size_t)mrows * p.x_pitch + 32 : 0) + xsums;
+  const size_t lds = park + (XL ? (size_t)mrows * p.x_pitch + kXZeroBytes : 0) + xsums;
   k_gemv<FMT, Pol, U, XL, WV><<<(unsigned)p.G, 64 * WV, lds, st>>>(p);
   return hipGetLastError();
 }
@@ -1156,7 +1162,7 @@ static hipError_t launch_dyn(DynParams &p, int64_t mrows, hipStream_t st) {
     return hipSuccess;
   }
   if (need > p.ws_bytes) return hipErrorInvalidValue;
-  const size_t lds = kDynCtlBytes + (XL ? (size_t)mrows * p.x_pitch + 32 : 0) +
+  const size_t lds = kDynCtlBytes + (XL ? (size_t)mrows * p.x_pitch + kXZeroBytes : 0) +
                      (size_t)kDynQueue * kDynWaves * mrows * 16 * sizeof(float);
   k_gemv_dyn<FMT, Pol, U, XL><<<(unsigned)p.G, 64 * (kDynWaves + 1), lds, st>>>(p);
   return hipGetLastError();
@@ -1170,7 +1176,7 @@ static hipError_t launch_dyn(DynParams &p, int64_t mrows, hipStream_t st) {
 template <int FMT, int ACT, template <int, int, bool, bool> class PolT, int A, int U_XL, int U_X>
 static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
   constexpr int BY = ActTraits<ACT>::BYTES;
-  const bool xl = mrows * stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) + 32 <= kGemvStageBytes;
+  const bool xl = mrows * stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) + kXZeroBytes <= kGemvStageBytes;
   constexpr int UR = U_XL < kRangeRing ? U_XL : kRangeRing;
   if (d.group) {
     // Grouped launch: the strips of every member, whole strips with staged
@@ -1178,7 +1184,7 @@ static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
     // 8 below); other configurations run one launch per member.
     const int pitch = stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK);
     const int total = d.group->sbase[d.group->nm];
-    if (d.w.pair || mrows * pitch + 32 > (total >= device_cus() ? kGemvStageBytes : kGemvSmallStageBytes))
+    if (d.w.pair || mrows * pitch + kXZeroBytes > (total >= device_cus() ? kGemvStageBytes : kGemvSmallStageBytes))
       return hipErrorNotSupported;
     GemvParams p = *d.group;
     p.x = d.x;
@@ -1197,7 +1203,7 @@ static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
     // would, so the rounds of workgroups over the CUs match the plain launch
     GemvParams p{d.w, d.x, d.y, d.M, d.m_base, d.y_dtype, 1, 0, d.ws, d.ws_bytes, 0, d.cnt, d.query};
     const int pitch = stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK);
-    if (mrows * pitch + 32 <= kGemvSmallStageBytes) {
+    if (mrows * pitch + kXZeroBytes <= kGemvSmallStageBytes) {
       p.x_pitch = pitch;
       return launch_ranges<FMT, PolT<A, ACT, true, true>, UR, true, kGemvSmallWaves>(p, st);
     }
@@ -1211,7 +1217,7 @@ static hipError_t launch_pol(DynParams &d, int64_t mrows, hipStream_t st) {
     return launch_ranges<FMT, PolT<A, ACT, false, false>, (U_X < kRangeRing ? U_X : kRangeRing), false, kGemvWaves>(
         p, st);
   }
-  if (mrows * stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) + 32 <= kGemvSmallStageBytes) {
+  if (mrows * stage_pitch(d.w, BY, FmtTraits<FMT>::CHUNK) + kXZeroBytes <= kGemvSmallStageBytes) {
     // Fewer strips than CUs, activations staged: one strip per workgroup of
     // kGemvSmallWaves waves, so each wave streams a short run of tiles and
     // nothing is reduced across workgroups.  Measured at M = 1..4 with
