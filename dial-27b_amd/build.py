@@ -35,9 +35,17 @@ FLAGS = [
 ]
 
 
+# Per-source flags.  The decode GEMV's MFMAs write their accumulators to
+# ordinary VGPRs: each tile's partial sums are read by VALU code right after
+# the MFMAs, and the AGPR form added a v_accvgpr_read per value (8 per Q4_K
+# tile); same occupancy, no spills, 27B layer decode +1.1-2.0 % (W8A16,
+# FP8-128).  The prefill GEMMs keep the compiler's choice.
+SOURCE_FLAGS = {"gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile {src} failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
